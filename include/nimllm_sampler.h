@@ -1,0 +1,158 @@
+/*
+ * nimllm_sampler.h -- C ABI of the MI355X (gfx950) token sampler.
+ *
+ * A batched, device-resident replacement for nimllm's `Sampler`
+ * (src/nimllm/sampler.nim).  One handle holds B independent samplers ("rows"),
+ * each with its own SamplerParams, RNG stream and accepted-token history,
+ * exactly as B separate `newSampler` objects would.  Every call is ordered on
+ * the handle's HIP stream; only the *_host variants block.
+ *
+ * The pipeline per row is the reference's (sampler.nim:59-121): penalties ->
+ * logit bias -> temperature -> top-k -> softmax -> top-p -> min-p -> draw, and
+ * temperature <= 0 is greedy argmax with no RNG draw.  Sampled ids are
+ * bit-exact with the reference's fp32 semantics (sequential fp32 sums in
+ * candidate order, float64 top-p compare, Nim's heap tie order on the top-k
+ * path, stable descending order on the full-sort path).  exp(float32) is
+ * evaluated correctly rounded.
+ *
+ * No symbol here allocates on the caller's behalf except nls_create (and
+ * nls_accept* when a row's history window outgrows its ring).
+ */
+#ifndef NIMLLM_SAMPLER_H
+#define NIMLLM_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: every entry point returns one.  Nothing throws across the ABI. */
+enum {
+  NLS_OK = 0,
+  NLS_ERR_INVALID_ARGUMENT = 1, /* NULL handle/pointer, batch < 1, bad row, ... */
+  NLS_ERR_EMPTY_VOCAB = 2,      /* vocab == 0 (the reference raises IndexDefect, sampler.nim:121) */
+  NLS_ERR_HIP = 3,              /* a HIP runtime call failed (see nls_last_error) */
+  NLS_ERR_OUT_OF_MEMORY = 4,
+  NLS_ERR_NO_DEVICE = 5,        /* no usable gfx950 device */
+  NLS_ERR_UNSUPPORTED = 6       /* a size beyond what this build supports */
+};
+
+/*
+ * Mirror of SamplerParams (sampler.nim:11-21), field for field.  float64 and
+ * int64 fields are kept because the reference compares top-p in float64
+ * (sampler.nim:107) and forms the penalty in float64 (:74).  `logitBias`
+ * (Table[int, float]) becomes (ids, values, count); when an id repeats, the
+ * last value wins, as assigning into the table would.  Nim zero-initialises
+ * omitted fields: a zero repeat_penalty is *active* (rp != 1), exactly as in
+ * the reference -- start from nls_default_sampling() to avoid that.
+ */
+typedef struct nls_params {
+  double temperature;        /* <= 0: greedy argmax                       */
+  int64_t top_k;             /* 0: off                                    */
+  double top_p;              /* >= 1 or <= 0: off                         */
+  double min_p;              /* <= 0: off                                 */
+  double repeat_penalty;     /* 1.0: off                                  */
+  int64_t repeat_last_n;     /* <= 0: whole history                       */
+  double presence_penalty;
+  double frequency_penalty;
+  int64_t seed;              /* < 0: non-reproducible seed                */
+  const int64_t* logit_bias_ids;    /* may be NULL when count == 0        */
+  const double* logit_bias_values;  /* -INFINITY forbids a token          */
+  int64_t logit_bias_count;
+} nls_params;
+
+typedef struct nls_sampler nls_sampler; /* opaque */
+
+/* Optional per-call inspection output (all device pointers, may be NULL). */
+typedef struct nls_debug {
+  int32_t* n;            /* [B] candidates kept after top-p/min-p (0 for greedy rows)  */
+  int32_t* ncand;        /* [B] candidates before the cutoffs (k, or V on the sort path) */
+  int32_t* cand_ids;     /* [B x cap] candidate ids in reference order, first min(n, cap) */
+  float* cand_probs;     /* [B x cap] softmax probabilities of those candidates           */
+  float* total;          /* [B] fp32 sum of the first n probabilities                     */
+  int32_t* path;         /* [B] NLS_PATH_* taken by the row                                */
+  int32_t cap;
+} nls_debug;
+
+enum {
+  NLS_PATH_GREEDY = 1,     /* argmax                                          */
+  NLS_PATH_TOPK = 2,       /* chunked top-k candidates + exact merge          */
+  NLS_PATH_FULL = 3,       /* full-vocabulary (sort) path, fast prefix kernel */
+  NLS_PATH_GENERIC = 4     /* whole-row sort; rows the fast kernels hand off  */
+};
+
+/* Presets: defaultSampling (sampler.nim:28-31) and greedySampling (:33-35). */
+nls_params nls_default_sampling(void);
+nls_params nls_greedy_sampling(void);
+
+/*
+ * newSampler (sampler.nim:37-39), batched.  per_row[batch] gives each row's
+ * params (copied; bias arrays are read during the call only).  The RNG of
+ * row b is initRand(seed_b), or a time/entropy seed when seed_b < 0.
+ * `stream` is a hipStream_t (NULL = the default stream).
+ */
+int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* stream,
+               nls_sampler** out);
+int nls_destroy(nls_sampler* s);
+int nls_set_stream(nls_sampler* s, void* stream);
+int32_t nls_batch(const nls_sampler* s);
+int64_t nls_vocab(const nls_sampler* s);
+
+/*
+ * accept (sampler.nim:41-43), batched.  Appends `count` ids to every row's
+ * history: ids is host memory [batch x count], row-major.  Any int64 is
+ * accepted; ids outside [0, vocab) occupy a history slot and are skipped by
+ * the penalties, as in the reference (:70).
+ */
+int nls_accept(nls_sampler* s, const int64_t* ids, int32_t count);
+/* accept for one row only. */
+int nls_accept_row(nls_sampler* s, int32_t row, const int64_t* ids, int32_t count);
+/* Appends one id per row straight from device memory (e.g. the previous
+ * nls_sample output), without a host round trip.  d_ids: device [batch]. */
+int nls_accept_device(nls_sampler* s, const int32_t* d_ids);
+/* Drops every row's history (a fresh newSampler keeps none). */
+int nls_clear_history(nls_sampler* s);
+
+/*
+ * sample (sampler.nim:59-121), batched and asynchronous.
+ *   d_logits  device [batch x vocab] fp32, row-major; read only, never modified
+ *   d_u       device [batch] float64 uniforms in [0,1) standing for each row's
+ *             rand(1.0) (:117); NULL draws from each row's own RNG, advancing
+ *             it only for rows with temperature > 0, as the reference does
+ *   d_out     device [batch] int32 sampled ids
+ *   dbg       optional inspection output (NULL for none)
+ */
+int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t* d_out,
+               const nls_debug* dbg);
+
+/* Blocking convenience for host-resident logits (a CPU model's output):
+ * copies h_logits [batch x vocab] to the device, samples with the rows' own
+ * RNGs and returns the ids in h_out [batch]. */
+int nls_sample_host(nls_sampler* s, const float* h_logits, int64_t* h_out);
+
+int nls_synchronize(nls_sampler* s);
+
+/* The first n values of rand(1.0) after initRand(seed) (Nim std/random). */
+int nls_rng_uniforms(int64_t seed, int64_t n, double* out);
+/* Reads back row `row`'s RNG state (two 64-bit words), e.g. to checkpoint. */
+int nls_get_rng_state(nls_sampler* s, int32_t row, uint64_t* a0, uint64_t* a1);
+int nls_set_rng_state(nls_sampler* s, int32_t row, uint64_t a0, uint64_t a1);
+
+/* Correctly rounded exp on fp32 inputs, on the device: d_out[i] = exp(d_in[i]). */
+int nls_expf_device(const float* d_in, float* d_out, int64_t n, void* stream);
+
+/* Measurement hook (no counterpart in the reference): when set, the next
+ * nls_sample records hipEvent_t `start` immediately before and `stop`
+ * immediately after its streaming kernel (the one full read of the logits), on
+ * the handle's stream, then clears the hook.  Pass NULLs to clear it. */
+int nls_profile_next(nls_sampler* s, void* start_event, void* stop_event);
+
+const char* nls_status_string(int status);
+/* Last HIP error text seen by this thread ("" if none). */
+const char* nls_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,341 @@
+"""MI355X token sampler -- Python host mirror of nimllm's `Sampler` over the C ABI.
+
+The compute lives in ``libnimllm_sampler.so`` (HIP kernels for gfx950, built from
+``csrc/`` by ``csrc/Makefile``); this module only marshals arguments through
+ctypes.  It mirrors src/nimllm/sampler.nim:
+
+* ``SamplerParams`` (:11-21), ``defaultSampling`` (:28-31), ``greedySampling`` (:33-35)
+* ``newSampler`` / ``Sampler.accept`` / ``Sampler.sample`` (:37-43, :59-121) for one
+  row, and ``BatchSampler`` for B independent rows on the device.
+
+There is no CPU fallback: without the built library or a GPU every entry
+point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libnimllm_sampler.so")
+
+NLS_OK = 0
+PATH_GREEDY, PATH_TOPK, PATH_FULL, PATH_GENERIC = 1, 2, 3, 4
+
+EXPORTED = (
+    "nls_default_sampling", "nls_greedy_sampling", "nls_create", "nls_destroy",
+    "nls_set_stream", "nls_batch", "nls_vocab", "nls_accept", "nls_accept_row",
+    "nls_accept_device", "nls_clear_history", "nls_sample", "nls_sample_host",
+    "nls_synchronize", "nls_rng_uniforms", "nls_get_rng_state", "nls_set_rng_state",
+    "nls_expf_device", "nls_profile_next", "nls_status_string", "nls_last_error",
+)
+
+
+class NlsParams(ctypes.Structure):
+    _fields_ = [
+        ("temperature", ctypes.c_double),
+        ("top_k", ctypes.c_int64),
+        ("top_p", ctypes.c_double),
+        ("min_p", ctypes.c_double),
+        ("repeat_penalty", ctypes.c_double),
+        ("repeat_last_n", ctypes.c_int64),
+        ("presence_penalty", ctypes.c_double),
+        ("frequency_penalty", ctypes.c_double),
+        ("seed", ctypes.c_int64),
+        ("logit_bias_ids", ctypes.POINTER(ctypes.c_int64)),
+        ("logit_bias_values", ctypes.POINTER(ctypes.c_double)),
+        ("logit_bias_count", ctypes.c_int64),
+    ]
+
+
+class NlsDebug(ctypes.Structure):
+    _fields_ = [
+        ("n", ctypes.c_void_p),
+        ("ncand", ctypes.c_void_p),
+        ("cand_ids", ctypes.c_void_p),
+        ("cand_probs", ctypes.c_void_p),
+        ("total", ctypes.c_void_p),
+        ("path", ctypes.c_void_p),
+        ("cap", ctypes.c_int32),
+    ]
+
+
+class SamplerError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    """Load the HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise SamplerError(f"{LIB_PATH} is missing: build it with `make -C {HERE}/csrc`")
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.POINTER
+        vp = ctypes.c_void_p
+        L.nls_default_sampling.restype = NlsParams
+        L.nls_greedy_sampling.restype = NlsParams
+        L.nls_create.argtypes = [P(NlsParams), ctypes.c_int32, ctypes.c_int64, vp, P(vp)]
+        L.nls_destroy.argtypes = [vp]
+        L.nls_set_stream.argtypes = [vp, vp]
+        L.nls_batch.argtypes = [vp]
+        L.nls_batch.restype = ctypes.c_int32
+        L.nls_vocab.argtypes = [vp]
+        L.nls_vocab.restype = ctypes.c_int64
+        L.nls_accept.argtypes = [vp, P(ctypes.c_int64), ctypes.c_int32]
+        L.nls_accept_row.argtypes = [vp, ctypes.c_int32, P(ctypes.c_int64), ctypes.c_int32]
+        L.nls_accept_device.argtypes = [vp, vp]
+        L.nls_clear_history.argtypes = [vp]
+        L.nls_sample.argtypes = [vp, vp, vp, vp, P(NlsDebug)]
+        L.nls_sample_host.argtypes = [vp, P(ctypes.c_float), P(ctypes.c_int64)]
+        L.nls_synchronize.argtypes = [vp]
+        L.nls_rng_uniforms.argtypes = [ctypes.c_int64, ctypes.c_int64, P(ctypes.c_double)]
+        L.nls_get_rng_state.argtypes = [vp, ctypes.c_int32, P(ctypes.c_uint64), P(ctypes.c_uint64)]
+        L.nls_set_rng_state.argtypes = [vp, ctypes.c_int32, ctypes.c_uint64, ctypes.c_uint64]
+        L.nls_expf_device.argtypes = [vp, vp, ctypes.c_int64, vp]
+        L.nls_profile_next.argtypes = [vp, vp, vp]
+        L.nls_status_string.argtypes = [ctypes.c_int]
+        L.nls_status_string.restype = ctypes.c_char_p
+        L.nls_last_error.restype = ctypes.c_char_p
+        _lib = L
+    return _lib
+
+
+def check(status: int, what: str = "") -> None:
+    if status != NLS_OK:
+        L = lib()
+        raise SamplerError(f"{what}: {L.nls_status_string(status).decode()} "
+                           f"({L.nls_last_error().decode()})")
+
+
+@dataclass
+class SamplerParams:
+    """SamplerParams (sampler.nim:11-21).  Omitted fields are zero, as in Nim."""
+
+    temperature: float = 0.0
+    topK: int = 0
+    topP: float = 0.0
+    minP: float = 0.0
+    repeatPenalty: float = 0.0
+    repeatLastN: int = 0
+    presencePenalty: float = 0.0
+    frequencyPenalty: float = 0.0
+    seed: int = 0
+    logitBias: dict = field(default_factory=dict)
+
+
+def defaultSampling() -> SamplerParams:
+    """sampler.nim:28-31"""
+    return SamplerParams(temperature=0.7, topK=40, topP=0.95, minP=0.05,
+                         repeatPenalty=1.1, repeatLastN=64, seed=-1)
+
+
+def greedySampling() -> SamplerParams:
+    """sampler.nim:33-35"""
+    return SamplerParams(temperature=0.0, topK=0, topP=1.0, repeatPenalty=1.0, seed=0)
+
+
+def _to_c(p: SamplerParams, keep: list) -> NlsParams:
+    c = NlsParams()
+    c.temperature = p.temperature
+    c.top_k = p.topK
+    c.top_p = p.topP
+    c.min_p = p.minP
+    c.repeat_penalty = p.repeatPenalty
+    c.repeat_last_n = p.repeatLastN
+    c.presence_penalty = p.presencePenalty
+    c.frequency_penalty = p.frequencyPenalty
+    c.seed = p.seed
+    n = len(p.logitBias)
+    if n:
+        ids = (ctypes.c_int64 * n)(*[int(k) for k in p.logitBias.keys()])
+        vals = (ctypes.c_double * n)(*[float(v) for v in p.logitBias.values()])
+        keep.extend([ids, vals])
+        c.logit_bias_ids = ids
+        c.logit_bias_values = vals
+    c.logit_bias_count = n
+    return c
+
+
+def rng_uniforms(seed: int, n: int):
+    """The first n values of rand(1.0) after initRand(seed) (Nim std/random)."""
+    arr = (ctypes.c_double * max(n, 1))()
+    check(lib().nls_rng_uniforms(seed, n, arr), "nls_rng_uniforms")
+    return [arr[i] for i in range(n)]
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+class BatchSampler:
+    """B independent samplers (one per row) on the current HIP device.
+
+    ``sample`` takes a device tensor of shape [B, V] (float32) and returns the
+    sampled ids as a device int32 tensor; it is asynchronous on ``stream``.
+    """
+
+    def __init__(self, params: Sequence[SamplerParams], vocab: int, stream=None):
+        import torch
+
+        self._torch = torch
+        L = lib()
+        keep: list = []
+        B = len(params)
+        arr = (NlsParams * B)(*[_to_c(p, keep) for p in params])
+        self._stream = stream
+        self.B, self.V = B, int(vocab)
+        h = ctypes.c_void_p()
+        check(L.nls_create(arr, B, int(vocab), self._stream_ptr(), ctypes.byref(h)), "nls_create")
+        self._h = h
+
+    def _stream_ptr(self):
+        s = self._stream
+        if s is None:
+            return None
+        return ctypes.c_void_p(s.cuda_stream if hasattr(s, "cuda_stream") else int(s))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().nls_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def accept(self, ids, row: Optional[int] = None):
+        """accept (sampler.nim:41-43): one id per row ([B]) or [B, n] ids; or
+        ids for a single `row`."""
+        import numpy as np
+
+        a = np.ascontiguousarray(np.asarray(ids, dtype=np.int64))
+        L = lib()
+        if row is not None:
+            a = a.reshape(-1)
+            check(L.nls_accept_row(self._h, int(row), a.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                   a.size), "nls_accept_row")
+            return
+        a = a.reshape(self.B, -1)
+        check(L.nls_accept(self._h, a.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), a.shape[1]),
+              "nls_accept")
+
+    def accept_device(self, d_ids):
+        assert d_ids.dtype == self._torch.int32 and d_ids.is_cuda and d_ids.numel() == self.B
+        check(lib().nls_accept_device(self._h, ctypes.c_void_p(d_ids.data_ptr())), "nls_accept_device")
+
+    def clear_history(self):
+        check(lib().nls_clear_history(self._h), "nls_clear_history")
+
+    def sample(self, logits, u=None, out=None, debug_cap: int = 0):
+        """sample (sampler.nim:59-121) for every row.  `u` (float64 [B], device)
+        stands for each row's rand(1.0); None draws from the rows' own RNGs.
+        With debug_cap > 0 returns (ids, debug dict of device tensors)."""
+        torch = self._torch
+        assert logits.is_cuda and logits.dtype == torch.float32 and logits.is_contiguous()
+        assert tuple(logits.shape) == (self.B, self.V), (logits.shape, self.B, self.V)
+        if u is not None:
+            assert u.is_cuda and u.dtype == torch.float64 and u.numel() == self.B and u.is_contiguous()
+        if out is None:
+            out = torch.empty(self.B, dtype=torch.int32, device=logits.device)
+        dbgp = None
+        dbg = None
+        if debug_cap > 0:
+            dev = logits.device
+            dbg = {
+                "n": torch.full((self.B,), -1, dtype=torch.int32, device=dev),
+                "ncand": torch.full((self.B,), -1, dtype=torch.int32, device=dev),
+                "cand_ids": torch.full((self.B, debug_cap), -1, dtype=torch.int32, device=dev),
+                "cand_probs": torch.zeros((self.B, debug_cap), dtype=torch.float32, device=dev),
+                "total": torch.zeros((self.B,), dtype=torch.float32, device=dev),
+                "path": torch.zeros((self.B,), dtype=torch.int32, device=dev),
+            }
+            dbgp = NlsDebug(dbg["n"].data_ptr(), dbg["ncand"].data_ptr(), dbg["cand_ids"].data_ptr(),
+                            dbg["cand_probs"].data_ptr(), dbg["total"].data_ptr(),
+                            dbg["path"].data_ptr(), debug_cap)
+        check(lib().nls_sample(self._h, ctypes.c_void_p(logits.data_ptr()),
+                               ctypes.c_void_p(_ptr(u)) if u is not None else None,
+                               ctypes.c_void_p(out.data_ptr()),
+                               ctypes.byref(dbgp) if dbgp is not None else None), "nls_sample")
+        return (out, dbg) if debug_cap > 0 else out
+
+    def sample_host(self, logits):
+        """Blocking: host [B, V] float32 logits -> host int64 [B] ids."""
+        import numpy as np
+
+        x = np.ascontiguousarray(np.asarray(logits, dtype=np.float32).reshape(self.B, self.V))
+        o = np.zeros(self.B, dtype=np.int64)
+        check(lib().nls_sample_host(self._h, x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                    o.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))), "nls_sample_host")
+        return o
+
+    def profile_next(self, start_event, stop_event):
+        """Time the next sample()'s streaming kernel with two torch.cuda.Events
+        (recorded on this sampler's stream)."""
+        check(lib().nls_profile_next(self._h, ctypes.c_void_p(start_event.cuda_event),
+                                     ctypes.c_void_p(stop_event.cuda_event)), "nls_profile_next")
+
+    def synchronize(self):
+        check(lib().nls_synchronize(self._h), "nls_synchronize")
+
+    def rng_state(self, row: int):
+        a0, a1 = ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().nls_get_rng_state(self._h, row, ctypes.byref(a0), ctypes.byref(a1)), "rng")
+        return a0.value, a1.value
+
+    def set_rng_state(self, row: int, a0: int, a1: int):
+        check(lib().nls_set_rng_state(self._h, row, a0, a1), "rng")
+
+
+class Sampler:
+    """One nimllm Sampler (sampler.nim:23-26) backed by a one-row BatchSampler.
+
+    ``sample(logits)`` accepts a host sequence/ndarray (copied to the device) or
+    a 1-D device tensor, and returns the id as a Python int.
+    """
+
+    def __init__(self, p: SamplerParams, vocab: int):
+        self.params = p
+        self._b = BatchSampler([p], vocab)
+
+    def accept(self, tok: int):
+        self._b.accept([int(tok)])
+
+    def sample(self, logitsIn) -> int:
+        torch = self._b._torch
+        if isinstance(logitsIn, torch.Tensor) and logitsIn.is_cuda:
+            out = self._b.sample(logitsIn.reshape(1, -1).contiguous().float())
+            return int(out.cpu()[0])
+        return int(self._b.sample_host(logitsIn)[0])
+
+
+def newSampler(p: Optional[SamplerParams] = None, vocab: int = 0) -> Sampler:
+    """newSampler (sampler.nim:37-39).  The vocabulary size is fixed per sampler
+    here because the device buffers are sized from it."""
+    if vocab <= 0:
+        raise SamplerError("newSampler needs the vocabulary size")
+    return Sampler(p if p is not None else defaultSampling(), vocab)
+
+
+def expf_device(x, out=None):
+    """Correctly rounded exp of a float32 device tensor."""
+    import torch
+
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    check(lib().nls_expf_device(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                x.numel(), None), "nls_expf_device")
+    return out
+
+
+def inf_bias() -> float:
+    return -math.inf

@@ -1,0 +1,597 @@
+// nls_api.cpp -- host side of the C ABI in include/nimllm_sampler.h.
+//
+// Owns the per-handle device state (row parameters, bias tables, history
+// rings, RNG states, scratch) and orders every launch on the handle's stream.
+// Mirrors src/nimllm/sampler.nim: newSampler (:37-39), accept (:41-43),
+// sample (:59-121), the presets (:28-35) and std/random's initRand.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <new>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../include/nimllm_sampler.h"
+#include "nls_internal.h"
+
+using namespace nls;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int hip_fail(hipError_t e, const char* what) {
+  g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+  return e == hipErrorOutOfMemory ? NLS_ERR_OUT_OF_MEMORY : NLS_ERR_HIP;
+}
+
+#define NLS_HIP(call)                                   \
+  do {                                                  \
+    hipError_t e_ = (call);                             \
+    if (e_ != hipSuccess) return hip_fail(e_, #call);   \
+  } while (0)
+
+// Nim std/random: initRand(seed) -- seed 0 -> int32.high, a0 = seed shr 16,
+// a1 = seed and 0xffff, jump (skipRandomNumbers), then one discarded `next`.
+struct NimRand {
+  uint64_t a0, a1;
+};
+inline uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+uint64_t nim_next(NimRand& r) {
+  const uint64_t s0 = r.a0;
+  uint64_t s1 = r.a1;
+  const uint64_t res = s0 + s1;
+  s1 ^= s0;
+  r.a0 = rotl(s0, 55) ^ s1 ^ (s1 << 14);
+  r.a1 = rotl(s1, 36);
+  return res;
+}
+NimRand nim_init_rand(int64_t seed) {
+  const int64_t s = seed != 0 ? seed : 2147483647LL;
+  NimRand r{(uint64_t)(s >> 16), (uint64_t)(s & 0xffff)};
+  const uint64_t jump[2] = {0xbeac0467eba5facbULL, 0xd86b048b86aa9922ULL};
+  uint64_t j0 = 0, j1 = 0;
+  for (uint64_t w : jump)
+    for (int b = 0; b < 64; ++b) {
+      if (w & (1ULL << b)) {
+        j0 ^= r.a0;
+        j1 ^= r.a1;
+      }
+      (void)nim_next(r);
+    }
+  r.a0 = j0;
+  r.a1 = j1;
+  (void)nim_next(r);
+  return r;
+}
+double nim_rand_unit(NimRand& r) {
+  const uint64_t x = nim_next(r);
+  const uint64_t bits = (0x3FFULL << 52) | (x >> 12);
+  double f;
+  std::memcpy(&f, &bits, sizeof f);
+  return f - 1.0;
+}
+
+template <typename T>
+int dalloc(T** p, size_t n) {
+  *p = nullptr;
+  if (n == 0) return NLS_OK;
+  NLS_HIP(hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T)));
+  return NLS_OK;
+}
+template <typename T>
+void dfree(T*& p) {
+  if (p) (void)hipFree(p);
+  p = nullptr;
+}
+
+}  // namespace
+
+struct nls_sampler {
+  int B = 0;
+  int64_t V = 0;
+  hipStream_t stream = nullptr;
+  int nchunks = 0;
+  int qmax = 0;
+  int ccap = 0;
+  int mcap = 0;
+  size_t merge_lds = 0;
+  int max_bias = 0;
+
+  std::vector<RowParams> h_rp;
+  std::vector<int64_t> h_len;     // accepted ids per row
+  std::vector<int> need_window;   // repeat_last_n (>0) or -1 (whole history), 0 if unused
+  int hcap = 0;
+  int pcap = 0;
+
+  RowParams* rp = nullptr;
+  int32_t* bias_ids = nullptr;
+  float* bias_vals = nullptr;
+  int32_t* hist = nullptr;
+  int64_t* hist_len = nullptr;
+  Patch* patches = nullptr;
+  int32_t* patch_cnt = nullptr;
+  uint64_t* prep_scratch = nullptr;
+  int64_t prep_stride = 0;
+  ChunkStat* stats = nullptr;
+  uint64_t* cand = nullptr;
+  uint64_t* rng = nullptr;
+  float* row_max = nullptr;
+  int32_t* generic_list = nullptr;
+  int32_t* generic_count = nullptr;
+  uint32_t* gen_scratch = nullptr;
+  int64_t gen_vpad = 0;
+  int gen_blocks = 0;
+  int32_t* stage_ids = nullptr;
+  size_t stage_cap = 0;
+  std::vector<int32_t> h_stage;
+  float* tmp_logits = nullptr;
+  int32_t* tmp_out = nullptr;
+  hipEvent_t prof_start = nullptr;
+  hipEvent_t prof_stop = nullptr;
+
+  ~nls_sampler() {
+    dfree(rp);
+    dfree(bias_ids);
+    dfree(bias_vals);
+    dfree(hist);
+    dfree(hist_len);
+    dfree(patches);
+    dfree(patch_cnt);
+    dfree(prep_scratch);
+    dfree(stats);
+    dfree(cand);
+    dfree(rng);
+    dfree(row_max);
+    dfree(generic_list);
+    dfree(generic_count);
+    dfree(gen_scratch);
+    dfree(stage_ids);
+    dfree(tmp_logits);
+    dfree(tmp_out);
+  }
+
+  // Grows the history ring (and the patch / prep buffers sized from it) so
+  // that every row's window fits after `extra` more ids are appended to row
+  // `row` (every row when row < 0).  Re-lays the ring out on the host.
+  int ensure_history(int row, int64_t extra) {
+    int64_t need = 0;
+    for (int b = 0; b < B; ++b) {
+      if (need_window[b] == 0) continue;
+      const int64_t len = h_len[b] + ((row < 0 || row == b) ? extra : 0);
+      const int64_t w = need_window[b] > 0 ? std::min<int64_t>(need_window[b], len) : len;
+      need = std::max(need, w);
+    }
+    if (need <= hcap && hist) return NLS_OK;
+    int64_t ncap = std::max<int64_t>(hcap, 16);
+    while (ncap < need) ncap *= 2;
+    if (ncap > (1 << 24)) {
+      g_last_error = "history window beyond 2^24 ids";
+      return NLS_ERR_UNSUPPORTED;
+    }
+    int32_t* nh = nullptr;
+    int rc = dalloc(&nh, (size_t)B * ncap);
+    if (rc) return rc;
+    if (hist) {
+      std::vector<int32_t> old((size_t)B * hcap), neu((size_t)B * ncap, -1);
+      NLS_HIP(hipMemcpyAsync(old.data(), hist, old.size() * 4, hipMemcpyDeviceToHost, stream));
+      NLS_HIP(hipStreamSynchronize(stream));
+      for (int b = 0; b < B; ++b) {
+        const int64_t len = h_len[b];
+        const int64_t keep = std::min<int64_t>(len, hcap);
+        for (int64_t j = len - keep; j < len; ++j)
+          neu[(size_t)b * ncap + (size_t)(j % ncap)] = old[(size_t)b * hcap + (size_t)(j % hcap)];
+      }
+      NLS_HIP(hipMemcpyAsync(nh, neu.data(), neu.size() * 4, hipMemcpyHostToDevice, stream));
+      NLS_HIP(hipStreamSynchronize(stream));
+    }
+    dfree(hist);
+    hist = nh;
+    hcap = (int)ncap;
+    // patch list: distinct window ids + bias ids
+    dfree(patches);
+    pcap = hcap + max_bias;
+    rc = dalloc(&patches, (size_t)B * pcap);
+    if (rc) return rc;
+    dfree(prep_scratch);
+    prep_stride = 0;
+    int npow = 1;
+    while (npow < hcap + max_bias) npow <<= 1;
+    if (npow > kPrepSortLds) {
+      prep_stride = npow;
+      rc = dalloc(&prep_scratch, (size_t)B * npow);
+      if (rc) return rc;
+    }
+    return NLS_OK;
+  }
+};
+
+extern "C" {
+
+nls_params nls_default_sampling(void) {
+  nls_params p;
+  std::memset(&p, 0, sizeof p);
+  p.temperature = 0.7;
+  p.top_k = 40;
+  p.top_p = 0.95;
+  p.min_p = 0.05;
+  p.repeat_penalty = 1.1;
+  p.repeat_last_n = 64;
+  p.seed = -1;
+  return p;
+}
+
+nls_params nls_greedy_sampling(void) {
+  nls_params p;
+  std::memset(&p, 0, sizeof p);
+  p.temperature = 0.0;
+  p.top_k = 0;
+  p.top_p = 1.0;
+  p.repeat_penalty = 1.0;
+  p.seed = 0;
+  return p;
+}
+
+const char* nls_status_string(int status) {
+  switch (status) {
+    case NLS_OK: return "ok";
+    case NLS_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case NLS_ERR_EMPTY_VOCAB: return "empty vocabulary";
+    case NLS_ERR_HIP: return "HIP runtime error";
+    case NLS_ERR_OUT_OF_MEMORY: return "out of device memory";
+    case NLS_ERR_NO_DEVICE: return "no usable device";
+    case NLS_ERR_UNSUPPORTED: return "unsupported size";
+    default: return "unknown status";
+  }
+}
+
+const char* nls_last_error(void) { return g_last_error.c_str(); }
+
+int nls_rng_uniforms(int64_t seed, int64_t n, double* out) {
+  if (n < 0 || (n > 0 && !out)) return NLS_ERR_INVALID_ARGUMENT;
+  NimRand r = nim_init_rand(seed);
+  for (int64_t i = 0; i < n; ++i) out[i] = nim_rand_unit(r);
+  return NLS_OK;
+}
+
+int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* stream,
+               nls_sampler** out) {
+  if (!out) return NLS_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  if (!per_row || batch < 1) return NLS_ERR_INVALID_ARGUMENT;
+  if (vocab <= 0) return NLS_ERR_EMPTY_VOCAB;
+  if (vocab > (int64_t)kMaxChunks * kChunkElems || vocab >= (1LL << 31)) {
+    g_last_error = "vocab beyond 64 x 16384";
+    return NLS_ERR_UNSUPPORTED;
+  }
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) {
+    g_last_error = "no HIP device";
+    return NLS_ERR_NO_DEVICE;
+  }
+  nls_sampler* s = new (std::nothrow) nls_sampler();
+  if (!s) return NLS_ERR_OUT_OF_MEMORY;
+  s->B = batch;
+  s->V = vocab;
+  s->stream = reinterpret_cast<hipStream_t>(stream);
+  s->nchunks = (int)((vocab + kChunkElems - 1) / kChunkElems);
+  const int B = batch;
+  const int V = (int)vocab;
+  s->h_rp.resize(B);
+  s->h_len.assign(B, 0);
+  s->need_window.assign(B, 0);
+
+  // bias tables: per row, in-range ids, last value wins, sorted by id
+  std::vector<int32_t> bid;
+  std::vector<float> bval;
+  std::vector<NimRand> rng_h(B);
+  std::random_device rd;
+  int kmax = 0;
+  for (int b = 0; b < B; ++b) {
+    const nls_params& p = per_row[b];
+    if (p.logit_bias_count < 0 || (p.logit_bias_count > 0 &&
+                                   (!p.logit_bias_ids || !p.logit_bias_values))) {
+      delete s;
+      return NLS_ERR_INVALID_ARGUMENT;
+    }
+    std::map<int64_t, double> table;
+    for (int64_t j = 0; j < p.logit_bias_count; ++j) table[p.logit_bias_ids[j]] = p.logit_bias_values[j];
+    RowParams& r = s->h_rp[b];
+    std::memset(&r, 0, sizeof r);
+    r.bias_off = (int32_t)bid.size();
+    for (const auto& kv : table) {
+      if (kv.first < 0 || kv.first >= vocab) continue;  // sampler.nim:76
+      bid.push_back((int32_t)kv.first);
+      bval.push_back((float)kv.second);
+    }
+    r.bias_cnt = (int32_t)bid.size() - r.bias_off;
+    s->max_bias = std::max(s->max_bias, (int)r.bias_cnt);
+    r.rp32 = (float)p.repeat_penalty;
+    r.minP32 = (float)p.min_p;
+    r.pen_active = (p.repeat_penalty != 1.0 || p.presence_penalty != 0 || p.frequency_penalty != 0);
+    r.rp_active = p.repeat_penalty != 1.0;
+    r.topp_active = (p.top_p > 0 && p.top_p < 1);
+    r.minp_active = p.min_p > 0;
+    r.topP = p.top_p;
+    r.freq = p.frequency_penalty;
+    r.pres = p.presence_penalty;
+    r.repeat_last_n = p.repeat_last_n;
+    if (p.temperature <= 0) {
+      r.mode = kModeGreedy;
+      r.invT = 1.0f;
+      r.k = V;
+    } else {
+      r.invT = (float)(1.0 / p.temperature);
+      const int64_t k = p.top_k > 0 ? std::min<int64_t>(p.top_k, vocab) : vocab;
+      r.k = (int32_t)k;
+      r.mode = k < vocab ? kModeTopK : kModeFull;
+      if (r.mode == kModeTopK && k <= kMaxTopKFast) kmax = std::max(kmax, (int)k);
+    }
+    if (r.pen_active) s->need_window[b] = p.repeat_last_n > 0 ? (int)std::min<int64_t>(p.repeat_last_n, 1 << 24) : -1;
+    int64_t seed = p.seed;
+    if (seed < 0) {
+      const uint64_t t = (uint64_t)std::chrono::high_resolution_clock::now().time_since_epoch().count();
+      seed = (int64_t)((((uint64_t)rd() << 32) ^ rd() ^ t) & 0x7fffffffffffffffULL);
+    }
+    rng_h[b] = nim_init_rand(seed);
+  }
+  // fast top-k geometry: the largest k whose merge fits in LDS
+  const size_t lds_limit = 150 * 1024;
+  auto merge_bytes = [&](int k) {
+    const int cc = chunk_cap_for_k(k);
+    int mc = 1;
+    while (mc < 2 * k) mc <<= 1;
+    return (size_t)s->nchunks * cc * 8 + (size_t)mc * 20;
+  };
+  int kfast = kmax;
+  while (kfast > 0 && merge_bytes(kfast) > lds_limit) kfast = kfast * 7 / 8;
+  int qmax = 0;
+  for (int b = 0; b < B; ++b) {
+    RowParams& r = s->h_rp[b];
+    r.fast = (r.mode == kModeTopK && r.k <= kfast) ? 1 : 0;
+    if (r.fast) qmax = std::max(qmax, (r.k + kChunkThreads - 1) / kChunkThreads);
+  }
+  s->qmax = qmax;
+  if (kfast > 0) {
+    s->ccap = chunk_cap_for_k(kfast);
+    int mc = 1;
+    while (mc < 2 * kfast) mc <<= 1;
+    s->mcap = mc;
+    s->merge_lds = merge_bytes(kfast);
+  } else {
+    s->ccap = 1;
+    s->mcap = 1;
+    s->merge_lds = 64;
+  }
+
+  int rc = NLS_OK;
+  auto fail = [&](int code) {
+    delete s;
+    return code;
+  };
+  (void)set_kernel_attributes();
+  if ((rc = dalloc(&s->rp, B))) return fail(rc);
+  if ((rc = dalloc(&s->bias_ids, std::max<size_t>(bid.size(), 1)))) return fail(rc);
+  if ((rc = dalloc(&s->bias_vals, std::max<size_t>(bval.size(), 1)))) return fail(rc);
+  if ((rc = dalloc(&s->hist_len, B))) return fail(rc);
+  if ((rc = dalloc(&s->patch_cnt, B))) return fail(rc);
+  if ((rc = dalloc(&s->stats, (size_t)B * s->nchunks))) return fail(rc);
+  if ((rc = dalloc(&s->cand, (size_t)B * s->nchunks * s->ccap))) return fail(rc);
+  if ((rc = dalloc(&s->rng, (size_t)2 * B))) return fail(rc);
+  if ((rc = dalloc(&s->row_max, B))) return fail(rc);
+  if ((rc = dalloc(&s->generic_list, B))) return fail(rc);
+  if ((rc = dalloc(&s->generic_count, 1))) return fail(rc);
+  int64_t vpad = 1;
+  while (vpad < vocab) vpad <<= 1;
+  s->gen_vpad = vpad;
+  s->gen_blocks = std::min(B, 256);
+  if ((rc = dalloc(&s->gen_scratch, (size_t)s->gen_blocks * vpad * 5))) return fail(rc);
+  if ((rc = s->ensure_history(-1, 0))) return fail(rc);
+
+  hipStream_t st = s->stream;
+  auto up = [&](void* dst, const void* src, size_t bytes) {
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st);
+  };
+  hipError_t e;
+  if ((e = up(s->rp, s->h_rp.data(), sizeof(RowParams) * B)) != hipSuccess)
+    return fail(hip_fail(e, "upload params"));
+  if (!bid.empty()) {
+    if ((e = up(s->bias_ids, bid.data(), bid.size() * 4)) != hipSuccess)
+      return fail(hip_fail(e, "upload bias"));
+    if ((e = up(s->bias_vals, bval.data(), bval.size() * 4)) != hipSuccess)
+      return fail(hip_fail(e, "upload bias"));
+  }
+  if ((e = up(s->hist_len, s->h_len.data(), sizeof(int64_t) * B)) != hipSuccess)
+    return fail(hip_fail(e, "upload history"));
+  if ((e = up(s->rng, rng_h.data(), sizeof(NimRand) * B)) != hipSuccess)
+    return fail(hip_fail(e, "upload rng"));
+  if ((e = hipStreamSynchronize(st)) != hipSuccess) return fail(hip_fail(e, "sync"));
+  *out = s;
+  return NLS_OK;
+}
+
+int nls_destroy(nls_sampler* s) {
+  if (!s) return NLS_ERR_INVALID_ARGUMENT;
+  (void)hipStreamSynchronize(s->stream);
+  delete s;
+  return NLS_OK;
+}
+
+int nls_set_stream(nls_sampler* s, void* stream) {
+  if (!s) return NLS_ERR_INVALID_ARGUMENT;
+  s->stream = reinterpret_cast<hipStream_t>(stream);
+  return NLS_OK;
+}
+
+int32_t nls_batch(const nls_sampler* s) { return s ? s->B : 0; }
+int64_t nls_vocab(const nls_sampler* s) { return s ? s->V : 0; }
+
+static int accept_impl(nls_sampler* s, int row, const int64_t* ids, int32_t count) {
+  if (!s || count < 0 || (count > 0 && !ids)) return NLS_ERR_INVALID_ARGUMENT;
+  if (row >= s->B) return NLS_ERR_INVALID_ARGUMENT;
+  if (count == 0) return NLS_OK;
+  const int rows = row >= 0 ? 1 : s->B;
+  int rc = s->ensure_history(row, count);
+  if (rc) return rc;
+  const size_t n = (size_t)rows * count;
+  s->h_stage.resize(n);
+  for (size_t i = 0; i < n; ++i) {
+    const int64_t id = ids[i];
+    s->h_stage[i] = (id >= 0 && id < s->V) ? (int32_t)id : -1;  // out of range: skipped later
+  }
+  if (n > s->stage_cap) {
+    dfree(s->stage_ids);
+    rc = dalloc(&s->stage_ids, n);
+    if (rc) return rc;
+    s->stage_cap = n;
+  }
+  NLS_HIP(hipMemcpyAsync(s->stage_ids, s->h_stage.data(), n * 4, hipMemcpyHostToDevice, s->stream));
+  NLS_HIP(launch_accept_host(s->stage_ids, s->B, count, s->hist, s->hist_len, s->hcap, row,
+                             s->stream));
+  NLS_HIP(hipStreamSynchronize(s->stream));
+  if (row >= 0)
+    s->h_len[row] += count;
+  else
+    for (int b = 0; b < s->B; ++b) s->h_len[b] += count;
+  return NLS_OK;
+}
+
+int nls_accept(nls_sampler* s, const int64_t* ids, int32_t count) {
+  return accept_impl(s, -1, ids, count);
+}
+
+int nls_accept_row(nls_sampler* s, int32_t row, const int64_t* ids, int32_t count) {
+  if (row < 0) return NLS_ERR_INVALID_ARGUMENT;
+  return accept_impl(s, row, ids, count);
+}
+
+int nls_accept_device(nls_sampler* s, const int32_t* d_ids) {
+  if (!s || !d_ids) return NLS_ERR_INVALID_ARGUMENT;
+  int rc = s->ensure_history(-1, 1);
+  if (rc) return rc;
+  NLS_HIP(launch_accept_device(d_ids, s->B, s->V, s->hist, s->hist_len, s->hcap, s->stream));
+  for (int b = 0; b < s->B; ++b) s->h_len[b] += 1;
+  return NLS_OK;
+}
+
+int nls_clear_history(nls_sampler* s) {
+  if (!s) return NLS_ERR_INVALID_ARGUMENT;
+  std::fill(s->h_len.begin(), s->h_len.end(), 0);
+  NLS_HIP(hipMemcpyAsync(s->hist_len, s->h_len.data(), sizeof(int64_t) * s->B,
+                         hipMemcpyHostToDevice, s->stream));
+  NLS_HIP(hipStreamSynchronize(s->stream));
+  return NLS_OK;
+}
+
+int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t* d_out,
+               const nls_debug* dbg) {
+  if (!s || !d_logits || !d_out) return NLS_ERR_INVALID_ARGUMENT;
+  if (dbg && dbg->cap < 0) return NLS_ERR_INVALID_ARGUMENT;
+  LaunchArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.logits = d_logits;
+  a.V = s->V;
+  a.B = s->B;
+  a.nchunks = s->nchunks;
+  a.qmax = s->qmax;
+  a.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
+  a.rp = s->rp;
+  a.hist = s->hist;
+  a.hist_len = s->hist_len;
+  a.hcap = s->hcap;
+  a.bias_ids = s->bias_ids;
+  a.bias_vals = s->bias_vals;
+  a.patches = s->patches;
+  a.patch_cnt = s->patch_cnt;
+  a.pcap = s->pcap;
+  a.prep_scratch = s->prep_scratch;
+  a.prep_stride = s->prep_stride;
+  a.stats = s->stats;
+  a.cand = s->cand;
+  a.ccap = s->ccap;
+  a.mcap = s->mcap;
+  a.merge_lds = s->merge_lds;
+  a.d_u = d_u;
+  a.rng = s->rng;
+  a.out = d_out;
+  a.row_max = s->row_max;
+  a.generic_list = s->generic_list;
+  a.generic_count = s->generic_count;
+  a.gen_scratch = s->gen_scratch;
+  a.gen_vpad = s->gen_vpad;
+  a.gen_blocks = s->gen_blocks;
+  if (dbg) {
+    a.dbg.n = dbg->n;
+    a.dbg.ncand = dbg->ncand;
+    a.dbg.cand_ids = dbg->cand_ids;
+    a.dbg.cand_probs = dbg->cand_probs;
+    a.dbg.total = dbg->total;
+    a.dbg.path = dbg->path;
+    a.dbg.cap = dbg->cap;
+  }
+  a.ev_start = s->prof_start;
+  a.ev_stop = s->prof_stop;
+  s->prof_start = s->prof_stop = nullptr;
+  NLS_HIP(launch_sample(a, s->stream));
+  return NLS_OK;
+}
+
+int nls_profile_next(nls_sampler* s, void* start_event, void* stop_event) {
+  if (!s || (!start_event) != (!stop_event)) return NLS_ERR_INVALID_ARGUMENT;
+  s->prof_start = reinterpret_cast<hipEvent_t>(start_event);
+  s->prof_stop = reinterpret_cast<hipEvent_t>(stop_event);
+  return NLS_OK;
+}
+
+int nls_sample_host(nls_sampler* s, const float* h_logits, int64_t* h_out) {
+  if (!s || !h_logits || !h_out) return NLS_ERR_INVALID_ARGUMENT;
+  const size_t n = (size_t)s->B * s->V;
+  int rc;
+  if (!s->tmp_logits && (rc = dalloc(&s->tmp_logits, n))) return rc;
+  if (!s->tmp_out && (rc = dalloc(&s->tmp_out, (size_t)s->B))) return rc;
+  NLS_HIP(hipMemcpyAsync(s->tmp_logits, h_logits, n * 4, hipMemcpyHostToDevice, s->stream));
+  rc = nls_sample(s, s->tmp_logits, nullptr, s->tmp_out, nullptr);
+  if (rc) return rc;
+  std::vector<int32_t> o(s->B);
+  NLS_HIP(hipMemcpyAsync(o.data(), s->tmp_out, (size_t)s->B * 4, hipMemcpyDeviceToHost, s->stream));
+  NLS_HIP(hipStreamSynchronize(s->stream));
+  for (int b = 0; b < s->B; ++b) h_out[b] = o[b];
+  return NLS_OK;
+}
+
+int nls_synchronize(nls_sampler* s) {
+  if (!s) return NLS_ERR_INVALID_ARGUMENT;
+  NLS_HIP(hipStreamSynchronize(s->stream));
+  return NLS_OK;
+}
+
+int nls_get_rng_state(nls_sampler* s, int32_t row, uint64_t* a0, uint64_t* a1) {
+  if (!s || row < 0 || row >= s->B || !a0 || !a1) return NLS_ERR_INVALID_ARGUMENT;
+  uint64_t st[2];
+  NLS_HIP(hipMemcpyAsync(st, s->rng + 2 * row, 16, hipMemcpyDeviceToHost, s->stream));
+  NLS_HIP(hipStreamSynchronize(s->stream));
+  *a0 = st[0];
+  *a1 = st[1];
+  return NLS_OK;
+}
+
+int nls_set_rng_state(nls_sampler* s, int32_t row, uint64_t a0, uint64_t a1) {
+  if (!s || row < 0 || row >= s->B) return NLS_ERR_INVALID_ARGUMENT;
+  uint64_t st[2] = {a0, a1};
+  NLS_HIP(hipMemcpyAsync(s->rng + 2 * row, st, 16, hipMemcpyHostToDevice, s->stream));
+  NLS_HIP(hipStreamSynchronize(s->stream));
+  return NLS_OK;
+}
+
+int nls_expf_device(const float* d_in, float* d_out, int64_t n, void* stream) {
+  if (n < 0 || (n > 0 && (!d_in || !d_out))) return NLS_ERR_INVALID_ARGUMENT;
+  NLS_HIP(launch_expf(d_in, d_out, n, reinterpret_cast<hipStream_t>(stream)));
+  return NLS_OK;
+}
+
+}  // extern "C"

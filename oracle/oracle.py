@@ -1,0 +1,176 @@
+"""ctypes binding of the CPU restatement (liboracle) -- TEST INFRASTRUCTURE.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
+module.  It loads ``oracle/libnls_oracle.so`` (built by ``oracle/Makefile``) and
+exposes the restated sampler (src/nimllm/sampler.nim:59-121), argmax (:45-49),
+softmaxInPlace (:51-57), topTokens (:123-130) and Nim std/random.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libnls_oracle.so")
+
+EXPF_LIBM = 0
+EXPF_CR = 1
+
+
+class Params(ctypes.Structure):
+    _fields_ = [
+        ("temperature", ctypes.c_double),
+        ("topK", ctypes.c_int64),
+        ("topP", ctypes.c_double),
+        ("minP", ctypes.c_double),
+        ("repeatPenalty", ctypes.c_double),
+        ("repeatLastN", ctypes.c_int64),
+        ("presencePenalty", ctypes.c_double),
+        ("frequencyPenalty", ctypes.c_double),
+        ("seed", ctypes.c_int64),
+    ]
+
+
+class Rand(ctypes.Structure):
+    _fields_ = [("a0", ctypes.c_uint64), ("a1", ctypes.c_uint64)]
+
+
+class Result(ctypes.Structure):
+    _fields_ = [
+        ("id", ctypes.c_int64),
+        ("greedy", ctypes.c_int32),
+        ("heap", ctypes.c_int32),
+        ("ncand", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("pos", ctypes.c_int64),
+        ("sum", ctypes.c_float),
+        ("total", ctypes.c_float),
+        ("r0", ctypes.c_float),
+        ("thr", ctypes.c_float),
+        ("margin_draw", ctypes.c_double),
+        ("margin_topp", ctypes.c_double),
+        ("margin_minp", ctypes.c_double),
+    ]
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.POINTER
+        L.nlo_init_rand.argtypes = [P(Rand), ctypes.c_int64]
+        L.nlo_next.argtypes = [P(Rand)]
+        L.nlo_next.restype = ctypes.c_uint64
+        L.nlo_skip_random_numbers.argtypes = [P(Rand)]
+        L.nlo_rand_float.argtypes = [P(Rand), ctypes.c_double]
+        L.nlo_rand_float.restype = ctypes.c_double
+        L.nlo_uniforms.argtypes = [ctypes.c_int64, ctypes.c_int64, P(ctypes.c_double)]
+        L.nlo_expf_cr.argtypes = [ctypes.c_float]
+        L.nlo_expf_cr.restype = ctypes.c_float
+        L.nlo_expf.argtypes = [ctypes.c_float, ctypes.c_int]
+        L.nlo_expf.restype = ctypes.c_float
+        L.nlo_sample.argtypes = [
+            P(Params), P(ctypes.c_float), ctypes.c_int64,
+            P(ctypes.c_int64), ctypes.c_int64,
+            P(ctypes.c_int64), P(ctypes.c_double), ctypes.c_int64,
+            ctypes.c_double, ctypes.c_int, P(Result),
+            P(ctypes.c_int64), P(ctypes.c_float), P(ctypes.c_float),
+        ]
+        L.nlo_sample.restype = ctypes.c_int64
+        L.nlo_sample_batch.argtypes = [
+            P(Params), P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64,
+            P(ctypes.c_int64), ctypes.c_int64, P(ctypes.c_int64),
+            P(ctypes.c_int64), P(ctypes.c_double), ctypes.c_int64, P(ctypes.c_int64),
+            P(ctypes.c_double), ctypes.c_int, P(ctypes.c_int64), ctypes.c_int,
+        ]
+        L.nlo_argmax.argtypes = [P(ctypes.c_float), ctypes.c_int64]
+        L.nlo_argmax.restype = ctypes.c_int64
+        L.nlo_softmax_inplace.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int]
+        L.nlo_top_tokens.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64,
+                                     ctypes.c_int, P(ctypes.c_int64), P(ctypes.c_float)]
+        L.nlo_top_tokens.restype = ctypes.c_int64
+        _lib = L
+    return _lib
+
+
+def _ptr(a, ct):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctypes.POINTER(ct))
+
+
+def make_params(**kw) -> Params:
+    p = Params()
+    for name, _ in Params._fields_:
+        setattr(p, name, kw.get(name, 0))
+    return p
+
+
+def uniforms(seed: int, n: int) -> np.ndarray:
+    out = np.zeros(n, dtype=np.float64)
+    if n:
+        lib().nlo_uniforms(seed, n, _ptr(out, ctypes.c_double))
+    return out
+
+
+def sample(params: Params, logits, history=(), bias=None, u=0.5,
+           expf_mode=EXPF_LIBM, want_cand=True):
+    """Run one restated `sample` call.  Returns (Result, cand, probs, final_logits)."""
+    L = lib()
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    V = x.shape[0]
+    h = np.ascontiguousarray(history, dtype=np.int64)
+    bias = bias or {}
+    bid = np.array(list(bias.keys()), dtype=np.int64)
+    bval = np.array(list(bias.values()), dtype=np.float64)
+    res = Result()
+    cand = np.zeros(max(V, 1), dtype=np.int64) if want_cand else None
+    probs = np.zeros(max(V, 1), dtype=np.float32) if want_cand else None
+    fl = np.zeros(max(V, 1), dtype=np.float32) if want_cand else None
+    L.nlo_sample(ctypes.byref(params), _ptr(x, ctypes.c_float), V,
+                 _ptr(h, ctypes.c_int64) if h.size else None, h.size,
+                 _ptr(bid, ctypes.c_int64) if bid.size else None,
+                 _ptr(bval, ctypes.c_double) if bval.size else None, bid.size,
+                 float(u), expf_mode, ctypes.byref(res),
+                 _ptr(cand, ctypes.c_int64), _ptr(probs, ctypes.c_float), _ptr(fl, ctypes.c_float))
+    if want_cand:
+        nc = res.ncand
+        return res, cand[:nc].copy(), probs[:nc].copy(), fl[:V].copy()
+    return res, None, None, None
+
+
+def sample_batch(params_list, logits, hist=None, hlen=None, bias_ids=None, bias_vals=None,
+                 nb=None, u=None, expf_mode=EXPF_LIBM, nthreads=1) -> np.ndarray:
+    """Rows [B, V] through the restated sampler on `nthreads` threads."""
+    L = lib()
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    B, V = x.shape
+    parr = (Params * B)(*params_list)
+    H = 0 if hist is None else hist.shape[1]
+    NB = 0 if bias_ids is None else bias_ids.shape[1]
+    hist64 = None if hist is None else np.ascontiguousarray(hist, dtype=np.int64)
+    hlen64 = None if hlen is None else np.ascontiguousarray(hlen, dtype=np.int64)
+    bid = None if bias_ids is None else np.ascontiguousarray(bias_ids, dtype=np.int64)
+    bv = None if bias_vals is None else np.ascontiguousarray(bias_vals, dtype=np.float64)
+    nb64 = None if nb is None else np.ascontiguousarray(nb, dtype=np.int64)
+    uu = np.ascontiguousarray(u, dtype=np.float64)
+    out = np.zeros(B, dtype=np.int64)
+    L.nlo_sample_batch(parr, _ptr(x, ctypes.c_float), B, V,
+                       _ptr(hist64, ctypes.c_int64), H, _ptr(hlen64, ctypes.c_int64),
+                       _ptr(bid, ctypes.c_int64), _ptr(bv, ctypes.c_double), NB,
+                       _ptr(nb64, ctypes.c_int64), _ptr(uu, ctypes.c_double), expf_mode,
+                       _ptr(out, ctypes.c_int64), nthreads)
+    return out
