@@ -879,7 +879,10 @@ __global__ void accept_host_kernel(const int32_t* __restrict__ ids, int B, int c
   const int b = row_only >= 0 ? row_only : (int)blockIdx.x;
   const int64_t len = hist_len[b];
   const int32_t* src = ids + (row_only >= 0 ? 0 : (int64_t)b * count);
-  for (int j = threadIdx.x; j < count; j += blockDim.x)
+  // Only the last hcap ids survive in the ring; writing just those keeps
+  // every slot single-writer when count > hcap.
+  const int first = count > hcap ? count - hcap : 0;
+  for (int j = first + (int)threadIdx.x; j < count; j += blockDim.x)
     hist[(int64_t)b * hcap + (int)((len + j) % hcap)] = src[j];
   __syncthreads();
   if (threadIdx.x == 0) hist_len[b] = len + count;
