@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <new>
@@ -96,37 +97,32 @@ struct nls_sampler {
   int B = 0;
   int64_t V = 0;
   hipStream_t stream = nullptr;
-  int nchunks = 0;
-  int qmax = 0;
-  int ccap = 0;
-  int mcap = 0;
-  size_t merge_lds = 0;
   int max_bias = 0;
 
   std::vector<RowParams> h_rp;
   std::vector<int64_t> h_len;     // accepted ids per row
   std::vector<int> need_window;   // repeat_last_n (>0) or -1 (whole history), 0 if unused
   int hcap = 0;
-  int pcap = 0;
+
+  // streaming-kernel plan
+  LaunchPlan plan{};
+  int S = 1, L = 0, xcd_map = 0;
+  int ccap = 0, nwords = 0, pcap = 0, mcap = 0, kcap = 0, offA = 0, pc = 0;
+  int parity = 0;  // which generic counter this call uses
 
   RowParams* rp = nullptr;
   int32_t* bias_ids = nullptr;
   float* bias_vals = nullptr;
   int32_t* hist = nullptr;
   int64_t* hist_len = nullptr;
-  Patch* patches = nullptr;
-  int32_t* patch_cnt = nullptr;
-  uint64_t* prep_scratch = nullptr;
-  int64_t prep_stride = 0;
-  ChunkStat* stats = nullptr;
-  uint64_t* cand = nullptr;
+  uint64_t* part_cand = nullptr;
+  SliceInfo* part_info = nullptr;
+  uint32_t* arrive = nullptr;
   uint64_t* rng = nullptr;
-  float* row_max = nullptr;
   int32_t* generic_list = nullptr;
-  int32_t* generic_count = nullptr;
+  int32_t* generic_count = nullptr;  // [2]
   uint32_t* gen_scratch = nullptr;
   int64_t gen_vpad = 0;
-  int gen_blocks = 0;
   int32_t* stage_ids = nullptr;
   size_t stage_cap = 0;
   std::vector<int32_t> h_stage;
@@ -141,13 +137,10 @@ struct nls_sampler {
     dfree(bias_vals);
     dfree(hist);
     dfree(hist_len);
-    dfree(patches);
-    dfree(patch_cnt);
-    dfree(prep_scratch);
-    dfree(stats);
-    dfree(cand);
+    dfree(part_cand);
+    dfree(part_info);
+    dfree(arrive);
     dfree(rng);
-    dfree(row_max);
     dfree(generic_list);
     dfree(generic_count);
     dfree(gen_scratch);
@@ -156,9 +149,9 @@ struct nls_sampler {
     dfree(tmp_out);
   }
 
-  // Grows the history ring (and the patch / prep buffers sized from it) so
-  // that every row's window fits after `extra` more ids are appended to row
-  // `row` (every row when row < 0).  Re-lays the ring out on the host.
+  // Grows the history ring so that every row's window fits after `extra`
+  // more ids are appended to row `row` (every row when row < 0).  Re-lays the
+  // ring out on the host.
   int ensure_history(int row, int64_t extra) {
     int64_t need = 0;
     for (int b = 0; b < B; ++b) {
@@ -193,23 +186,74 @@ struct nls_sampler {
     dfree(hist);
     hist = nh;
     hcap = (int)ncap;
-    // patch list: distinct window ids + bias ids
-    dfree(patches);
-    pcap = hcap + max_bias;
-    rc = dalloc(&patches, (size_t)B * pcap);
-    if (rc) return rc;
-    dfree(prep_scratch);
-    prep_stride = 0;
-    int npow = 1;
-    while (npow < hcap + max_bias) npow <<= 1;
-    if (npow > kPrepSortLds) {
-      prep_stride = npow;
-      rc = dalloc(&prep_scratch, (size_t)B * npow);
-      if (rc) return rc;
-    }
     return NLS_OK;
   }
 };
+
+namespace {
+
+int next_pow2_i(int64_t n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  return (v && *v) ? std::atoi(v) : dflt;
+}
+
+// Streaming-kernel geometry for a batch: workgroup size, slices per row, LDS
+// layout, and the largest k the streaming kernel takes (larger k rows go to
+// the whole-row kernel).
+struct Geometry {
+  int nt, S, L, ccap, nwords, pcap, mcap, kcap, offA, pc, q;
+  bool wave;
+  size_t lds;
+};
+
+Geometry plan_geometry(int B, int64_t V, int kmax, int ncu) {
+  Geometry g{};
+  // 256-thread workgroups, >= 4 per CU: rows are split into S slices until the
+  // grid holds about 4 workgroups per CU, keeping >= 2 tiles per slice.
+  // a whole row per 1024-thread workgroup once the batch fills the chip;
+  // smaller batches split rows over 256-thread workgroups
+  g.nt = env_int("NLS_STREAM_NT", B >= ncu ? 1024 : 256) == 1024 ? 1024 : 256;
+  const int64_t te = (int64_t)g.nt * kStreamVec4 * 4;
+  const int want = g.nt == 1024 ? 1 : std::max(1, (4 * ncu + B - 1) / B);
+  g.S = std::max(1, env_int("NLS_STREAM_S", want));
+  g.S = (int)std::min<int64_t>({(int64_t)g.S, std::max<int64_t>(1, V / (2 * te)), (int64_t)kMaxSlices});
+  g.S = std::max(g.S, 1);
+  int64_t L = (V + g.S - 1) / g.S;
+  L = (L + 3) / 4 * 4;
+  g.S = (int)((V + L - 1) / L);
+  g.L = (int)L;
+  const int k = std::max(kmax, 1);
+  g.pc = g.S > 1 ? (2 * k + 64 + 7) / 8 * 8 : 0;
+  g.wave = kmax <= kWaveTopK;
+  g.ccap = next_pow2_i(std::max<int64_t>({1024, 4LL * k, ((int64_t)g.S * g.pc + 1) / 2}));
+  if (g.wave) g.ccap = std::max(g.ccap, g.nt / 64 * kWaveCap);  // one buffer region per wave
+  if (g.S > 1) g.pc = std::max(g.pc, (2 * g.ccap / g.S) / 8 * 8);
+  g.nwords = (int)((L + 31) / 32);
+  g.mcap = next_pow2_i(std::max(2 * k, 2));
+  g.kcap = k;
+  g.q = 1;
+  while (g.q < 8 && (int64_t)g.q * g.nt < 2LL * k) g.q <<= 1;
+  const size_t cand = (size_t)2 * g.ccap * 8;
+  const size_t head = (size_t)g.nwords * 4 + (((size_t)g.nwords * 2 + 3) & ~(size_t)3);
+  const size_t tail = (size_t)g.mcap * 8 + (size_t)g.kcap * 12;
+  g.offA = (int)cand;
+  // room for 4 workgroups per CU (160 KB of LDS), more when k or V need it
+  const size_t target = (size_t)(g.nt == 1024 ? 140 : 31) * 1024;
+  const size_t min_lds = cand + std::max(head + (size_t)256 * 16, tail);
+  const size_t lds = std::min(std::max(target, min_lds), nls::max_dynamic_lds());
+  g.pcap = 0;  // 16 bytes per patched id: final value, bias, flags, id
+  if (cand + head < lds) g.pcap = (int)std::min<size_t>(65535, (lds - cand - head) / 16);
+  g.lds = cand + std::max(head + (size_t)g.pcap * 16, tail);
+  return g;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -265,8 +309,8 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   *out = nullptr;
   if (!per_row || batch < 1) return NLS_ERR_INVALID_ARGUMENT;
   if (vocab <= 0) return NLS_ERR_EMPTY_VOCAB;
-  if (vocab > (int64_t)kMaxChunks * kChunkElems || vocab >= (1LL << 31)) {
-    g_last_error = "vocab beyond 64 x 16384";
+  if (vocab >= (1LL << 31) - 16) {
+    g_last_error = "vocab beyond 2^31";
     return NLS_ERR_UNSUPPORTED;
   }
   int ndev = 0;
@@ -279,7 +323,6 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   s->B = batch;
   s->V = vocab;
   s->stream = reinterpret_cast<hipStream_t>(stream);
-  s->nchunks = (int)((vocab + kChunkElems - 1) / kChunkElems);
   const int B = batch;
   const int V = (int)vocab;
   s->h_rp.resize(B);
@@ -340,57 +383,66 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
     }
     rng_h[b] = nim_init_rand(seed);
   }
-  // fast top-k geometry: the largest k whose merge fits in LDS
-  const size_t lds_limit = 150 * 1024;
-  auto merge_bytes = [&](int k) {
-    const int cc = chunk_cap_for_k(k);
-    int mc = 1;
-    while (mc < 2 * k) mc <<= 1;
-    return (size_t)s->nchunks * cc * 8 + (size_t)mc * 20;
-  };
+  // streaming geometry: the largest k whose buffers fit in LDS
+  int dev = 0, ncu = 0;
+  (void)hipGetDevice(&dev);
+  if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 1)
+    ncu = 256;
   int kfast = kmax;
-  while (kfast > 0 && merge_bytes(kfast) > lds_limit) kfast = kfast * 7 / 8;
-  int qmax = 0;
+  Geometry g = plan_geometry(B, vocab, kfast, ncu);
+  while (kfast > 0 && (g.lds > max_dynamic_lds() || g.pcap < 256)) {
+    kfast = kfast * 7 / 8;
+    g = plan_geometry(B, vocab, kfast, ncu);
+  }
+  const bool stream_ok = g.lds <= max_dynamic_lds() && g.pcap >= 1;  // false only for vocabularies far beyond 2^19
+  if (!stream_ok) g.lds = 0;                    // every row then goes to the whole-row kernel
+  bool any_full = false;
   for (int b = 0; b < B; ++b) {
     RowParams& r = s->h_rp[b];
-    r.fast = (r.mode == kModeTopK && r.k <= kfast) ? 1 : 0;
-    if (r.fast) qmax = std::max(qmax, (r.k + kChunkThreads - 1) / kChunkThreads);
+    r.fast = stream_ok && (r.mode == kModeGreedy || (r.mode == kModeTopK && r.k <= kfast)) ? 1 : 0;
+    any_full |= !r.fast;
   }
-  s->qmax = qmax;
-  if (kfast > 0) {
-    s->ccap = chunk_cap_for_k(kfast);
-    int mc = 1;
-    while (mc < 2 * kfast) mc <<= 1;
-    s->mcap = mc;
-    s->merge_lds = merge_bytes(kfast);
-  } else {
-    s->ccap = 1;
-    s->mcap = 1;
-    s->merge_lds = 64;
-  }
+  s->S = g.S;
+  s->L = g.L;
+  s->xcd_map = (g.S > 1 && B % 8 == 0) ? 1 : 0;
+  s->ccap = g.ccap;
+  s->nwords = g.nwords;
+  s->pcap = g.pcap;
+  s->mcap = g.mcap;
+  s->kcap = g.kcap;
+  s->offA = g.offA;
+  s->pc = g.pc;
+  s->plan.nt = g.nt;
+  s->plan.q = g.q;
+  s->plan.wave = g.wave;
+  s->plan.lds = g.lds;
+  s->plan.gen_blocks = any_full ? std::min(B, 256) : std::min(B, 8);
 
   int rc = NLS_OK;
   auto fail = [&](int code) {
     delete s;
     return code;
   };
-  (void)set_kernel_attributes();
+  {
+    const hipError_t e = set_kernel_attributes();
+    if (e != hipSuccess) return fail(hip_fail(e, "hipFuncSetAttribute"));
+  }
   if ((rc = dalloc(&s->rp, B))) return fail(rc);
   if ((rc = dalloc(&s->bias_ids, std::max<size_t>(bid.size(), 1)))) return fail(rc);
   if ((rc = dalloc(&s->bias_vals, std::max<size_t>(bval.size(), 1)))) return fail(rc);
   if ((rc = dalloc(&s->hist_len, B))) return fail(rc);
-  if ((rc = dalloc(&s->patch_cnt, B))) return fail(rc);
-  if ((rc = dalloc(&s->stats, (size_t)B * s->nchunks))) return fail(rc);
-  if ((rc = dalloc(&s->cand, (size_t)B * s->nchunks * s->ccap))) return fail(rc);
+  if (s->S > 1) {
+    if ((rc = dalloc(&s->part_cand, (size_t)B * s->S * s->pc))) return fail(rc);
+    if ((rc = dalloc(&s->part_info, (size_t)B * s->S))) return fail(rc);
+  }
+  if ((rc = dalloc(&s->arrive, B))) return fail(rc);
   if ((rc = dalloc(&s->rng, (size_t)2 * B))) return fail(rc);
-  if ((rc = dalloc(&s->row_max, B))) return fail(rc);
   if ((rc = dalloc(&s->generic_list, B))) return fail(rc);
-  if ((rc = dalloc(&s->generic_count, 1))) return fail(rc);
+  if ((rc = dalloc(&s->generic_count, 2))) return fail(rc);
   int64_t vpad = 1;
   while (vpad < vocab) vpad <<= 1;
   s->gen_vpad = vpad;
-  s->gen_blocks = std::min(B, 256);
-  if ((rc = dalloc(&s->gen_scratch, (size_t)s->gen_blocks * vpad * 5))) return fail(rc);
+  if ((rc = dalloc(&s->gen_scratch, (size_t)s->plan.gen_blocks * vpad * 5))) return fail(rc);
   if ((rc = s->ensure_history(-1, 0))) return fail(rc);
 
   hipStream_t st = s->stream;
@@ -410,6 +462,10 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
     return fail(hip_fail(e, "upload history"));
   if ((e = up(s->rng, rng_h.data(), sizeof(NimRand) * B)) != hipSuccess)
     return fail(hip_fail(e, "upload rng"));
+  if ((e = hipMemsetAsync(s->arrive, 0, sizeof(uint32_t) * B, st)) != hipSuccess)
+    return fail(hip_fail(e, "clear counters"));
+  if ((e = hipMemsetAsync(s->generic_count, 0, sizeof(int32_t) * 2, st)) != hipSuccess)
+    return fail(hip_fail(e, "clear counters"));
   if ((e = hipStreamSynchronize(st)) != hipSuccess) return fail(hip_fail(e, "sync"));
   *out = s;
   return NLS_OK;
@@ -492,52 +548,74 @@ int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t
                const nls_debug* dbg) {
   if (!s || !d_logits || !d_out) return NLS_ERR_INVALID_ARGUMENT;
   if (dbg && dbg->cap < 0) return NLS_ERR_INVALID_ARGUMENT;
-  LaunchArgs a;
+  DebugPtrs dp;
+  std::memset(&dp, 0, sizeof dp);
+  if (dbg) {
+    dp.n = dbg->n;
+    dp.ncand = dbg->ncand;
+    dp.cand_ids = dbg->cand_ids;
+    dp.cand_probs = dbg->cand_probs;
+    dp.total = dbg->total;
+    dp.path = dbg->path;
+    dp.cap = dbg->cap;
+  }
+  int32_t* cnt_now = s->generic_count + s->parity;
+  int32_t* cnt_next = s->generic_count + (s->parity ^ 1);
+  StreamArgs a;
   std::memset(&a, 0, sizeof a);
   a.logits = d_logits;
   a.V = s->V;
   a.B = s->B;
-  a.nchunks = s->nchunks;
-  a.qmax = s->qmax;
-  a.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
+  a.S = s->S;
+  a.L = s->L;
+  a.xcd_map = s->xcd_map;
   a.rp = s->rp;
   a.hist = s->hist;
   a.hist_len = s->hist_len;
   a.hcap = s->hcap;
   a.bias_ids = s->bias_ids;
   a.bias_vals = s->bias_vals;
-  a.patches = s->patches;
-  a.patch_cnt = s->patch_cnt;
-  a.pcap = s->pcap;
-  a.prep_scratch = s->prep_scratch;
-  a.prep_stride = s->prep_stride;
-  a.stats = s->stats;
-  a.cand = s->cand;
   a.ccap = s->ccap;
+  a.nwords = s->nwords;
+  a.pcap = s->pcap;
   a.mcap = s->mcap;
-  a.merge_lds = s->merge_lds;
+  a.kcap = s->kcap;
+  a.offA = s->offA;
+  a.part_cand = s->part_cand;
+  a.part_info = s->part_info;
+  a.arrive = s->arrive;
+  a.pc = s->pc;
   a.d_u = d_u;
   a.rng = s->rng;
   a.out = d_out;
-  a.row_max = s->row_max;
   a.generic_list = s->generic_list;
-  a.generic_count = s->generic_count;
-  a.gen_scratch = s->gen_scratch;
-  a.gen_vpad = s->gen_vpad;
-  a.gen_blocks = s->gen_blocks;
-  if (dbg) {
-    a.dbg.n = dbg->n;
-    a.dbg.ncand = dbg->ncand;
-    a.dbg.cand_ids = dbg->cand_ids;
-    a.dbg.cand_probs = dbg->cand_probs;
-    a.dbg.total = dbg->total;
-    a.dbg.path = dbg->path;
-    a.dbg.cap = dbg->cap;
-  }
-  a.ev_start = s->prof_start;
-  a.ev_stop = s->prof_stop;
+  a.generic_count = cnt_now;
+  a.dbg = dp;
+  GenericArgs ga;
+  std::memset(&ga, 0, sizeof ga);
+  ga.logits = d_logits;
+  ga.V = s->V;
+  ga.rp = s->rp;
+  ga.hist = s->hist;
+  ga.hist_len = s->hist_len;
+  ga.hcap = s->hcap;
+  ga.bias_ids = s->bias_ids;
+  ga.bias_vals = s->bias_vals;
+  ga.generic_list = s->generic_list;
+  ga.generic_count = cnt_now;
+  ga.next_count = cnt_next;
+  ga.scratch = s->gen_scratch;
+  ga.vpad = s->gen_vpad;
+  ga.d_u = d_u;
+  ga.rng = s->rng;
+  ga.out = d_out;
+  ga.dbg = dp;
+  LaunchPlan lp = s->plan;
+  lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
+  hipEvent_t e0 = s->prof_start, e1 = s->prof_stop;
   s->prof_start = s->prof_stop = nullptr;
-  NLS_HIP(launch_sample(a, s->stream));
+  NLS_HIP(launch_sample(a, ga, lp, s->stream, e0, e1));
+  s->parity ^= 1;
   return NLS_OK;
 }
 

@@ -28,42 +28,33 @@ struct RowParams {
   int32_t minp_active; // minP > 0 (:110)
   int32_t bias_off;    // into the per-handle bias arrays (sorted, unique, in range)
   int32_t bias_cnt;
-  int32_t fast;        // 1: top-k row handled by the chunk+merge kernels
+  int32_t fast;        // 1: greedy/top-k row handled by the streaming kernel
   double topP;         // compared in float64 (:107)
   double freq;         // frequencyPenalty
   double pres;         // presencePenalty
   int64_t repeat_last_n;
 };
 
-// One logit touched by penalties and/or bias; the per-row list is sorted by id.
-enum PatchFlags : int32_t { kPatchPen = 1, kPatchBias = 2 };
-struct Patch {
-  int32_t id;
-  int32_t flags;
-  float pen;   // float32(cnt * frequency + presence), formed in float64 (:74)
-  float bias;  // float32(logitBias[id]) (:76)
-};
+// Patch flags: which of penalty (:71-74) and bias (:76) touch a logit.
+enum PatchFlags : uint32_t { kPatchPen = 1u, kPatchBias = 2u };
 
-// Per (row, chunk) summary written by the streaming pass.
-enum ChunkFlags : int32_t { kChunkOverflow = 1 };
-struct ChunkStat {
-  float vmax;     // max of the chunk's final values (first index on ties)
-  int32_t amax;   // its index (global token id)
-  int32_t ncand;  // candidates written (top-k rows)
-  int32_t flags;
-};
-
-// Streaming-pass geometry.
-constexpr int kChunkThreads = 256;
-constexpr int kChunkVec4 = 16;  // float4 loads per thread
-constexpr int kChunkElems = kChunkThreads * kChunkVec4 * 4;  // 16384
-constexpr int kMaxChunks = 64;
+// Streaming-kernel geometry.
+constexpr int kStreamVec4 = 4;       // float4 loads per thread per tile
 constexpr int kMaxTopKFast = 2048;   // larger k goes to the whole-row kernel
-constexpr int kPrepSortLds = 4096;   // history+bias entries sorted in LDS
-constexpr int kMergeThreads = 256;
 constexpr int kGenericThreads = 1024;
+constexpr int kMaxSlices = 64;
+constexpr int kWaveCap = 256;        // per-wave candidate buffer of the k <= 64 path
+constexpr int kWaveTopK = 64;        // largest k of the wave path
 
-inline int chunk_cap_for_k(int k) { return k + k / 4 + 64; }
+// Slice-exchange record of one (row, slice) when a row is split over S
+// workgroups.
+enum SliceFlags : int32_t { kSliceOverflow = 1, kSliceNan0 = 2 /* element 0 of the row is NaN */ };
+struct SliceInfo {
+  int32_t n;      // candidates written
+  int32_t flags;  // SliceFlags
+  int32_t amax;   // first argmax of the slice's final values
+  int32_t vmax;   // its value (float bits)
+};
 
 struct DebugPtrs {
   int32_t* n;
@@ -75,49 +66,77 @@ struct DebugPtrs {
   int32_t cap;
 };
 
-struct LaunchArgs {
+struct StreamArgs {
   const float* logits;
   int64_t V;
   int B;
-  int nchunks;
-  int qmax;  // max top-Q over top-k rows (1, 2, 4 or 8); 0 if none
-  bool vec4;
+  int S;        // workgroups (slices) per row
+  int L;        // slice length, a multiple of 4
+  int xcd_map;  // 1: a row's slices are placed on one XCD (B % 8 == 0)
   const RowParams* rp;
   const int32_t* hist;
   const int64_t* hist_len;
   int hcap;
   const int32_t* bias_ids;
   const float* bias_vals;
-  Patch* patches;
-  int32_t* patch_cnt;
-  int pcap;
-  uint64_t* prep_scratch;
-  int64_t prep_stride;
-  ChunkStat* stats;
-  uint64_t* cand;
-  int ccap;
-  int mcap;
-  size_t merge_lds;
+  // dynamic LDS layout: cand[2][ccap] u64 | region A
+  int ccap;     // candidate buffer entries (each of two ping-pong buffers)
+  int nwords;   // patch bitmap words, ceil(L / 32)
+  int pcap;     // distinct patched ids per slice held in LDS
+  int mcap;     // member sort capacity, a power of two >= 2k
+  int kcap;     // >= every fast row's k
+  int offA;     // byte offset of region A
+  // slice exchange (S > 1)
+  uint64_t* part_cand;  // [B*S*pc]
+  SliceInfo* part_info; // [B*S]
+  uint32_t* arrive;     // [B], zero between calls
+  int pc;
+  // outputs
   const double* d_u;
   uint64_t* rng;
   int32_t* out;
-  float* row_max;
   int32_t* generic_list;
-  int32_t* generic_count;
-  uint32_t* gen_scratch;
-  int64_t gen_vpad;
-  int gen_blocks;
+  int32_t* generic_count;  // this call's counter (zero on entry)
   DebugPtrs dbg;
-  hipEvent_t ev_start;  // optional: recorded around the streaming kernel
-  hipEvent_t ev_stop;
 };
 
-hipError_t launch_sample(const LaunchArgs& a, hipStream_t s);
+struct GenericArgs {
+  const float* logits;
+  int64_t V;
+  const RowParams* rp;
+  const int32_t* hist;
+  const int64_t* hist_len;
+  int hcap;
+  const int32_t* bias_ids;
+  const float* bias_vals;
+  const int32_t* generic_list;
+  const int32_t* generic_count;  // this call's counter
+  int32_t* next_count;           // the next call's counter, zeroed here
+  uint32_t* scratch;             // per workgroup: 5 x vpad uint32
+  int64_t vpad;
+  const double* d_u;
+  uint64_t* rng;
+  int32_t* out;
+  DebugPtrs dbg;
+};
+
+struct LaunchPlan {
+  int nt;        // streaming workgroup size: 256 or 1024
+  bool wave;     // every top-k row has k <= kWaveTopK: per-wave candidate buffers
+  int q;         // per-thread top-Q of the threshold refresh: 1, 2, 4 or 8
+  bool vec4;     // 16-byte loads (V % 4 == 0 and aligned logits)
+  size_t lds;    // dynamic LDS bytes of the streaming kernel
+  int gen_blocks;
+};
+
+hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const LaunchPlan& lp,
+                         hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop);
 hipError_t launch_accept_host(const int32_t* d_ids, int B, int count, int32_t* hist,
                               int64_t* hist_len, int hcap, int row_only, hipStream_t s);
 hipError_t launch_accept_device(const int32_t* d_ids, int B, int64_t V, int32_t* hist,
                                 int64_t* hist_len, int hcap, hipStream_t s);
 hipError_t launch_expf(const float* x, float* y, int64_t n, hipStream_t s);
 hipError_t set_kernel_attributes();
+size_t max_dynamic_lds();
 
 }  // namespace nls

@@ -1,18 +1,19 @@
 // nls_kernels.hip -- gfx950 kernels of the batched token sampler.
 //
-// Pipeline for one nls_sample call over B rows of V fp32 logits:
-//   1. prep_kernel     (B workgroups)  history window + logit bias -> sorted patch
-//                       list per row (penalties S2 and bias S3, sampler.nim:64-76)
-//   2. chunk_kernel    (B x ceil(V/16384) workgroups)  the single HBM pass: each
-//                       workgroup streams a 64 KB chunk into registers, applies
-//                       the patches and temperature (:80-81), reduces max/argmax,
-//                       and for top-k rows keeps every value that can still be
-//                       among the row's k best (superset, exact).
-//   3. merge_kernel    (B workgroups)  greedy rows: argmax (:77-78); top-k rows:
-//                       the exact heap membership/order (:85-95), softmax (:98-100),
-//                       top-p (:103-108), min-p (:110-114) and the draw (:115-121).
-//   4. generic_kernel  whole-row kernel for full-sort rows (:96-97) and for any
-//                       top-k row whose candidate set overflowed the fast path.
+// One nls_sample call over B rows of V fp32 logits runs two kernels:
+//   1. stream_kernel   (B x S workgroups; S slices per row)  the single HBM
+//      pass.  A workgroup builds its slice's penalty/bias patch table in LDS
+//      from the row's history window and logit bias (sampler.nim:64-76),
+//      streams the slice tile by tile (occupancy hides HBM latency), applies patches
+//      and temperature (:80-81), tracks the first argmax (:45-49, :77-78) and,
+//      on top-k rows, keeps every value that can still be among the row's k
+//      best in an LDS buffer behind a rising threshold.  The workgroup that
+//      completes a row (the only one when S == 1) selects the heap-path
+//      members in reference order (:85-95), then runs softmax (:98-100),
+//      top-p (:103-108), min-p (:110-114) and the draw (:115-121).
+//   2. generic_kernel  whole-row stable radix sort for full-sort rows
+//      (:96-97) and for rows the streaming kernel hands on (candidate or
+//      patch overflow).
 //
 // All fp32/fp64 arithmetic follows the reference's order; this file is built
 // with -ffp-contract=off so no multiply-add is fused.
@@ -25,324 +26,39 @@
 
 namespace nls {
 
-// Apply one patch to the original logit: penalties first (:71-74), then bias (:76).
-__device__ __forceinline__ float apply_patch(float v, const Patch& p, const RowParams& P) {
-  if (p.flags & kPatchPen) {
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Penalties first (:71-74), then bias (:76), on the original logit.
+__device__ __forceinline__ float apply_patch(float v, float pen, float bias, uint32_t flags,
+                                             const RowParams& P) {
+  if (flags & kPatchPen) {
     if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
-    v = v - p.pen;
+    v = v - pen;
   }
-  if (p.flags & kPatchBias) v = v + p.bias;
+  if (flags & kPatchBias) v = v + bias;
   return v;
 }
 
-// ---------------------------------------------------------------------------
-// 1. prep: sorted patch list per row
-// ---------------------------------------------------------------------------
-// Entries: history id -> (id << 32); bias j -> (id << 32) | 0x80000000 | j;
-// out-of-range history ids -> all-ones (dropped, sampler.nim:70).  After an
-// ascending sort, a run of equal ids holds that id's history occurrences
-// followed by its bias entry.
-template <int NT>
-__device__ void prep_row(uint64_t* a, int npow, int n_hist, int n, const RowParams& P, int row,
-                         int64_t V, const int32_t* __restrict__ hist, int64_t len, int hcap,
-                         const int32_t* __restrict__ bias_ids, const float* __restrict__ bias_vals,
-                         Patch* __restrict__ out, int32_t* __restrict__ out_cnt, int* smem) {
-  for (int i = threadIdx.x; i < npow; i += NT) {
-    uint64_t e = ~0ull;
-    if (i < n_hist) {
-      const int64_t j = len - n_hist + i;
-      const int id = hist[(int64_t)row * hcap + (int)(j % hcap)];
-      if (id >= 0 && id < V) e = (uint64_t)(uint32_t)id << 32;
-    } else if (i < n) {
-      const int b = i - n_hist;
-      e = ((uint64_t)(uint32_t)bias_ids[P.bias_off + b] << 32) | 0x80000000ull | (uint64_t)b;
-    }
-    a[i] = e;
-  }
-  __syncthreads();
-  bitonic_sort_u64<NT>(a, npow, false);
-  // valid entries form a prefix; count them
-  int nv_local = 0;
-  for (int i = threadIdx.x; i < npow; i += NT) nv_local += (a[i] != ~0ull);
-  const int nv = block_sum<NT>(nv_local, smem);
-  // runs: thread t owns the contiguous slice [lo, hi)
-  const int per = (nv + NT - 1) / NT;
-  const int lo = min(nv, (int)threadIdx.x * per), hi = min(nv, lo + per);
-  int starts = 0;
-  for (int i = lo; i < hi; ++i)
-    starts += (i == 0 || (a[i] >> 32) != (a[i - 1] >> 32));
-  int total;
-  int pos = block_excl_scan<NT>(starts, smem, total);
-  for (int i = lo; i < hi; ++i) {
-    const uint64_t id = a[i] >> 32;
-    if (!(i == 0 || id != (a[i - 1] >> 32))) continue;
-    // run end: first entry with a larger id (binary search)
-    int l = i + 1, r = nv;
-    while (l < r) {
-      const int m = (l + r) >> 1;
-      if ((a[m] >> 32) == id)
-        l = m + 1;
-      else
-        r = m;
-    }
-    const int end = l - 1;
-    const bool has_bias = (a[end] & 0x80000000ull) != 0;
-    const int cnt = (end - i + 1) - (has_bias ? 1 : 0);
-    Patch p;
-    p.id = (int32_t)id;
-    p.flags = (cnt > 0 ? kPatchPen : 0) | (has_bias ? kPatchBias : 0);
-    p.pen = 0.0f;
-    if (cnt > 0) {
-      const double pen = (double)cnt * P.freq + P.pres;  // float64, one rounding (:74)
-      p.pen = (float)pen;
-    }
-    p.bias = has_bias ? bias_vals[P.bias_off + (int)(a[end] & 0x7fffffffull)] : 0.0f;
-    out[pos++] = p;
-  }
-  if (threadIdx.x == 0) out_cnt[row] = total;
-}
-
-__global__ __launch_bounds__(256) void prep_kernel(
-    const RowParams* __restrict__ rp, int64_t V, const int32_t* __restrict__ hist,
-    const int64_t* __restrict__ hist_len, int hcap, const int32_t* __restrict__ bias_ids,
-    const float* __restrict__ bias_vals, Patch* __restrict__ patches,
-    int32_t* __restrict__ patch_cnt, int pcap, uint64_t* __restrict__ gscratch,
-    int64_t gscratch_stride, int32_t* __restrict__ generic_count) {
-  constexpr int NT = 256;
-  __shared__ uint64_t sbuf[kPrepSortLds];
-  __shared__ int smem[NT / kWave + 4];
-  const int row = blockIdx.x;
-  if (row == 0 && threadIdx.x == 0) *generic_count = 0;
-  const RowParams P = rp[row];
-  const int64_t len = hist_len[row];
-  int n_hist = 0;
-  if (len > 0 && P.pen_active)
-    n_hist = (int)((P.repeat_last_n > 0) ? (P.repeat_last_n < len ? P.repeat_last_n : len) : len);
-  const int n = n_hist + P.bias_cnt;
-  if (n == 0) {
-    if (threadIdx.x == 0) patch_cnt[row] = 0;
-    return;
-  }
-  const int npow = next_pow2(n);
-  Patch* out = patches + (int64_t)row * pcap;
-  if (npow <= kPrepSortLds) {
-    prep_row<NT>(sbuf, npow, n_hist, n, P, row, V, hist, len, hcap, bias_ids, bias_vals, out,
-                 patch_cnt, smem);
-  } else {
-    prep_row<NT>(gscratch + (int64_t)row * gscratch_stride, npow, n_hist, n, P, row, V, hist,
-                 len, hcap, bias_ids, bias_vals, out, patch_cnt, smem);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// 2. chunk pass (the only full read of the logits)
-// ---------------------------------------------------------------------------
-// Lower bound for the chunk's k-th largest: the k-th largest of the threads'
-// top-Q values (those are k real chunk elements), so every element that can be
-// among the row's k best is >= it.
-template <int Q>
-__device__ __forceinline__ void topq_insert(uint32_t (&t)[Q], uint32_t key) {
-  if (key > t[Q - 1]) {
-    t[Q - 1] = key;
-#pragma unroll
-    for (int s = Q - 1; s > 0; --s) {
-      if (t[s] > t[s - 1]) {
-        const uint32_t x = t[s];
-        t[s] = t[s - 1];
-        t[s - 1] = x;
-      }
-    }
-  }
-}
-
-constexpr int kPatchRound = 512;
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-template <int NV4, int Q, bool VEC>
-__global__ __launch_bounds__(kChunkThreads) void chunk_kernel(
-    const float* __restrict__ logits, int64_t V, int nchunks, const RowParams* __restrict__ rp,
-    const Patch* __restrict__ patches, const int32_t* __restrict__ patch_cnt, int pcap,
-    ChunkStat* __restrict__ stats, uint64_t* __restrict__ cand, int ccap) {
-  constexpr int NT = kChunkThreads;
-  constexpr int NE = NV4 * 4;
-  constexpr int CH = NT * NE;
-  __shared__ uint32_t bitmap[CH / 32];
-  __shared__ Patch plist[kPatchRound];
-  __shared__ uint32_t hist[256];
-  __shared__ int smem[NT / kWave + 4];
-  __shared__ float red_v[NT / kWave];
-  __shared__ int red_i[NT / kWave];
-  __shared__ int prange[2];
-
-  const int row = blockIdx.x / nchunks;
-  const int c = blockIdx.x - row * nchunks;
-  const RowParams P = rp[row];
-  const int c0 = c * CH;
-  const int clen = (int)((V - c0) < CH ? (V - c0) : CH);
-  const float* __restrict__ src = logits + (int64_t)row * V + c0;
-  const int tid = threadIdx.x;
-
-  float v[NE];
+// Loads tile `toff` of a slice into registers: thread t owns the float4 groups
+// (j * NT + t) for j < NV4, so each wave's load covers 1 KB contiguously.
+// Elements at or beyond `len` read as 0 and are masked by the caller.
+template <int NT, int NV4, bool VEC>
+__device__ __forceinline__ void load_tile(f32x4 (&R)[NV4], const float* __restrict__ src, int toff,
+                                          int len) {
 #pragma unroll
   for (int j = 0; j < NV4; ++j) {
-    const int o = (j * NT + tid) * 4;
-    if (VEC && o + 4 <= clen) {
-      const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + o));
-      v[4 * j + 0] = t.x;
-      v[4 * j + 1] = t.y;
-      v[4 * j + 2] = t.z;
-      v[4 * j + 3] = t.w;
+    const int o = toff + (j * NT + (int)threadIdx.x) * 4;
+    if (VEC) {
+      // VEC implies len % 4 == 0: a group is either whole or absent
+      R[j] = (o < len) ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + o))
+                       : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[4 * j + e] = (o + e < clen) ? src[o + e] : 0.0f;
+      R[j].x = (o + 0 < len) ? src[o + 0] : 0.0f;
+      R[j].y = (o + 1 < len) ? src[o + 1] : 0.0f;
+      R[j].z = (o + 2 < len) ? src[o + 2] : 0.0f;
+      R[j].w = (o + 3 < len) ? src[o + 3] : 0.0f;
     }
   }
-
-  // ---- patches (penalties + bias) for ids in [c0, c0 + clen) ----
-  const int pn = patch_cnt[row];
-  if (pn > 0) {
-    const Patch* __restrict__ pl = patches + (int64_t)row * pcap;
-    if (tid < 2) {
-      const int target = c0 + (tid ? clen : 0);
-      int l = 0, r = pn;
-      while (l < r) {
-        const int m = (l + r) >> 1;
-        if (pl[m].id < target)
-          l = m + 1;
-        else
-          r = m;
-      }
-      prange[tid] = l;
-    }
-    __syncthreads();
-    const int pa = prange[0], pb = prange[1];
-    for (int base = pa; base < pb; base += kPatchRound) {
-      const int cnt = min(kPatchRound, pb - base);
-      for (int q = tid; q < CH / 32; q += NT) bitmap[q] = 0u;
-      for (int q = tid; q < cnt; q += NT) plist[q] = pl[base + q];
-      __syncthreads();
-      for (int q = tid; q < cnt; q += NT) {
-        const int off = plist[q].id - c0;
-        atomicOr(&bitmap[off >> 5], 1u << (off & 31));
-      }
-      __syncthreads();
-#pragma unroll
-      for (int j = 0; j < NV4; ++j) {
-        const int o = (j * NT + tid) * 4;
-        const uint32_t bits4 = (bitmap[o >> 5] >> (o & 31)) & 15u;
-        if (bits4) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if ((bits4 >> e) & 1u) {
-              const int id = c0 + o + e;
-              int l = 0, r = cnt - 1;
-              while (l < r) {
-                const int m = (l + r) >> 1;
-                if (plist[m].id < id)
-                  l = m + 1;
-                else
-                  r = m;
-              }
-              v[4 * j + e] = apply_patch(v[4 * j + e], plist[l], P);
-            }
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-
-  // ---- temperature (:80-81) ----
-  if (P.mode != kModeGreedy) {
-    const float invT = P.invT;
-#pragma unroll
-    for (int q = 0; q < NE; ++q) v[q] = v[q] * invT;
-  }
-
-  // ---- max / first argmax ----
-  {
-    float bv = -__builtin_inff();
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < NV4; ++j) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int o = (j * NT + tid) * 4 + e;
-        if (o < clen) argmax_merge(bv, bi, v[4 * j + e], c0 + o);
-      }
-    }
-    wave_argmax(bv, bi);
-    if (lane_id() == 0) {
-      red_v[tid >> 6] = bv;
-      red_i[tid >> 6] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      float fv = red_v[0];
-      int fi = red_i[0];
-      for (int w = 1; w < NT / kWave; ++w) argmax_merge(fv, fi, red_v[w], red_i[w]);
-      ChunkStat& s = stats[blockIdx.x];
-      s.vmax = fv;
-      s.amax = fi;
-      s.ncand = 0;
-      s.flags = 0;
-    }
-  }
-  if (P.mode != kModeTopK || !P.fast) return;
-
-  // ---- top-k candidates: every value >= LB, LB <= the chunk's k-th largest ----
-  const int k = P.k;
-  uint32_t lb = 0u;
-  if (clen > k && k <= NT * Q) {
-    uint32_t tops[Q];
-#pragma unroll
-    for (int q = 0; q < Q; ++q) tops[q] = 0u;
-#pragma unroll
-    for (int j = 0; j < NV4; ++j) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int o = (j * NT + tid) * 4 + e;
-        if (o < clen) topq_insert<Q>(tops, f2key(v[4 * j + e]));
-      }
-    }
-    lb = block_radix_select<NT>(
-        [&](auto fn) {
-#pragma unroll
-          for (int q = 0; q < Q; ++q) fn(tops[q]);
-        },
-        k, hist, smem);
-  }
-  int mine = 0;
-#pragma unroll
-  for (int j = 0; j < NV4; ++j) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int o = (j * NT + tid) * 4 + e;
-      mine += (o < clen && f2key(v[4 * j + e]) >= lb);
-    }
-  }
-  int total;
-  int pos = block_excl_scan<NT>(mine, smem, total);
-  if (total > ccap) {
-    if (tid == 0) {
-      stats[blockIdx.x].ncand = total;
-      stats[blockIdx.x].flags = kChunkOverflow;
-    }
-    return;
-  }
-  uint64_t* __restrict__ dst = cand + (int64_t)blockIdx.x * ccap;
-#pragma unroll
-  for (int j = 0; j < NV4; ++j) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int o = (j * NT + tid) * 4 + e;
-      if (o < clen) {
-        const uint32_t key = f2key(v[4 * j + e]);
-        if (key >= lb) dst[pos++] = ((uint64_t)key << 32) | (uint32_t)(c0 + o);
-      }
-    }
-  }
-  if (tid == 0) stats[blockIdx.x].ncand = total;
 }
 
 // ---------------------------------------------------------------------------
@@ -362,7 +78,7 @@ struct TailOut {
 };
 
 template <int NT, typename VPtr, typename IPtr, typename EPtr>
-__device__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr e, int ncand, const RowParams& P,
+__device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr e, int ncand, const RowParams& P,
                                        double u, int* smem) {
   const float mx = val[0];  // candidates are in non-increasing order
   for (int i = threadIdx.x; i < ncand; i += NT) e[i] = expf_cr(val[i] - mx);
@@ -448,7 +164,7 @@ __device__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr e, int ncand, co
 
 
 template <int NT, typename EPtr, typename IPtr>
-__device__ void write_debug(const DebugPtrs& dbg, int row, int path, int n, int ncand,
+__device__ __forceinline__ void write_debug(const DebugPtrs& dbg, int row, int path, int n, int ncand,
                             float total, IPtr ids, EPtr probs) {
   if (threadIdx.x == 0) {
     if (dbg.n) dbg.n[row] = n;
@@ -474,169 +190,953 @@ __device__ __forceinline__ double row_uniform(const double* __restrict__ d_u, ui
   return u;
 }
 
-// ---------------------------------------------------------------------------
-// 3. merge: greedy rows and top-k rows
-// ---------------------------------------------------------------------------
-// Dynamic LDS: entries[ncap] u64 | members[mcap] u64 | vals[mcap] f32 |
-//              ids[mcap] i32 | e[mcap] f32
-template <int NT>
-__global__ __launch_bounds__(NT) void merge_kernel(
-    const RowParams* __restrict__ rp, int nchunks, const ChunkStat* __restrict__ stats,
-    const uint64_t* __restrict__ cand, int ccap, int mcap, const double* __restrict__ d_u,
-    uint64_t* __restrict__ rng, int32_t* __restrict__ out, float* __restrict__ row_max,
-    int32_t* __restrict__ generic_list, int32_t* __restrict__ generic_count, DebugPtrs dbg) {
-  extern __shared__ __align__(16) unsigned char dyn[];
-  __shared__ uint32_t hist[256];
-  __shared__ int smem[NT / kWave + 4];
-  __shared__ int offs[kMaxChunks + 1];
-  __shared__ int s_flag;
-  const int row = blockIdx.x;
-  const RowParams P = rp[row];
-  const ChunkStat* st = stats + (int64_t)row * nchunks;
 
-  if (P.mode == kModeGreedy) {
-    if (threadIdx.x == 0) {
-      float bv = st[0].vmax;
-      int bi = st[0].amax;
-      for (int c = 1; c < nchunks; ++c) argmax_merge(bv, bi, st[c].vmax, st[c].amax);
-      out[row] = bi;
-      if (dbg.n) dbg.n[row] = 0;
-      if (dbg.ncand) dbg.ncand[row] = 0;
-      if (dbg.total) dbg.total[row] = 0.0f;
-      if (dbg.path) dbg.path[row] = 1;
-    }
-    return;
-  }
-  if (P.mode == kModeFull || !P.fast) {
-    if (threadIdx.x == 0) {
-      float bv = st[0].vmax;
-      int bi = st[0].amax;
-      for (int c = 1; c < nchunks; ++c) argmax_merge(bv, bi, st[c].vmax, st[c].amax);
-      row_max[row] = bv;
-      generic_list[atomicAdd(generic_count, 1)] = row;
-    }
-    return;
-  }
-  // ---- top-k row ----
-  if (threadIdx.x == 0) {
-    int acc = 0, flag = 0;
-    for (int c = 0; c < nchunks; ++c) {
-      offs[c] = acc;
-      acc += st[c].ncand;
-      flag |= st[c].flags;
-    }
-    offs[nchunks] = acc;
-    s_flag = flag;
-  }
-  __syncthreads();
-  const int N = offs[nchunks];
-  if (s_flag || N > nchunks * ccap) {
-    if (threadIdx.x == 0) generic_list[atomicAdd(generic_count, 1)] = row;
-    return;
-  }
-  const int ncap = nchunks * ccap;
-  uint64_t* ent = reinterpret_cast<uint64_t*>(dyn);
-  uint64_t* mem = ent + ncap;
-  float* vals = reinterpret_cast<float*>(mem + mcap);
-  int32_t* ids = reinterpret_cast<int32_t*>(vals + mcap);
-  float* ebuf = reinterpret_cast<float*>(ids + mcap);
+// Agent-scope (device-wide coherent) relaxed stores and loads for the slice
+// exchange between workgroups of one row.
+template <typename T>
+__device__ __forceinline__ void store_agent(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T load_agent(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-  for (int c = 0; c < nchunks; ++c) {
-    const int cnt = offs[c + 1] - offs[c];
-    const uint64_t* srcc = cand + ((int64_t)row * nchunks + c) * ccap;
-    for (int i = threadIdx.x; i < cnt; i += NT) ent[offs[c] + i] = srcc[i];
-  }
-  __syncthreads();
-  const int k = P.k;
-  const uint32_t T = block_radix_select<NT>(
-      [&](auto fn) {
-        for (int i = threadIdx.x; i < N; i += NT) fn((uint32_t)(ent[i] >> 32));
-      },
-      k, hist, smem);
-  int gt_l = 0, ge_l = 0;
-  for (int i = threadIdx.x; i < N; i += NT) {
-    const uint32_t key = (uint32_t)(ent[i] >> 32);
-    gt_l += key > T;
-    ge_l += key >= T;
-  }
-  const int gt = block_sum<NT>(gt_l, smem);
-  const int ge = block_sum<NT>(ge_l, smem);
-  const int m = k - gt;  // ties at T to keep
-  const int kpow = next_pow2(k);
-  if (ge == k) {
-    // no excess ties: the members are exactly the entries >= T
-    int mine = 0;
-    for (int i = threadIdx.x; i < N; i += NT) mine += ((uint32_t)(ent[i] >> 32) >= T);
-    int tot;
-    int pos = block_excl_scan<NT>(mine, smem, tot);
-    for (int i = threadIdx.x; i < N; i += NT)
-      if ((uint32_t)(ent[i] >> 32) >= T) mem[pos++] = ent[i];
-  } else {
-    // excess ties: heap rule (members = G + the m largest indices among ties
-    // at or before p*, p* = index of the k-th entry >= T in index order)
-    if (next_pow2(ge) > mcap) {
-      if (threadIdx.x == 0) generic_list[atomicAdd(generic_count, 1)] = row;
-      return;
-    }
-    const int gpow = next_pow2(ge);
-    int mine = 0;
-    for (int i = threadIdx.x; i < N; i += NT) mine += ((uint32_t)(ent[i] >> 32) >= T);
-    int tot;
-    int pos = block_excl_scan<NT>(mine, smem, tot);
-    for (int i = threadIdx.x; i < N; i += NT) {
-      const uint64_t x = ent[i];
-      if ((uint32_t)(x >> 32) >= T) mem[pos++] = (x << 32) | (x >> 32);  // idx-major
-    }
-    for (int i = ge + threadIdx.x; i < gpow; i += NT) mem[i] = ~0ull;
-    __syncthreads();
-    bitonic_sort_u64<NT>(mem, gpow, false);
-    // ties among the first k (index order); keep the last m of them
-    int tl = 0;
-    const int per = (k + NT - 1) / NT;
-    const int lo = min(k, (int)threadIdx.x * per), hi = min(k, lo + per);
-    for (int i = lo; i < hi; ++i) tl += ((uint32_t)mem[i] == T);
-    int ntie;
-    int trank = block_excl_scan<NT>(tl, smem, ntie);
-    // members, written key-major into ent[] (free now): every entry with
-    // key > T (any index) plus the selected ties
-    int keep_l = 0;
-    for (int i = threadIdx.x; i < ge; i += NT) keep_l += ((uint32_t)mem[i] > T);
-    int gtot;
-    int gpos = block_excl_scan<NT>(keep_l, smem, gtot);
-    for (int i = threadIdx.x; i < ge; i += NT) {
-      const uint64_t x = mem[i];
-      if ((uint32_t)x > T) ent[gpos++] = (x << 32) | (x >> 32);
-    }
-    for (int i = lo; i < hi; ++i) {
-      const uint64_t x = mem[i];
-      if ((uint32_t)x == T) {
-        if (trank >= ntie - m) ent[gtot + (trank - (ntie - m))] = (x << 32) | (x >> 32);
-        ++trank;
-      }
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < k; i += NT) mem[i] = ent[i];
-    __syncthreads();
-  }
-  for (int i = k + threadIdx.x; i < kpow; i += NT) mem[i] = 0ull;
-  __syncthreads();
-  // reference order: descending (value, index)
-  bitonic_sort_u64<NT>(mem, kpow, true);
-  for (int i = threadIdx.x; i < k; i += NT) {
-    vals[i] = key2f((uint32_t)(mem[i] >> 32));
-    ids[i] = (int32_t)(uint32_t)mem[i];
-  }
-  __syncthreads();
-  __shared__ double s_u;
-  if (threadIdx.x == 0) s_u = row_uniform(d_u, rng, row);
-  __syncthreads();
-  const TailOut t = softmax_cutoff_draw<NT>(vals, ids, ebuf, k, P, s_u, smem);
-  if (threadIdx.x == 0) out[row] = t.id;
-  write_debug<NT>(dbg, row, 2, t.n, k, t.total, ids, ebuf);
+__device__ __forceinline__ void push_generic(int32_t* list, int32_t* count, int row) {
+  list[atomicAdd(count, 1)] = row;
 }
 
 // ---------------------------------------------------------------------------
-// 4. generic: whole-row stable radix sort, then the reference's tail
+// Heap-path members (sampler.nim:85-95) from a candidate set
+// ---------------------------------------------------------------------------
+// ent[0..N): (key << 32 | id) entries holding every element of the row whose
+// key is >= some threshold no larger than the row's k-th largest key, with
+// N >= k and k < V.  Writes the k members, key-major and in no particular
+// order, to mem[0..k).  Membership: T = k-th largest, G = {key > T},
+// m = k - |G|, p* = index at which the running count of {key >= T} reaches
+// k; members = G + the m largest indices among ties at T with index <= p*.
+// Returns false (uniformly) when the tie set does not fit `mem`.
+// `s_cnt` is an LDS counter set to 0 before the call.
+template <int NT>
+__device__ __forceinline__ bool topk_members(uint64_t* ent, int N, int k, uint64_t* mem, int mcap,
+                                             uint32_t* hist, int* smem, int* s_cnt) {
+  // fit = k: stop as soon as the items >= the current prefix are exactly k
+  const SelectResult sr = block_select<NT>(
+      [&](auto fn) {
+        for (int i0 = 0; i0 < N; i0 += NT) {
+          const int i = i0 + (int)threadIdx.x;
+          const bool in = i < N;
+          fn(in ? (uint32_t)(ent[i] >> 32) : 0u, in);
+        }
+      },
+      k, k, hist, smem);
+  const uint32_t T = sr.tau;
+  const int gt = sr.gt, ge = sr.ge;
+  if (ge == k) {
+    // no excess ties: the members are exactly the entries >= T
+    for (int i = threadIdx.x; i < N; i += NT) {
+      const uint64_t x = ent[i];
+      if ((uint32_t)(x >> 32) >= T) mem[atomicAdd(s_cnt, 1)] = x;
+    }
+    __syncthreads();
+    return true;
+  }
+  // excess ties at the exact T (the select ran to the last digit)
+  const int m = k - gt;
+  const int gpow = next_pow2(ge);
+  if (gpow > mcap) return false;
+  int mine = 0;
+  for (int i = threadIdx.x; i < N; i += NT) mine += ((uint32_t)(ent[i] >> 32) >= T);
+  int tot;
+  int pos = block_excl_scan<NT>(mine, smem, tot);
+  for (int i = threadIdx.x; i < N; i += NT) {
+    const uint64_t x = ent[i];
+    if ((uint32_t)(x >> 32) >= T) mem[pos++] = (x << 32) | (x >> 32);  // index-major
+  }
+  for (int i = ge + threadIdx.x; i < gpow; i += NT) mem[i] = ~0ull;
+  __syncthreads();
+  bitonic_sort_u64<NT>(mem, gpow, false);
+  // mem[0..k): the elements >= T with index <= p*; keep the last m ties
+  int tl = 0;
+  const int per = (k + NT - 1) / NT;
+  const int lo = min(k, (int)threadIdx.x * per), hi = min(k, lo + per);
+  for (int i = lo; i < hi; ++i) tl += ((uint32_t)mem[i] == T);
+  int ntie;
+  int trank = block_excl_scan<NT>(tl, smem, ntie);
+  int keep_l = 0;
+  for (int i = threadIdx.x; i < ge; i += NT) keep_l += ((uint32_t)mem[i] > T);
+  int gtot;
+  int gpos = block_excl_scan<NT>(keep_l, smem, gtot);
+  for (int i = threadIdx.x; i < ge; i += NT) {
+    const uint64_t x = mem[i];
+    if ((uint32_t)x > T) ent[gpos++] = (x << 32) | (x >> 32);
+  }
+  for (int i = lo; i < hi; ++i) {
+    const uint64_t x = mem[i];
+    if ((uint32_t)x == T) {
+      if (trank >= ntie - m) ent[gtot + (trank - (ntie - m))] = (x << 32) | (x >> 32);
+      ++trank;
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < k; i += NT) mem[i] = ent[i];
+  __syncthreads();
+  return true;
+}
+
+// The row's uniform (sampler.nim:117): the caller's value, or the next
+// rand(1.0) of the row's own stream, whose advanced state is written back.
+// `u_in`/`st` were read at kernel start by the calling lane.
+__device__ __forceinline__ double take_uniform(const double* d_u, double u_in, uint64_t st0,
+                                               uint64_t st1, uint64_t* rng, int row) {
+  if (d_u) return u_in;
+  uint64_t st[2] = {st0, st1};
+  const double u = nim_rand_unit(st);
+  rng[2 * row] = st[0];
+  rng[2 * row + 1] = st[1];
+  return u;
+}
+
+__device__ __forceinline__ float lane_fc(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+
+// The reference's tail on one wave, for k <= 64 members (mem[0..k), any
+// order): lane i holds candidate i after a descending (value, index) bitonic
+// sort (sampler.nim:88-95), then softmax (:98-100, :51-57), top-p (:103-108),
+// min-p (:110-114) and the draw (:115-121).  Every sequential fp32 sum runs
+// in candidate order as an unrolled chain; the top-p running sum doubles as
+// `total`, which the reference accumulates with the same operations.
+__device__ __forceinline__ void wave_tail(const uint64_t* mem, int k, const RowParams& P,
+                                          double u_lane0, int row, int32_t* out,
+                                          const DebugPtrs& dbg) {
+  const int lane = lane_id();
+  uint64_t x = (lane < k) ? mem[lane] : 0ull;
+#pragma unroll
+  for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint32_t ylo = (uint32_t)__shfl_xor((int)(uint32_t)x, stride, kWave);
+      const uint32_t yhi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), stride, kWave);
+      const uint64_t y = ((uint64_t)yhi << 32) | ylo;
+      const bool keep_max = ((lane & stride) == 0) == ((lane & size) == 0);
+      x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
+    }
+  }
+  const bool valid = lane < k;
+  const int id = (int)(uint32_t)x;
+  const float v = key2f((uint32_t)(x >> 32));
+  const float mx = lane_fc(v, 0);
+  const float e = valid ? expf_cr(v - mx) : 0.0f;
+  // s = e_0 + e_1 + ... in order; the zero tail past k leaves s unchanged
+  float ssum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kWave; ++i) ssum = ssum + lane_fc(e, i);
+  const float p = valid ? e / ssum : 0.0f;
+  float acc = 0.0f, cum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kWave; ++i) {
+    acc = acc + lane_fc(p, i);
+    if (lane == i) cum = acc;
+  }
+  int n = k;
+  if (P.topp_active) {
+    const uint64_t m = __ballot(valid && (double)cum >= P.topP);
+    if (m) n = __ffsll((unsigned long long)m);
+  }
+  if (P.minp_active) {
+    const float thr = lane_fc(p, 0) * P.minP32;
+    const uint64_t m = __ballot(lane >= 1 && lane < n && !(p >= thr));
+    if (m) n = __ffsll((unsigned long long)m) - 1;
+  }
+  const float total = lane_fc(cum, n - 1);
+  const double u = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(u_lane0), 0),
+                                    __builtin_amdgcn_readlane(__double2loint(u_lane0), 0));
+  float r = (float)u * total;
+  float rl = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kWave; ++i) {
+    r = r - lane_fc(p, i);
+    if (lane == i) rl = r;
+  }
+  const uint64_t hit = __ballot(lane < n && rl <= 0.0f);
+  const int pos = hit ? __ffsll((unsigned long long)hit) - 1 : n - 1;
+  const int tok = __builtin_amdgcn_readlane(id, pos);
+  if (lane == 0) {
+    out[row] = tok;
+    if (dbg.n) dbg.n[row] = n;
+    if (dbg.ncand) dbg.ncand[row] = k;
+    if (dbg.total) dbg.total[row] = total;
+    if (dbg.path) dbg.path[row] = 2;
+  }
+  if (lane < min(n, dbg.cap)) {
+    if (dbg.cand_ids) dbg.cand_ids[(int64_t)row * dbg.cap + lane] = id;
+    if (dbg.cand_probs) dbg.cand_probs[(int64_t)row * dbg.cap + lane] = p;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 1. stream_kernel
+// ---------------------------------------------------------------------------
+// Dynamic LDS: cand[2][ccap] u64 | region A.
+// Region A up to the final selection: bitmap[nwords] u32 | wpre[nwords] u16
+// (padded to 4 bytes) | pfin[pcap] f32 | pbias[pcap] f32 | pflag[pcap] u32 |
+// pid[pcap] i32.  Afterwards it holds the tail: mem[mcap] u64 |
+// vals[kcap] f32 | ids[kcap] i32 | e[kcap] f32.
+//
+// Penalties and bias touch few ids of a slice [lo, lo + len) (the patched
+// ids).  Bit (id - lo) of `bitmap` marks them; patch p of a marked id sits
+// at wpre[w] + popcount(bits of word w below it).  Their original logits are
+// gathered up front and their final values (pfin) computed once, so the
+// stream leaves them out -- only where a value would be kept or would raise
+// the argmax does it test the bitmap -- and they rejoin the candidates (or
+// the argmax) after the stream.
+template <int NT, bool VEC, int Q, bool WAVE>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT <= 256 ? 4 : 2)))
+void stream_kernel(const StreamArgs a) {
+  constexpr int NW = NT / kWave;
+  constexpr int NV4 = kStreamVec4;
+  constexpr int NE = NV4 * 4;
+  constexpr int TE = NT * NE;
+  constexpr int PER = kWaveCap / kWave;  // wave path: buffer entries per lane
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ int smem[NW + 4];
+  // block_select histogram; while streaming, the wave path's per-wave ones
+  constexpr int kHistWords = kSelWords > NW * kWaveBins ? kSelWords : NW * kWaveBins;
+  __shared__ uint32_t shist[kHistWords];
+  __shared__ int s_wn[NW];
+  __shared__ uint32_t s_wt[NW];
+  __shared__ uint32_t s_tau;  // wave path: the highest published wave threshold
+  __shared__ int s_tile_cnt[3];
+  __shared__ int s_cnt;
+  __shared__ float s_rv[NW];
+  __shared__ int s_ri[NW];
+  __shared__ int s_last;
+  __shared__ double s_u;
+
+  int row, sl;
+  if (a.xcd_map) {
+    const int x = (int)(blockIdx.x & 7u), slot = (int)(blockIdx.x >> 3);
+    row = (slot / a.S) * 8 + x;
+    sl = slot - (slot / a.S) * a.S;
+  } else {
+    row = (int)blockIdx.x / a.S;
+    sl = (int)blockIdx.x - row * a.S;
+  }
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wv = tid >> 6;
+  const RowParams P = a.rp[row];
+  const int64_t hlen = a.hist_len[row];
+  if (P.mode == kModeFull || !P.fast) {
+    if (sl == 0 && tid == 0) push_generic(a.generic_list, a.generic_count, row);
+    return;
+  }
+  const bool greedy = P.mode == kModeGreedy;
+  const bool topk = P.mode == kModeTopK;
+  const int k = P.k;
+  const int lo = sl * a.L;
+  const int len = (int)min((int64_t)a.L, a.V - (int64_t)lo);
+  const float* __restrict__ src = a.logits + (int64_t)row * a.V + lo;
+  const int ntiles = (len + TE - 1) / TE;
+  // the first tile is in flight while the patch table is built
+  f32x4 R[NV4];
+  load_tile<NT, NV4, VEC>(R, src, 0, len);
+
+  uint64_t* cand = reinterpret_cast<uint64_t*>(lds);
+  unsigned char* regA = lds + a.offA;
+  uint32_t* bitmap = reinterpret_cast<uint32_t*>(regA);
+  uint16_t* wpre = reinterpret_cast<uint16_t*>(regA + (size_t)a.nwords * 4);
+  float* pfin = reinterpret_cast<float*>(regA + (size_t)a.nwords * 4 + (((size_t)a.nwords * 2 + 3) & ~(size_t)3));
+  float* pbias = pfin + a.pcap;
+  uint32_t* pflag = reinterpret_cast<uint32_t*>(pbias + a.pcap);  // flags | count << 2
+  int32_t* pid = reinterpret_cast<int32_t*>(pflag + a.pcap);
+
+  // the row's uniform or RNG state, read now so the tail does not wait
+  double u_in = 0.0;
+  uint64_t st0 = 0ull, st1 = 0ull;
+  if (tid == 0 && !greedy) {
+    if (a.d_u) {
+      u_in = a.d_u[row];
+    } else {
+      st0 = a.rng[2 * row];
+      st1 = a.rng[2 * row + 1];
+    }
+  }
+  for (int q = tid; q < kHistWords; q += NT) shist[q] = 0u;  // the selects need it zeroed
+  if (tid == 0) {
+    s_tile_cnt[0] = 0;
+    s_tile_cnt[1] = 0;
+    s_tile_cnt[2] = 0;
+    s_cnt = 0;
+    s_tau = 0u;
+  }
+
+  // ---- patched ids (penalties :64-74, bias :75-76) ----
+  bool ovf = false;
+  int npatch = 0;
+  int n_hist = 0;
+  if (P.pen_active && hlen > 0)
+    n_hist = (int)((P.repeat_last_n > 0 && P.repeat_last_n < hlen) ? P.repeat_last_n : hlen);
+  const bool has_patch = n_hist > 0 || P.bias_cnt > 0;
+  if (has_patch) {
+    constexpr int HPT = 8;  // window ids per thread per round trip
+    const int nw = (len + 31) >> 5;
+    const int hbase = (int)((hlen - n_hist) % a.hcap);
+    const int32_t* __restrict__ hrow = a.hist + (int64_t)row * a.hcap;
+    // slice-local offset of window entry i, or -1 when it is not in the slice
+    // (ids outside [0, V) are stored as -1 by accept)
+    auto hist_loc = [&](int i) -> int {
+      int slot = hbase + i;
+      if (slot >= a.hcap) slot -= a.hcap;
+      const int id = hrow[slot];
+      const int loc = id - lo;
+      return (id >= 0 && loc >= 0 && loc < len) ? loc : -1;
+    };
+    const bool one_round = n_hist <= NT * HPT;
+    int hl[HPT];
+    float hraw[HPT];
+    if (one_round) {
+#pragma unroll
+      for (int h = 0; h < HPT; ++h) {
+        const int i = h * NT + tid;
+        hl[h] = (i < n_hist) ? hist_loc(i) : -1;
+      }
+#pragma unroll
+      for (int h = 0; h < HPT; ++h) hraw[h] = hl[h] >= 0 ? src[hl[h]] : 0.0f;
+    }
+    // fn(loc, raw) for every window entry of the slice (loc < 0: not in it)
+    auto for_window = [&](auto fn) __attribute__((always_inline)) {
+      if (one_round) {
+#pragma unroll
+        for (int h = 0; h < HPT; ++h) fn(hl[h], hraw[h]);
+      } else {
+        for (int b0 = 0; b0 < n_hist; b0 += NT * HPT) {
+          int l[HPT];
+          float r[HPT];
+#pragma unroll
+          for (int h = 0; h < HPT; ++h) {
+            const int i = b0 + h * NT + tid;
+            l[h] = (i < n_hist) ? hist_loc(i) : -1;
+          }
+#pragma unroll
+          for (int h = 0; h < HPT; ++h) r[h] = l[h] >= 0 ? src[l[h]] : 0.0f;
+#pragma unroll
+          for (int h = 0; h < HPT; ++h) fn(l[h], r[h]);
+        }
+      }
+    };
+    // bias entries of this thread (one round trip when bias_cnt <= NT)
+    const bool bias_one = P.bias_cnt <= NT;
+    int b_loc = -1;
+    float b_val = 0.0f, b_raw = 0.0f;
+    if (bias_one && tid < P.bias_cnt) {
+      const int loc = a.bias_ids[P.bias_off + tid] - lo;
+      b_val = a.bias_vals[P.bias_off + tid];
+      b_loc = (loc >= 0 && loc < len) ? loc : -1;
+      if (b_loc >= 0) b_raw = src[b_loc];
+    }
+    for (int w = tid; w < nw; w += NT) bitmap[w] = 0u;
+    __syncthreads();
+    for_window([&](int loc, float) {
+      if (loc >= 0) atomicOr(&bitmap[loc >> 5], 1u << (loc & 31));
+    });
+    if (bias_one) {
+      if (b_loc >= 0) atomicOr(&bitmap[b_loc >> 5], 1u << (b_loc & 31));
+    } else {
+      for (int j = tid; j < P.bias_cnt; j += NT) {
+        const int loc = a.bias_ids[P.bias_off + j] - lo;
+        if (loc >= 0 && loc < len) atomicOr(&bitmap[loc >> 5], 1u << (loc & 31));
+      }
+    }
+    __syncthreads();
+    const int wpt = (nw + NT - 1) / NT;
+    const int w0 = min(nw, tid * wpt), w1 = min(nw, w0 + wpt);
+    int c = 0;
+    for (int w = w0; w < w1; ++w) c += __popc(bitmap[w]);
+    int pre = block_excl_scan<NT>(c, smem, npatch);
+    if (npatch > a.pcap) {
+      ovf = true;  // uniform
+    } else {
+      for (int w = w0; w < w1; ++w) {
+        wpre[w] = (uint16_t)pre;
+        pre += __popc(bitmap[w]);
+      }
+      for (int p = tid; p < npatch; p += NT) {
+        pbias[p] = 0.0f;
+        pflag[p] = 0u;
+      }
+      __syncthreads();
+      auto pidx = [&](int loc) -> int {
+        const int w = loc >> 5;
+        return wpre[w] + __popc(bitmap[w] & ((1u << (loc & 31)) - 1u));
+      };
+      // every writer of pfin[p] / pid[p] stores the same value
+      for_window([&](int loc, float raw) {
+        if (loc >= 0) {
+          const int p = pidx(loc);
+          atomicAdd(&pflag[p], 4u);
+          pfin[p] = raw;
+          pid[p] = lo + loc;
+        }
+      });
+      auto put_bias = [&](int loc, float val, float raw) {
+        const int p = pidx(loc);
+        pbias[p] = val;  // bias ids are unique per row
+        atomicOr(&pflag[p], (uint32_t)kPatchBias);
+        pfin[p] = raw;
+        pid[p] = lo + loc;
+      };
+      if (bias_one) {
+        if (b_loc >= 0) put_bias(b_loc, b_val, b_raw);
+      } else {
+        for (int j = tid; j < P.bias_cnt; j += NT) {
+          const int loc = a.bias_ids[P.bias_off + j] - lo;
+          if (loc >= 0 && loc < len) put_bias(loc, a.bias_vals[P.bias_off + j], src[loc]);
+        }
+      }
+      __syncthreads();
+      // final values: penalties then bias on the original logit (:71-76),
+      // then temperature (:80-81) on the sampling rows
+      for (int p = tid; p < npatch; p += NT) {
+        const uint32_t fl = pflag[p];
+        const uint32_t cnt = fl >> 2;
+        float v = pfin[p];
+        if (cnt) {
+          if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
+          v = v - (float)((double)cnt * P.freq + P.pres);  // float64, one rounding (:74)
+        }
+        if (fl & kPatchBias) v = v + pbias[p];
+        if (!greedy) v = v * P.invT;
+        pfin[p] = v;
+      }
+    }
+  }
+  __syncthreads();
+  auto patched = [&](int loc) -> bool {  // loc: slice-local offset
+    return has_patch && ((bitmap[loc >> 5] >> (loc & 31)) & 1u);
+  };
+
+  // ---- the stream ----
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+  int buf_n = 0, cur = 0;
+  uint32_t tau = 0u;
+  // wave path (k <= 64): this wave's buffer count, threshold and overflow
+  int wn = 0;
+  uint32_t wtau = 0u;
+  bool wovf = false;
+
+  auto process = [&](float (&v)[NE], int t) __attribute__((always_inline)) {
+    const int toff = t * TE;
+    const bool full = toff + TE <= len;  // no element of the tile lies past the slice
+    // This thread's first element of the tile, made opaque so that the
+    // per-element offsets below are formed here, not hoisted out of the tile
+    // loop into one register each.
+    int obase = toff + tid * 4;
+    asm volatile("" : "+v"(obase));
+    // With 16-byte loads len % 4 == 0, so a float4 group is wholly in or out.
+    auto loc_of = [&](int q) -> int { return obase + (q >> 2) * NT * 4 + (q & 3); };
+    auto valid = [&](int q) -> bool {
+      const int o = obase + (q >> 2) * NT * 4;
+      return full || (VEC ? o < len : o + (q & 3) < len);
+    };
+    if (greedy) {
+      // argmax (:45-49): only a lane whose tile maximum beats its running
+      // best walks the tile in index order (strict >, so the first index wins)
+      float tmx = -__builtin_inff();
+#pragma unroll
+      for (int q = 0; q < NE; ++q)
+        if (valid(q) && v[q] > tmx) tmx = v[q];
+      // (nothing chosen yet: equal values still pick the first index, so a
+      // row of -inf answers its first id)
+      if (tmx > bv || (tmx == bv && bi == 0x7fffffff)) {
+#pragma unroll
+        for (int q = 0; q < NE; ++q)
+          if (valid(q) && !patched(loc_of(q))) argmax_merge(bv, bi, v[q], lo + loc_of(q));
+      }
+      return;
+    }
+    // temperature (:80-81)
+    {
+      const float invT = P.invT;
+#pragma unroll
+      for (int q = 0; q < NE; ++q) v[q] = v[q] * invT;
+    }
+    auto gid = [&](int q) -> uint32_t { return (uint32_t)(lo + loc_of(q)); };
+    if constexpr (WAVE) {
+      // ---- wave path: this wave's own buffer, no barrier ----
+      // Prefilter in the float domain: key(v) >= t implies !(v < key2f(t))
+      // (NaN passes too), so keys are formed only where some lane passes.
+      uint64_t* wb = cand + (size_t)wv * kWaveCap;
+      uint32_t* whist = shist + wv * kWaveBins;
+      if (t == 0) {
+        // Block-wide start: the k-th largest of the per-thread maxima of the
+        // first tile (k real elements) bounds the row's k-th largest from below.
+        uint32_t tmax = 0u;
+        bool has = false;
+#pragma unroll
+        for (int q = 0; q < NE; ++q) {
+          if (valid(q) && !patched(loc_of(q))) {
+            tmax = max(tmax, f2key(v[q]));
+            has = true;
+          }
+        }
+        if (block_sum<NT>(has ? 1 : 0, smem) >= k) {
+          wtau = block_select<NT>([&](auto fn) { fn(tmax, has); }, k, -1, shist, smem).tau;
+          __syncthreads();  // the select's histogram overlaps the per-wave ones
+        }
+      }
+      // any wave's threshold is a lower bound of the k-th largest of the row
+      wtau = max(wtau, __hip_atomic_load(&s_tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+      float thr_f = key2f(wtau);
+      int npf = 0;  // prefilter passes of this tile, over the wave
+#pragma unroll
+      for (int q = 0; q < NE; ++q) npf += __popcll(__ballot(valid(q) && !(v[q] < thr_f)));
+      if (npf == 0) return;
+      if (wn + npf > kWaveCap) {
+        // Raise the threshold to a lower bound of the k-th largest of all this
+        // wave has seen (buffer + tile): the k-th largest of the per-lane top-2.
+        uint32_t tops[2] = {0u, 0u};
+        int nm = 0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int i = lane + j * kWave;
+          if (i < wn) {
+            topq_insert<2>(tops, (uint32_t)(wb[i] >> 32));
+            ++nm;
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < NE; ++q) {
+          if (valid(q) && !(v[q] < thr_f) && !patched(loc_of(q))) {
+            const uint32_t kq = f2key(v[q]);
+            if (kq >= wtau) {
+              topq_insert<2>(tops, kq);
+              ++nm;
+            }
+          }
+        }
+        const int nv = min(nm, 2);
+        int tv;
+        (void)wave_excl_sum_small<2>(nv, tv);
+        if (tv >= k) {
+          wtau = wave_select(
+                     [&](auto fn) {
+#pragma unroll
+                       for (int q = 0; q < 2; ++q) fn(tops[q], q < nv);
+                     },
+                     k, k + k / 2, whist)
+                     .tau;
+          thr_f = key2f(wtau);
+        }
+        // compact the buffer to the new threshold
+        uint64_t xs[PER];
+        int keep = 0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int i = lane + j * kWave;
+          xs[j] = (i < wn) ? wb[i] : 0ull;
+          keep += (i < wn && (uint32_t)(xs[j] >> 32) >= wtau);
+        }
+        int ktot;
+        int pos = wave_excl_sum_small<3>(keep, ktot);  // keep <= PER = 4
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int i = lane + j * kWave;
+          if (i < wn && (uint32_t)(xs[j] >> 32) >= wtau) wb[pos++] = xs[j];
+        }
+        wn = ktot;
+        npf = 0;
+#pragma unroll
+        for (int q = 0; q < NE; ++q) npf += __popcll(__ballot(valid(q) && !(v[q] < thr_f)));
+        if (wn + npf > kWaveCap) {
+          wovf = true;  // ties or an adversarial order crowd the buffer
+          return;
+        }
+      }
+      // append every unpatched value >= the threshold (each passes the prefilter)
+#pragma unroll
+      for (int q = 0; q < NE; ++q) {
+        if (__ballot(valid(q) && !(v[q] < thr_f)) == 0ull) continue;
+        const uint32_t kq = f2key(v[q]);
+        const bool keep = valid(q) && kq >= wtau && !patched(loc_of(q));
+        const uint64_t m = __ballot(keep);
+        if (keep) wb[wn + (int)__popcll(m & lanes_below())] = ((uint64_t)kq << 32) | gid(q);
+        wn += (int)__popcll(m);
+      }
+      if (wn >= 2 * k + kWave) {
+        // tighten: the k-th largest of the buffer (which holds every value >=
+        // the old threshold) is a lower bound of the k-th largest of the row
+        uint64_t xs[PER];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int i = lane + j * kWave;
+          xs[j] = (i < wn) ? wb[i] : 0ull;
+        }
+        const int n0 = wn;
+        const SelectResult r = wave_select(
+            [&](auto fn) {
+#pragma unroll
+              for (int j = 0; j < PER; ++j) fn((uint32_t)(xs[j] >> 32), lane + j * kWave < n0);
+            },
+            k, k + k / 4, whist);
+        int keep = 0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) keep += (lane + j * kWave < n0 && (uint32_t)(xs[j] >> 32) >= r.tau);
+        int ktot;
+        int pos = wave_excl_sum_small<3>(keep, ktot);
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+          if (lane + j * kWave < n0 && (uint32_t)(xs[j] >> 32) >= r.tau) wb[pos++] = xs[j];
+        wn = ktot;
+        wtau = r.tau;
+        if (lane == 0) atomicMax(&s_tau, wtau);
+      }
+      return;
+    } else {
+      // ---- block path (k > 64): one buffer, a barrier per tile ----
+      auto use = [&](int q) -> bool { return valid(q) && !patched(loc_of(q)); };
+      uint32_t key[NE];
+#pragma unroll
+      for (int q = 0; q < NE; ++q) key[q] = f2key(v[q]);
+      int mine = 0;
+#pragma unroll
+      for (int q = 0; q < NE; ++q) mine += (use(q) && key[q] >= tau);
+      int wtot;
+      const int wex = wave_excl_sum_small<5>(mine, wtot);  // mine <= NE = 16
+      const int slot = t % 3;
+      int wbase = 0;
+      if (lane == 0 && wtot) wbase = atomicAdd(&s_tile_cnt[slot], wtot);
+      wbase = __shfl(wbase, 0, kWave);
+      __syncthreads();
+      const int ttot = s_tile_cnt[slot];
+      if (tid == 0) s_tile_cnt[(t + 2) % 3] = 0;
+      uint64_t* cb = cand + (size_t)cur * a.ccap;
+      if (buf_n + ttot <= a.ccap) {
+        int pos = buf_n + wbase + wex;
+#pragma unroll
+        for (int q = 0; q < NE; ++q)
+          if (use(q) && key[q] >= tau) cb[pos++] = ((uint64_t)key[q] << 32) | gid(q);
+        buf_n += ttot;
+        return;
+      }
+      // threshold refresh (uniform): raise tau, compact into the other buffer
+      uint64_t* nb = cand + (size_t)(cur ^ 1) * a.ccap;
+      uint32_t tops[Q];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) tops[q] = 0u;
+      int nmine = 0;
+      for (int i = tid; i < buf_n; i += NT) {
+        topq_insert<Q>(tops, (uint32_t)(cb[i] >> 32));
+        ++nmine;
+      }
+#pragma unroll
+      for (int q = 0; q < NE; ++q) {
+        if (use(q) && key[q] >= tau) {
+          topq_insert<Q>(tops, key[q]);
+          ++nmine;
+        }
+      }
+      const int nv = min(nmine, Q);
+      const int tv = block_sum<NT>(nv, smem);
+      // t1 <= the k-th largest of the per-thread tops (k real elements), so t1
+      // is a lower bound of the k-th largest of everything seen.  A coarse
+      // digit prefix is enough while it admits few elements; otherwise refine
+      // to the exact k-th largest of the tops.
+      auto tops_select = [&](int fit) -> uint32_t {
+        return block_select<NT>(
+                   [&](auto fn) {
+#pragma unroll
+                     for (int q = 0; q < Q; ++q) fn(tops[q], q < nv);
+                   },
+                   k, fit, shist, smem)
+            .tau;
+      };
+      auto count_ge = [&](uint32_t th) -> int {
+        int c = 0;
+        for (int i = tid; i < buf_n; i += NT) c += ((uint32_t)(cb[i] >> 32) >= th);
+#pragma unroll
+        for (int q = 0; q < NE; ++q) c += (use(q) && key[q] >= th);
+        return block_sum<NT>(c, smem);
+      };
+      uint32_t t1 = tau;
+      int cnt = buf_n + ttot;
+      if (tv >= k) {
+        t1 = tops_select(2 * k);
+        cnt = count_ge(t1);
+        if (cnt > a.ccap / 2) {
+          t1 = tops_select(-1);
+          cnt = count_ge(t1);
+        }
+      }
+      if (cnt > a.ccap) {
+        // only ties at t1, or values crowded into few threads, get here: the
+        // whole-row kernel takes the row
+        ovf = true;
+        return;
+      }
+      int c1 = 0;
+      for (int i = tid; i < buf_n; i += NT) c1 += ((uint32_t)(cb[i] >> 32) >= t1);
+#pragma unroll
+      for (int q = 0; q < NE; ++q) c1 += (use(q) && key[q] >= t1);
+      int tot;
+      int pos = block_excl_scan<NT>(c1, smem, tot);
+      for (int i = tid; i < buf_n; i += NT) {
+        const uint64_t x = cb[i];
+        if ((uint32_t)(x >> 32) >= t1) nb[pos++] = x;
+      }
+#pragma unroll
+      for (int q = 0; q < NE; ++q)
+        if (use(q) && key[q] >= t1) nb[pos++] = ((uint64_t)key[q] << 32) | gid(q);
+      __syncthreads();
+      cur ^= 1;
+      buf_n = tot;
+      tau = t1;
+    }
+  };
+
+  if (!ovf) {
+    for (int t = 0; t < ntiles; ++t) {
+      if (t > 0) load_tile<NT, NV4, VEC>(R, src, t * TE, len);
+      float v[NE];
+#pragma unroll
+      for (int j = 0; j < NV4; ++j) {
+        v[4 * j + 0] = R[j].x;
+        v[4 * j + 1] = R[j].y;
+        v[4 * j + 2] = R[j].z;
+        v[4 * j + 3] = R[j].w;
+      }
+      process(v, t);
+      if (ovf || wovf) break;  // ovf is block-uniform; wovf is set only on the wave path
+    }
+  }
+
+  // ---- the slice's candidates: stream buffer(s) + patched values ----
+  uint64_t* ent = cand + (size_t)cur * a.ccap;
+  int N = buf_n;
+  if (topk) {
+    uint32_t tau_all = tau;  // a lower bound of the row's k-th largest, uniform
+    if constexpr (WAVE) {
+      // concatenate the wave buffers into the second buffer
+      if (lane == 0) {
+        s_wn[wv] = wovf ? -1 : wn;
+        s_wt[wv] = wtau;
+      }
+      __syncthreads();
+      int off = 0;
+      N = 0;
+      tau_all = 0u;
+      for (int w = 0; w < NW; ++w) {
+        const int nw_ = s_wn[w];
+        tau_all = max(tau_all, s_wt[w]);
+        if (nw_ < 0) {
+          ovf = true;
+        } else {
+          if (w == wv) off = N;
+          N += nw_;
+        }
+      }
+      ent = cand + a.ccap;
+      if (!ovf) {
+        const uint64_t* wb = cand + (size_t)wv * kWaveCap;
+        for (int i = lane; i < wn; i += kWave) ent[off + i] = wb[i];
+      }
+      __syncthreads();
+    }
+    if (!ovf && npatch > 0) {
+      // patched values >= tau_all join the candidates
+      if (tid == 0) s_cnt = N;
+      __syncthreads();
+      for (int p = tid; p < npatch; p += NT) {
+        const uint32_t kp = f2key(pfin[p]);
+        if (kp >= tau_all) {
+          const int i = atomicAdd(&s_cnt, 1);
+          if (i < a.ccap) ent[i] = ((uint64_t)kp << 32) | (uint32_t)pid[p];
+        }
+      }
+      __syncthreads();
+      N = s_cnt;
+      if (N > a.ccap) ovf = true;  // uniform
+      __syncthreads();
+      if (tid == 0) s_cnt = 0;
+    }
+  } else {
+    // greedy: patched final values join the argmax
+    for (int p = tid; p < npatch; p += NT) argmax_merge(bv, bi, pfin[p], pid[p]);
+  }
+  // argmax (:45-49) starts from index 0: when its value is NaN nothing
+  // compares greater and the answer stays 0
+  bool nan0 = false;
+  if (greedy && lo == 0 && len > 0 && tid == 0) {
+    float x0 = src[0];
+    if (patched(0)) x0 = pfin[wpre[0] + 0];
+    nan0 = x0 != x0;
+  }
+
+  // ---- slice argmax (first index on ties) ----
+  wave_argmax(bv, bi);
+  if (lane == 0) {
+    s_rv[wv] = bv;
+    s_ri[wv] = bi;
+  }
+  __syncthreads();
+  float rv = s_rv[0];
+  int ri = s_ri[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) argmax_merge(rv, ri, s_rv[w], s_ri[w]);
+
+  if (a.S > 1) {
+    // ---- publish this slice; the last one to arrive completes the row ----
+    const int64_t part = (int64_t)row * a.S + sl;
+    uint64_t* pdst = a.part_cand + part * a.pc;
+    int nout = 0;
+    int flags = (ovf ? kSliceOverflow : 0) | (nan0 ? kSliceNan0 : 0);
+    if (topk && !ovf) {
+      if (N > a.pc) {
+        const SelectResult r = block_select<NT>(
+            [&](auto fn) {
+              for (int i0 = 0; i0 < N; i0 += NT) {
+                const int i = i0 + tid;
+                const bool in = i < N;
+                fn(in ? (uint32_t)(ent[i] >> 32) : 0u, in);
+              }
+            },
+            k, a.pc, shist, smem);
+        if (r.ge > a.pc) {
+          flags = kSliceOverflow;
+        } else {
+          int mine = 0;
+          for (int i = tid; i < N; i += NT) mine += ((uint32_t)(ent[i] >> 32) >= r.tau);
+          int tot;
+          int pos = block_excl_scan<NT>(mine, smem, tot);
+          for (int i = tid; i < N; i += NT)
+            if ((uint32_t)(ent[i] >> 32) >= r.tau) store_agent(&pdst[pos++], ent[i]);
+          nout = tot;
+        }
+      } else {
+        for (int i = tid; i < N; i += NT) store_agent(&pdst[i], ent[i]);
+        nout = N;
+      }
+    }
+    if (tid == 0) {
+      store_agent(&a.part_info[part].n, nout);
+      store_agent(&a.part_info[part].flags, flags);
+      store_agent(&a.part_info[part].amax, ri);
+      store_agent(&a.part_info[part].vmax, __float_as_int(rv));
+    }
+    // The slice data above is written with agent-scope stores, which go to
+    // the device's point of coherence; waiting for their completion before
+    // the arrival count is bumped orders them without an L2 writeback.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+      s_last = (__hip_atomic_fetch_add(&a.arrive[row], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1));
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) __hip_atomic_store(&a.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // slice records: one per thread, then every thread reads them from LDS.
+    // s_off borrows the select histogram (free here; 5 * kMaxSlices words < kSelWords).
+    int* s_off = reinterpret_cast<int*>(shist);
+    static_assert(5 * kMaxSlices <= kSelWords, "slice records must fit the histogram");
+    if (tid < a.S) {
+      const SliceInfo* in = a.part_info + (int64_t)row * a.S + tid;
+      const int nj = load_agent(&in->n);
+      const int fl = load_agent(&in->flags);
+      s_off[kMaxSlices + tid] = (nj < 0 || nj > a.pc) ? -1 : nj;  // never trust a count past the buffer
+      s_off[2 * kMaxSlices + tid] = fl;
+      s_off[3 * kMaxSlices + tid] = load_agent(&in->amax);
+      s_off[4 * kMaxSlices + tid] = load_agent(&in->vmax);
+    }
+    __syncthreads();
+    int any = 0;
+    N = 0;
+    rv = -__builtin_inff();
+    ri = 0x7fffffff;
+    for (int j = 0; j < a.S; ++j) {
+      const int nj = s_off[kMaxSlices + j];
+      any |= s_off[2 * kMaxSlices + j] | (nj < 0 ? kSliceOverflow : 0);
+      nan0 = nan0 || (s_off[2 * kMaxSlices + j] & kSliceNan0);
+      argmax_merge(rv, ri, __int_as_float(s_off[4 * kMaxSlices + j]), s_off[3 * kMaxSlices + j]);
+      s_off[j] = N;  // start of slice j in the merged buffer
+      if (nj > 0) N += nj;
+    }
+    ovf = (any & kSliceOverflow) != 0;
+    if (topk && !ovf) {
+      ent = cand;  // both ping-pong buffers: 2 * ccap >= S * pc entries
+      constexpr int MR = 8;  // loads in flight per thread
+      for (int b0 = 0; b0 < N; b0 += NT * MR) {
+        uint64_t xv[MR];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          const int i = b0 + r * NT + tid;
+          xv[r] = 0ull;
+          if (i < N) {
+            int j = 0;
+            while (j + 1 < a.S && s_off[j + 1] <= i) ++j;
+            xv[r] = load_agent(a.part_cand + ((int64_t)row * a.S + j) * a.pc + (i - s_off[j]));
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          const int i = b0 + r * NT + tid;
+          if (i < N) ent[i] = xv[r];
+        }
+      }
+    }
+    __syncthreads();
+    for (int q = tid; q < 5 * kMaxSlices; q += NT) s_off[q] = 0;  // restore the zeroed histogram
+    __syncthreads();
+  }
+  if (ovf) {
+    if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
+    return;
+  }
+  if (!topk) {
+    if (tid == 0) {
+      a.out[row] = nan0 ? 0 : ri;
+      if (a.dbg.n) a.dbg.n[row] = 0;
+      if (a.dbg.ncand) a.dbg.ncand[row] = 0;
+      if (a.dbg.total) a.dbg.total[row] = 0.0f;
+      if (a.dbg.path) a.dbg.path[row] = 1;
+    }
+    return;
+  }
+  // ---- the row's heap-path members, then the reference's tail ----
+  uint64_t* mem = reinterpret_cast<uint64_t*>(regA);
+  if (!topk_members<NT>(ent, N, k, mem, a.mcap, shist, smem, &s_cnt)) {
+    if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
+    return;
+  }
+  if (k <= kWave) {
+    if (wv != 0) return;
+    double u = 0.0;
+    if (lane == 0) u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
+    wave_tail(mem, k, P, u, row, a.out, a.dbg);
+    return;
+  }
+  // k > 64: block-wide sort of the members, then the block tail
+  float* vals = reinterpret_cast<float*>(mem + a.mcap);
+  int32_t* ids = reinterpret_cast<int32_t*>(vals + a.kcap);
+  float* ebuf = reinterpret_cast<float*>(ids + a.kcap);
+  const int kpow = next_pow2(k);
+  for (int i = k + tid; i < kpow; i += NT) mem[i] = 0ull;
+  __syncthreads();
+  bitonic_sort_u64<NT>(mem, kpow, true);
+  for (int i = tid; i < k; i += NT) {
+    vals[i] = key2f((uint32_t)(mem[i] >> 32));
+    ids[i] = (int32_t)(uint32_t)mem[i];
+  }
+  if (tid == 0) s_u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
+  __syncthreads();
+  const TailOut to = softmax_cutoff_draw<NT>(vals, ids, ebuf, k, P, s_u, smem);
+  if (tid == 0) a.out[row] = to.id;
+  write_debug<NT>(a.dbg, row, 2, to.n, k, to.total, ids, ebuf);
+}
+
+// ---------------------------------------------------------------------------
+// 2. generic_kernel: whole-row stable radix sort, then the reference's tail
 // ---------------------------------------------------------------------------
 // Scratch per workgroup: keysA, idxA, keysB, idxB (uint32 each, vpad) and
 // f32 work (vpad).  Keys are ~f2key(value): an ascending stable sort gives
@@ -644,7 +1144,7 @@ __global__ __launch_bounds__(NT) void merge_kernel(
 constexpr int kGenIPT = 8;
 
 template <int NT>
-__device__ void radix_sort_pass(const uint32_t* __restrict__ kin, const uint32_t* __restrict__ iin,
+__device__ __forceinline__ void radix_sort_pass(const uint32_t* __restrict__ kin, const uint32_t* __restrict__ iin,
                                 uint32_t* __restrict__ kout, uint32_t* __restrict__ iout, int n,
                                 int shift, uint32_t* wcnt /*[NT/64][256]*/,
                                 uint32_t* dbase /*[256]*/, uint32_t* drun /*[256]*/) {
@@ -745,45 +1245,98 @@ __device__ __forceinline__ int upper_bound_u32(const uint32_t* a, int n, uint32_
   return l;
 }
 
+
 template <int NT>
-__global__ __launch_bounds__(NT) void generic_kernel(
-    const float* __restrict__ logits, int64_t V, const RowParams* __restrict__ rp,
-    const Patch* __restrict__ patches, const int32_t* __restrict__ patch_cnt, int pcap,
-    const int32_t* __restrict__ generic_list, const int32_t* __restrict__ generic_count,
-    const float* __restrict__ row_max, const double* __restrict__ d_u, uint64_t* __restrict__ rng,
-    int32_t* __restrict__ out, uint32_t* __restrict__ scratch, int64_t vpad, DebugPtrs dbg) {
+__global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
   constexpr int NW = NT / kWave;
   __shared__ uint32_t wcnt[NW * 256];
   __shared__ uint32_t dbase[256];
   __shared__ uint32_t drun[256];
-  __shared__ int smem[NT / kWave + 4];
+  __shared__ int smem[NW + 4];
   __shared__ double s_u;
-  __shared__ float s_f;
   __shared__ int s_i[4];
-  const int n = (int)V;
-  uint32_t* kA = scratch + (int64_t)blockIdx.x * vpad * 5;
-  uint32_t* iA = kA + vpad;
-  uint32_t* kB = iA + vpad;
-  uint32_t* iB = kB + vpad;
-  float* work = reinterpret_cast<float*>(iB + vpad);
-  const int count = *generic_count;
-  const int lane = lane_id();
-  (void)row_max;
+  __shared__ float s_rv[NW];
+  __shared__ int s_ri[NW];
+  const int n = (int)a.V;
+  const int tid = threadIdx.x;
+  uint32_t* kA = a.scratch + (int64_t)blockIdx.x * a.vpad * 5;
+  uint32_t* iA = kA + a.vpad;
+  uint32_t* kB = iA + a.vpad;
+  uint32_t* iB = kB + a.vpad;
+  float* work = reinterpret_cast<float*>(iB + a.vpad);
+  if (blockIdx.x == 0 && tid == 0) *a.next_count = 0;
+  const int count = *a.generic_count;
   for (int li = blockIdx.x; li < count; li += gridDim.x) {
-    const int row = generic_list[li];
-    const RowParams P = rp[row];
-    const float* __restrict__ src = logits + (int64_t)row * V;
-    // final values -> keys (patches applied over the plain pass)
-    for (int i = threadIdx.x; i < n; i += NT) {
-      kA[i] = ~f2key(src[i] * P.invT);
-      iA[i] = (uint32_t)i;
+    const int row = a.generic_list[li];
+    const RowParams P = a.rp[row];
+    const float* __restrict__ src = a.logits + (int64_t)row * a.V;
+    // window counts (kB) and bias slots + 1 (iB) per id (:64-76)
+    for (int i = tid; i < n; i += NT) {
+      kB[i] = 0u;
+      iB[i] = 0u;
     }
     __syncthreads();
-    const int pn = patch_cnt[row];
-    const Patch* pl = patches + (int64_t)row * pcap;
-    for (int q = threadIdx.x; q < pn; q += NT) {
-      const Patch p = pl[q];
-      kA[p.id] = ~f2key(apply_patch(src[p.id], p, P) * P.invT);
+    const int64_t hlen = a.hist_len[row];
+    int n_hist = 0;
+    if (P.pen_active && hlen > 0)
+      n_hist = (int)((P.repeat_last_n > 0 && P.repeat_last_n < hlen) ? P.repeat_last_n : hlen);
+    if (n_hist > 0) {
+      const int hbase = (int)((hlen - n_hist) % a.hcap);
+      const int32_t* __restrict__ hrow = a.hist + (int64_t)row * a.hcap;
+      for (int i = tid; i < n_hist; i += NT) {
+        int slot = hbase + i;
+        if (slot >= a.hcap) slot -= a.hcap;
+        const int id = hrow[slot];
+        if (id >= 0 && id < n) atomicAdd(&kB[id], 1u);
+      }
+    }
+    for (int j = tid; j < P.bias_cnt; j += NT) iB[a.bias_ids[P.bias_off + j]] = (uint32_t)j + 1u;
+    __syncthreads();
+    const bool greedy = P.mode == kModeGreedy;
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    for (int i = tid; i < n; i += NT) {
+      float v = src[i];
+      const uint32_t c = kB[i];
+      if (c) {
+        if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
+        v = v - (float)((double)c * P.freq + P.pres);
+      }
+      const uint32_t bj = iB[i];
+      if (bj) v = v + a.bias_vals[P.bias_off + (int)bj - 1];
+      if (greedy) {
+        argmax_merge(bv, bi, v, i);
+      } else {
+        kA[i] = ~f2key(v * P.invT);
+        iA[i] = (uint32_t)i;
+      }
+    }
+    if (greedy) {
+      wave_argmax(bv, bi);
+      if (lane_id() == 0) {
+        s_rv[tid >> 6] = bv;
+        s_ri[tid >> 6] = bi;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        float rv = s_rv[0];
+        int ri = s_ri[0];
+        for (int w = 1; w < NW; ++w) argmax_merge(rv, ri, s_rv[w], s_ri[w]);
+        // argmax (:45-49) starts at index 0 and NaN compares greater than nothing
+        float x0 = src[0];
+        if (kB[0]) {
+          if (P.rp_active) x0 = (x0 > 0.0f) ? (x0 / P.rp32) : (x0 * P.rp32);
+          x0 = x0 - (float)((double)kB[0] * P.freq + P.pres);
+        }
+        if (iB[0]) x0 = x0 + a.bias_vals[P.bias_off + (int)iB[0] - 1];
+        a.out[row] = (x0 != x0) ? 0 : ri;
+        if (a.dbg.n) a.dbg.n[row] = 0;
+        if (a.dbg.ncand) a.dbg.ncand[row] = 0;
+        if (a.dbg.total) a.dbg.total[row] = 0.0f;
+        if (a.dbg.path) a.dbg.path[row] = 1;
+      }
+      __syncthreads();
+      continue;
     }
     __syncthreads();
     radix_sort_pass<NT>(kA, iA, kB, iB, n, 0, wcnt, dbase, drun);
@@ -791,21 +1344,20 @@ __global__ __launch_bounds__(NT) void generic_kernel(
     radix_sort_pass<NT>(kA, iA, kB, iB, n, 16, wcnt, dbase, drun);
     radix_sort_pass<NT>(kB, iB, kA, iA, n, 24, wcnt, dbase, drun);
     // kA: ~key ascending (value descending, index ascending on ties)
-    if (threadIdx.x == 0) s_u = row_uniform(d_u, rng, row);
+    if (tid == 0) s_u = row_uniform(a.d_u, a.rng, row);
     __syncthreads();
     if (P.mode == kModeFull) {
-      // candidates = the whole sorted row; values into work, ids stay in iA
-      for (int i = threadIdx.x; i < n; i += NT) work[i] = key2f(~kA[i]);
+      // candidates = the whole sorted row (:96-97); values into work, ids stay in iA
+      for (int i = tid; i < n; i += NT) work[i] = key2f(~kA[i]);
       __syncthreads();
-      // reuse kB as the exp buffer
       const TailOut t = softmax_cutoff_draw<NT>(work, iA, reinterpret_cast<float*>(kB), n, P, s_u,
                                                 smem);
-      if (threadIdx.x == 0) out[row] = t.id;
-      write_debug<NT>(dbg, row, 4, t.n, n, t.total, iA, reinterpret_cast<float*>(kB));
+      if (tid == 0) a.out[row] = t.id;
+      write_debug<NT>(a.dbg, row, 4, t.n, n, t.total, iA, reinterpret_cast<float*>(kB));
       __syncthreads();
       continue;
     }
-    // ---- top-k row (k < V) by the heap rule ----
+    // ---- top-k row (k < V) by the heap rule (:85-95) ----
     const int k = P.k;
     const uint32_t Tn = kA[k - 1];  // ~key of the k-th largest
     const int g = lower_bound_u32(kA, n, Tn);
@@ -820,23 +1372,23 @@ __global__ __launch_bounds__(NT) void generic_kernel(
       // indices ascending (in kB), then merge-walk with the ties (iA[g..tend)).
       const int gp = next_pow2(g > 0 ? g : 1);
       uint64_t* gs = reinterpret_cast<uint64_t*>(kB);  // spans kB+iB
-      for (int i = threadIdx.x; i < gp; i += NT) gs[i] = (i < g) ? (uint64_t)iA[i] : ~0ull;
+      for (int i = tid; i < gp; i += NT) gs[i] = (i < g) ? (uint64_t)iA[i] : ~0ull;
       __syncthreads();
       bitonic_sort_u64<NT>(gs, gp, false);
-      if (threadIdx.x == 0) {
-        int a = 0, b = 0;  // a over G, b over ties
+      if (tid == 0) {
+        int x = 0, y = 0;  // x over G, y over ties
         int taken = 0;
         while (taken < k) {
-          const uint64_t gi = (a < g) ? gs[a] : ~0ull;
-          const uint64_t ti = (g + b < tend) ? (uint64_t)iA[g + b] : ~0ull;
+          const uint64_t gi = (x < g) ? gs[x] : ~0ull;
+          const uint64_t ti = (g + y < tend) ? (uint64_t)iA[g + y] : ~0ull;
           if (gi < ti)
-            ++a;
+            ++x;
           else
-            ++b;
+            ++y;
           ++taken;
         }
-        s_i[0] = g + b - m;  // the last m ties taken
-        s_i[1] = g + b;
+        s_i[0] = g + y - m;  // the last m ties taken
+        s_i[1] = g + y;
       }
       __syncthreads();
       take_lo = s_i[0];
@@ -845,15 +1397,15 @@ __global__ __launch_bounds__(NT) void generic_kernel(
     }
     // reference order: value descending, index descending on ties.  Reverse
     // every run of equal values among G; the selected ties come last, reversed.
-    for (int i = threadIdx.x; i < g; i += NT) {
+    for (int i = tid; i < g; i += NT) {
       const uint32_t key = kA[i];
-      const int a = lower_bound_u32(kA, g, key);
-      const int b = upper_bound_u32(kA, g, key);
-      const int o = a + (b - 1 - i);
+      const int x = lower_bound_u32(kA, g, key);
+      const int y = upper_bound_u32(kA, g, key);
+      const int o = x + (y - 1 - i);
       work[o] = key2f(~key);
       reinterpret_cast<int32_t*>(kB)[o] = (int32_t)iA[i];
     }
-    for (int i = take_lo + threadIdx.x; i < take_hi; i += NT) {
+    for (int i = take_lo + tid; i < take_hi; i += NT) {
       const int o = g + (take_hi - 1 - i);
       work[o] = key2f(~kA[i]);
       reinterpret_cast<int32_t*>(kB)[o] = (int32_t)iA[i];
@@ -861,12 +1413,10 @@ __global__ __launch_bounds__(NT) void generic_kernel(
     __syncthreads();
     const TailOut t = softmax_cutoff_draw<NT>(work, reinterpret_cast<int32_t*>(kB),
                                               reinterpret_cast<float*>(iB), k, P, s_u, smem);
-    if (threadIdx.x == 0) out[row] = t.id;
-    write_debug<NT>(dbg, row, 4, t.n, k, t.total, reinterpret_cast<int32_t*>(kB),
+    if (tid == 0) a.out[row] = t.id;
+    write_debug<NT>(a.dbg, row, 4, t.n, k, t.total, reinterpret_cast<int32_t*>(kB),
                     reinterpret_cast<float*>(iB));
     __syncthreads();
-    (void)lane;
-    (void)s_f;
   }
 }
 
@@ -909,46 +1459,37 @@ __global__ void expf_kernel(const float* __restrict__ x, float* __restrict__ y, 
 // ---------------------------------------------------------------------------
 // launchers (called from nls_api.cpp)
 // ---------------------------------------------------------------------------
-
-
-template <int Q, bool VEC>
-static hipError_t launch_chunk(const LaunchArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((chunk_kernel<kChunkVec4, Q, VEC>), dim3(a.B * a.nchunks),
-                     dim3(kChunkThreads), 0, s, a.logits, a.V, a.nchunks, a.rp, a.patches,
-                     a.patch_cnt, a.pcap, a.stats, a.cand, a.ccap);
+template <int NT, bool VEC, int Q, bool WAVE>
+static hipError_t launch_stream_t(const StreamArgs& a, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((stream_kernel<NT, VEC, Q, WAVE>), dim3(a.B * a.S), dim3(NT), lds, s, a);
   return hipGetLastError();
 }
 
-hipError_t launch_sample(const LaunchArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(prep_kernel, dim3(a.B), dim3(256), 0, s, a.rp, a.V, a.hist, a.hist_len,
-                     a.hcap, a.bias_ids, a.bias_vals, a.patches, a.patch_cnt, a.pcap,
-                     a.prep_scratch, a.prep_stride, a.generic_count);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const int q = a.qmax <= 1 ? 1 : a.qmax <= 2 ? 2 : a.qmax <= 4 ? 4 : 8;
-  if (a.ev_start && (e = hipEventRecord(a.ev_start, s)) != hipSuccess) return e;
-  if (a.vec4) {
-    if (q == 1) e = launch_chunk<1, true>(a, s);
-    else if (q == 2) e = launch_chunk<2, true>(a, s);
-    else if (q == 4) e = launch_chunk<4, true>(a, s);
-    else e = launch_chunk<8, true>(a, s);
-  } else {
-    if (q == 1) e = launch_chunk<1, false>(a, s);
-    else if (q == 2) e = launch_chunk<2, false>(a, s);
-    else if (q == 4) e = launch_chunk<4, false>(a, s);
-    else e = launch_chunk<8, false>(a, s);
+template <int NT, bool VEC>
+static hipError_t launch_stream_q(const StreamArgs& a, const LaunchPlan& p, hipStream_t s) {
+  if (p.wave) return launch_stream_t<NT, VEC, 1, true>(a, p.lds, s);
+  switch (p.q) {
+    case 1: return launch_stream_t<NT, VEC, 1, false>(a, p.lds, s);
+    case 2: return launch_stream_t<NT, VEC, 2, false>(a, p.lds, s);
+    case 4: return launch_stream_t<NT, VEC, 4, false>(a, p.lds, s);
+    default: return launch_stream_t<NT, VEC, 8, false>(a, p.lds, s);
   }
-  if (e != hipSuccess) return e;
-  if (a.ev_stop && (e = hipEventRecord(a.ev_stop, s)) != hipSuccess) return e;
-  hipLaunchKernelGGL(merge_kernel<kMergeThreads>, dim3(a.B), dim3(kMergeThreads), a.merge_lds, s,
-                     a.rp, a.nchunks, a.stats, a.cand, a.ccap, a.mcap, a.d_u, a.rng, a.out,
-                     a.row_max, a.generic_list, a.generic_count, a.dbg);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(generic_kernel<kGenericThreads>, dim3(a.gen_blocks), dim3(kGenericThreads),
-                     0, s, a.logits, a.V, a.rp, a.patches, a.patch_cnt, a.pcap, a.generic_list,
-                     a.generic_count, a.row_max, a.d_u, a.rng, a.out, a.gen_scratch, a.gen_vpad,
-                     a.dbg);
+}
+
+static hipError_t launch_stream(const StreamArgs& a, const LaunchPlan& p, hipStream_t s) {
+  if (p.nt == 1024)
+    return p.vec4 ? launch_stream_q<1024, true>(a, p, s) : launch_stream_q<1024, false>(a, p, s);
+  return p.vec4 ? launch_stream_q<256, true>(a, p, s) : launch_stream_q<256, false>(a, p, s);
+}
+
+hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const LaunchPlan& lp,
+                         hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  hipError_t e;
+  if (ev_start && (e = hipEventRecord(ev_start, s)) != hipSuccess) return e;
+  if ((e = launch_stream(sa, lp, s)) != hipSuccess) return e;
+  if (ev_stop && (e = hipEventRecord(ev_stop, s)) != hipSuccess) return e;
+  hipLaunchKernelGGL(generic_kernel<kGenericThreads>, dim3(lp.gen_blocks), dim3(kGenericThreads),
+                     0, s, ga);
   return hipGetLastError();
 }
 
@@ -966,9 +1507,30 @@ hipError_t launch_accept_device(const int32_t* d_ids, int B, int64_t V, int32_t*
   return hipGetLastError();
 }
 
+size_t max_dynamic_lds() { return 143 * 1024; }  // 160 KB of LDS less the largest static part
+
+template <int NT, bool VEC, int Q, bool WAVE>
+static hipError_t set_attr_one() {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(&stream_kernel<NT, VEC, Q, WAVE>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_dynamic_lds());
+}
+
+template <int NT, bool VEC>
+static hipError_t set_attr_q() {
+  hipError_t e;
+  if ((e = set_attr_one<NT, VEC, 1, true>()) != hipSuccess) return e;
+  if ((e = set_attr_one<NT, VEC, 1, false>()) != hipSuccess) return e;
+  if ((e = set_attr_one<NT, VEC, 2, false>()) != hipSuccess) return e;
+  if ((e = set_attr_one<NT, VEC, 4, false>()) != hipSuccess) return e;
+  return set_attr_one<NT, VEC, 8, false>();
+}
+
 hipError_t set_kernel_attributes() {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(&merge_kernel<kMergeThreads>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 8192);
+  hipError_t e;
+  if ((e = set_attr_q<256, true>()) != hipSuccess) return e;
+  if ((e = set_attr_q<256, false>()) != hipSuccess) return e;
+  if ((e = set_attr_q<1024, true>()) != hipSuccess) return e;
+  return set_attr_q<1024, false>();
 }
 
 hipError_t launch_expf(const float* x, float* y, int64_t n, hipStream_t s) {
