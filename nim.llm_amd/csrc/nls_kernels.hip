@@ -302,26 +302,24 @@ __device__ __forceinline__ float lane_fc(float x, int l) {
 }
 
 // The reference's tail on one wave, for k <= 64 members (mem[0..k), any
-// order): lane i holds candidate i after a descending (value, index) bitonic
+// order): lane i holds candidate i after a descending (value, index) rank
 // sort (sampler.nim:88-95), then softmax (:98-100, :51-57), top-p (:103-108),
 // min-p (:110-114) and the draw (:115-121).  Every sequential fp32 sum runs
 // in candidate order as an unrolled chain; the top-p running sum doubles as
 // `total`, which the reference accumulates with the same operations.
-__device__ __forceinline__ void wave_tail(const uint64_t* mem, int k, const RowParams& P,
+__device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams& P,
                                           double u_lane0, int row, int32_t* out,
                                           const DebugPtrs& dbg) {
   const int lane = lane_id();
+  // rank sort: each member's position is the number of members above it
+  // (entries are distinct (key, id) pairs; the zero padding ranks last)
   uint64_t x = (lane < k) ? mem[lane] : 0ull;
-#pragma unroll
-  for (int size = 2; size <= kWave; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const uint32_t ylo = (uint32_t)__shfl_xor((int)(uint32_t)x, stride, kWave);
-      const uint32_t yhi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), stride, kWave);
-      const uint64_t y = ((uint64_t)yhi << 32) | ylo;
-      const bool keep_max = ((lane & stride) == 0) == ((lane & size) == 0);
-      x = keep_max ? (x > y ? x : y) : (x < y ? x : y);
-    }
+  {
+    int rank = 0;
+#pragma unroll 8
+    for (int j = 0; j < k; ++j) rank += (mem[j] > x);  // one LDS broadcast per step
+    if (lane < k) mem[rank] = x;  // the whole wave has read mem[] above
+    x = (lane < k) ? mem[lane] : 0ull;
   }
   const bool valid = lane < k;
   const int id = (int)(uint32_t)x;
@@ -439,9 +437,7 @@ void stream_kernel(const StreamArgs a) {
   const int len = (int)min((int64_t)a.L, a.V - (int64_t)lo);
   const float* __restrict__ src = a.logits + (int64_t)row * a.V + lo;
   const int ntiles = (len + TE - 1) / TE;
-  // the first tile is in flight while the patch table is built
-  f32x4 R[NV4];
-  load_tile<NT, NV4, VEC>(R, src, 0, len);
+  f32x4 R0[NV4];
 
   uint64_t* cand = reinterpret_cast<uint64_t*>(lds);
   unsigned char* regA = lds + a.offA;
@@ -495,50 +491,45 @@ void stream_kernel(const StreamArgs a) {
     };
     const bool one_round = n_hist <= NT * HPT;
     int hl[HPT];
-    float hraw[HPT];
     if (one_round) {
 #pragma unroll
       for (int h = 0; h < HPT; ++h) {
         const int i = h * NT + tid;
         hl[h] = (i < n_hist) ? hist_loc(i) : -1;
       }
-#pragma unroll
-      for (int h = 0; h < HPT; ++h) hraw[h] = hl[h] >= 0 ? src[hl[h]] : 0.0f;
     }
-    // fn(loc, raw) for every window entry of the slice (loc < 0: not in it)
+    // fn(loc) for every window entry of the slice (loc < 0: not in it)
     auto for_window = [&](auto fn) __attribute__((always_inline)) {
       if (one_round) {
 #pragma unroll
-        for (int h = 0; h < HPT; ++h) fn(hl[h], hraw[h]);
+        for (int h = 0; h < HPT; ++h) fn(hl[h]);
       } else {
         for (int b0 = 0; b0 < n_hist; b0 += NT * HPT) {
           int l[HPT];
-          float r[HPT];
 #pragma unroll
           for (int h = 0; h < HPT; ++h) {
             const int i = b0 + h * NT + tid;
             l[h] = (i < n_hist) ? hist_loc(i) : -1;
           }
 #pragma unroll
-          for (int h = 0; h < HPT; ++h) r[h] = l[h] >= 0 ? src[l[h]] : 0.0f;
-#pragma unroll
-          for (int h = 0; h < HPT; ++h) fn(l[h], r[h]);
+          for (int h = 0; h < HPT; ++h) fn(l[h]);
         }
       }
     };
     // bias entries of this thread (one round trip when bias_cnt <= NT)
     const bool bias_one = P.bias_cnt <= NT;
     int b_loc = -1;
-    float b_val = 0.0f, b_raw = 0.0f;
+    float b_val = 0.0f;
     if (bias_one && tid < P.bias_cnt) {
       const int loc = a.bias_ids[P.bias_off + tid] - lo;
       b_val = a.bias_vals[P.bias_off + tid];
       b_loc = (loc >= 0 && loc < len) ? loc : -1;
-      if (b_loc >= 0) b_raw = src[b_loc];
     }
+    // the first tile follows the window and bias reads into the memory queues
+    load_tile<NT, NV4, VEC>(R0, src, 0, len);
     for (int w = tid; w < nw; w += NT) bitmap[w] = 0u;
     __syncthreads();
-    for_window([&](int loc, float) {
+    for_window([&](int loc) {
       if (loc >= 0) atomicOr(&bitmap[loc >> 5], 1u << (loc & 31));
     });
     if (bias_one) {
@@ -571,46 +562,31 @@ void stream_kernel(const StreamArgs a) {
         const int w = loc >> 5;
         return wpre[w] + __popc(bitmap[w] & ((1u << (loc & 31)) - 1u));
       };
-      // every writer of pfin[p] / pid[p] stores the same value
-      for_window([&](int loc, float raw) {
+      // every writer of pid[p] stores the same value
+      for_window([&](int loc) {
         if (loc >= 0) {
           const int p = pidx(loc);
           atomicAdd(&pflag[p], 4u);
-          pfin[p] = raw;
           pid[p] = lo + loc;
         }
       });
-      auto put_bias = [&](int loc, float val, float raw) {
+      auto put_bias = [&](int loc, float val) {
         const int p = pidx(loc);
         pbias[p] = val;  // bias ids are unique per row
         atomicOr(&pflag[p], (uint32_t)kPatchBias);
-        pfin[p] = raw;
         pid[p] = lo + loc;
       };
       if (bias_one) {
-        if (b_loc >= 0) put_bias(b_loc, b_val, b_raw);
+        if (b_loc >= 0) put_bias(b_loc, b_val);
       } else {
         for (int j = tid; j < P.bias_cnt; j += NT) {
           const int loc = a.bias_ids[P.bias_off + j] - lo;
-          if (loc >= 0 && loc < len) put_bias(loc, a.bias_vals[P.bias_off + j], src[loc]);
+          if (loc >= 0 && loc < len) put_bias(loc, a.bias_vals[P.bias_off + j]);
         }
-      }
-      __syncthreads();
-      // final values: penalties then bias on the original logit (:71-76),
-      // then temperature (:80-81) on the sampling rows
-      for (int p = tid; p < npatch; p += NT) {
-        const uint32_t fl = pflag[p];
-        const uint32_t cnt = fl >> 2;
-        float v = pfin[p];
-        if (cnt) {
-          if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
-          v = v - (float)((double)cnt * P.freq + P.pres);  // float64, one rounding (:74)
-        }
-        if (fl & kPatchBias) v = v + pbias[p];
-        if (!greedy) v = v * P.invT;
-        pfin[p] = v;
       }
     }
+  } else {
+    load_tile<NT, NV4, VEC>(R0, src, 0, len);
   }
   __syncthreads();
   auto patched = [&](int loc) -> bool {  // loc: slice-local offset
@@ -682,7 +658,9 @@ void stream_kernel(const StreamArgs a) {
             has = true;
           }
         }
-        if (block_sum<NT>(has ? 1 : 0, smem) >= k) {
+        // a thread lacks `has` only when its NE values are all patched
+        const bool surely = full && npatch <= NE * (NT - k);
+        if ((surely ? NT : block_sum<NT>(has ? 1 : 0, smem)) >= k) {
           wtau = block_select<NT>([&](auto fn) { fn(tmax, has); }, k, -1, shist, smem).tau;
           __syncthreads();  // the select's histogram overlaps the per-wave ones
         }
@@ -896,20 +874,42 @@ void stream_kernel(const StreamArgs a) {
     }
   };
 
-  if (!ovf) {
-    for (int t = 0; t < ntiles; ++t) {
-      if (t > 0) load_tile<NT, NV4, VEC>(R, src, t * TE, len);
-      float v[NE];
+  auto unpack = [&](float (&v)[NE], const f32x4 (&R)[NV4]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int j = 0; j < NV4; ++j) {
-        v[4 * j + 0] = R[j].x;
-        v[4 * j + 1] = R[j].y;
-        v[4 * j + 2] = R[j].z;
-        v[4 * j + 3] = R[j].w;
-      }
-      process(v, t);
-      if (ovf || wovf) break;  // ovf is block-uniform; wovf is set only on the wave path
+    for (int j = 0; j < NV4; ++j) {
+      v[4 * j + 0] = R[j].x;
+      v[4 * j + 1] = R[j].y;
+      v[4 * j + 2] = R[j].z;
+      v[4 * j + 3] = R[j].w;
     }
+  };
+  if (!ovf) {
+    // ovf is block-uniform; wovf is set only on the wave path (no barriers there)
+    for (int t = 0; t < ntiles; ++t) {
+      float v[NE];
+      if (t > 0) load_tile<NT, NV4, VEC>(R0, src, t * TE, len);
+      unpack(v, R0);
+      process(v, t);
+      if (ovf || wovf) break;
+    }
+  }
+  // the patched ids' original logits (read back after the stream, likely from
+  // cache) and their final values: penalties then bias (:71-76), then
+  // temperature (:80-81) on the sampling rows
+  if (!ovf && npatch > 0) {
+    for (int p = tid; p < npatch; p += NT) {
+      const uint32_t fl = pflag[p];
+      const uint32_t cnt = fl >> 2;
+      float v = src[pid[p] - lo];
+      if (cnt) {
+        if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
+        v = v - (float)((double)cnt * P.freq + P.pres);  // float64, one rounding (:74)
+      }
+      if (fl & kPatchBias) v = v + pbias[p];
+      if (!greedy) v = v * P.invT;
+      pfin[p] = v;
+    }
+    __syncthreads();
   }
 
   // ---- the slice's candidates: stream buffer(s) + patched values ----
