@@ -96,6 +96,9 @@ def main():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--copy-ref", action="store_true",
+                    help="also run a plain 256 MiB device copy three times (the reference "
+                         "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (rows shard across GPUs with no "
@@ -200,6 +203,16 @@ def main():
         "parity_spot_check": {"rows": int(len(chk)), "bit_exact": parity_ok},
     }
     s.close()
+    if args.copy_ref:
+        n = 64 * 1024 * 1024  # 64 Mi floats = 256 MiB read and 256 MiB written per copy
+        a = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        res["copy_ref_bytes"] = n * 4
+        del a, b
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, args.cpu_budget)
     else:
