@@ -394,7 +394,9 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
     kfast = kfast * 7 / 8;
     g = plan_geometry(B, vocab, kfast, ncu);
   }
-  const bool stream_ok = g.lds <= max_dynamic_lds() && g.pcap >= 1;  // false only for vocabularies far beyond 2^19
+  // (false only for vocabularies far beyond 2^19; the slice's byte size must
+  // also fit the 32-bit range of the kernel's buffer loads)
+  const bool stream_ok = g.lds <= max_dynamic_lds() && g.pcap >= 1 && g.L < (1 << 28);
   if (!stream_ok) g.lds = 0;                    // every row then goes to the whole-row kernel
   bool any_full = false;
   for (int b = 0; b < B; ++b) {
@@ -416,7 +418,9 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   s->plan.q = g.q;
   s->plan.wave = g.wave;
   s->plan.lds = g.lds;
-  s->plan.gen_blocks = any_full ? std::min(B, 256) : std::min(B, 8);
+  // Without full-sort rows the whole-row kernel only serves the rare row the
+  // streaming kernel hands on: one workgroup keeps that launch cheap.
+  s->plan.gen_blocks = any_full ? std::min(B, 256) : 1;
 
   int rc = NLS_OK;
   auto fail = [&](int code) {

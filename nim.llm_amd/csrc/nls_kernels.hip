@@ -39,25 +39,45 @@ __device__ __forceinline__ float apply_patch(float v, float pen, float bias, uin
   return v;
 }
 
-// Loads tile `toff` of a slice into registers: thread t owns the float4 groups
-// (j * NT + t) for j < NV4, so each wave's load covers 1 KB contiguously.
-// Elements at or beyond `len` read as 0 and are masked by the caller.
-template <int NT, int NV4, bool VEC>
-__device__ __forceinline__ void load_tile(f32x4 (&R)[NV4], const float* __restrict__ src, int toff,
-                                          int len) {
+// Reads a row-uniform value through the constant address space, which lets
+// the compiler use scalar loads: nothing in the kernel writes it.
+template <typename T>
+__device__ __forceinline__ T load_const(const T* p) {
+  static_assert(sizeof(T) % 4 == 0, "whole words");
+  typedef const __attribute__((address_space(4))) uint32_t ConstWord;
+  const ConstWord* w = (const ConstWord*)p;
+  uint32_t x[sizeof(T) / 4];
 #pragma unroll
-  for (int j = 0; j < NV4; ++j) {
-    const int o = toff + (j * NT + (int)threadIdx.x) * 4;
-    if (VEC) {
-      // VEC implies len % 4 == 0: a group is either whole or absent
-      R[j] = (o < len) ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + o))
-                       : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    } else {
-      R[j].x = (o + 0 < len) ? src[o + 0] : 0.0f;
-      R[j].y = (o + 1 < len) ? src[o + 1] : 0.0f;
-      R[j].z = (o + 2 < len) ? src[o + 2] : 0.0f;
-      R[j].w = (o + 3 < len) ? src[o + 3] : 0.0f;
-    }
+  for (size_t i = 0; i < sizeof(T) / 4; ++i) x[i] = w[i];
+  return __builtin_bit_cast(T, x);
+}
+
+// Buffer resource over a slice of `len` floats: loads at or beyond `len`
+// return 0 without touching memory, so tile loads need no per-lane branch (a
+// divergent branch around a load makes the compiler wait for it on the spot).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const float* src, int len) {
+  constexpr int kRsrcWord3 = 0x00020000;  // gfx9 untyped 32-bit buffer
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), (short)0, len * 4, kRsrcWord3);
+}
+
+// Loads float4 group j of tile `toff` of a slice: thread t owns the groups
+// (j * NT + t), so each wave's load covers 1 KB contiguously.  Elements at or
+// beyond the slice read as 0 and are masked by the caller.  Loads are
+// nontemporal: every logit is read once.
+template <int NT, bool VEC>
+__device__ __forceinline__ f32x4 load_group(__amdgpu_buffer_rsrc_t rs, int toff, int j) {
+  constexpr int kNT = 2;  // cache policy: nt
+  const int b = (toff + (j * NT + (int)threadIdx.x) * 4) * 4;
+  if (VEC) {
+    // VEC implies len % 4 == 0: a group is either whole or absent
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, b, 0, kNT));
+  } else {
+    f32x4 r;
+    r.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, b + 0, 0, kNT));
+    r.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, b + 4, 0, kNT));
+    r.z = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, b + 8, 0, kNT));
+    r.w = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, b + 12, 0, kNT));
+    return r;
   }
 }
 
@@ -405,6 +425,7 @@ void stream_kernel(const StreamArgs a) {
   __shared__ int s_wn[NW];
   __shared__ uint32_t s_wt[NW];
   __shared__ uint32_t s_tau;  // wave path: the highest published wave threshold
+  __shared__ uint32_t s_top[kWave];  // wave path: the lane maxima of tile 0
   __shared__ int s_tile_cnt[3];
   __shared__ int s_cnt;
   __shared__ float s_rv[NW];
@@ -424,8 +445,10 @@ void stream_kernel(const StreamArgs a) {
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wv = tid >> 6;
-  const RowParams P = a.rp[row];
-  const int64_t hlen = a.hist_len[row];
+  // Row constants through the scalar unit: the constant address space tells
+  // the compiler that nothing in this kernel writes them.
+  const RowParams P = load_const(a.rp + row);
+  const int64_t hlen = load_const(a.hist_len + row);
   if (P.mode == kModeFull || !P.fast) {
     if (sl == 0 && tid == 0) push_generic(a.generic_list, a.generic_count, row);
     return;
@@ -437,7 +460,12 @@ void stream_kernel(const StreamArgs a) {
   const int len = (int)min((int64_t)a.L, a.V - (int64_t)lo);
   const float* __restrict__ src = a.logits + (int64_t)row * a.V + lo;
   const int ntiles = (len + TE - 1) / TE;
-  f32x4 R0[NV4];
+  const __amdgpu_buffer_rsrc_t rs = slice_rsrc(src, len);
+  f32x4 R0[NV4];  // the tile in flight
+  auto first_tiles = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NV4; ++j) R0[j] = load_group<NT, VEC>(rs, 0, j);
+  };
 
   uint64_t* cand = reinterpret_cast<uint64_t*>(lds);
   unsigned char* regA = lds + a.offA;
@@ -448,15 +476,16 @@ void stream_kernel(const StreamArgs a) {
   uint32_t* pflag = reinterpret_cast<uint32_t*>(pbias + a.pcap);  // flags | count << 2
   int32_t* pid = reinterpret_cast<int32_t*>(pflag + a.pcap);
 
-  // the row's uniform or RNG state, read now so the tail does not wait
+  // the row's uniform or RNG state, read now (scalar loads) so the tail
+  // does not wait
   double u_in = 0.0;
   uint64_t st0 = 0ull, st1 = 0ull;
-  if (tid == 0 && !greedy) {
+  if (!greedy) {
     if (a.d_u) {
-      u_in = a.d_u[row];
+      u_in = load_const(a.d_u + row);
     } else {
-      st0 = a.rng[2 * row];
-      st1 = a.rng[2 * row + 1];
+      st0 = load_const(a.rng + 2 * row);
+      st1 = load_const(a.rng + 2 * row + 1);
     }
   }
   for (int q = tid; q < kHistWords; q += NT) shist[q] = 0u;  // the selects need it zeroed
@@ -475,29 +504,59 @@ void stream_kernel(const StreamArgs a) {
   if (P.pen_active && hlen > 0)
     n_hist = (int)((P.repeat_last_n > 0 && P.repeat_last_n < hlen) ? P.repeat_last_n : hlen);
   const bool has_patch = n_hist > 0 || P.bias_cnt > 0;
-  if (has_patch) {
-    constexpr int HPT = 8;  // window ids per thread per round trip
-    const int nw = (len + 31) >> 5;
-    const int hbase = (int)((hlen - n_hist) % a.hcap);
-    const int32_t* __restrict__ hrow = a.hist + (int64_t)row * a.hcap;
-    // slice-local offset of window entry i, or -1 when it is not in the slice
-    // (ids outside [0, V) are stored as -1 by accept)
-    auto hist_loc = [&](int i) -> int {
-      int slot = hbase + i;
-      if (slot >= a.hcap) slot -= a.hcap;
-      const int id = hrow[slot];
-      const int loc = id - lo;
-      return (id >= 0 && loc >= 0 && loc < len) ? loc : -1;
-    };
-    const bool one_round = n_hist <= NT * HPT;
-    int hl[HPT];
-    if (one_round) {
+  constexpr int HPT = 8;  // window ids per thread per round trip
+  const bool one_round = n_hist <= NT * HPT;
+  const bool bias_one = P.bias_cnt <= NT;  // one bias entry per thread at most
+  const int hbase = n_hist > 0 ? (int)((hlen - n_hist) % a.hcap) : 0;
+  const int32_t* __restrict__ hrow = a.hist + (int64_t)row * a.hcap;
+  // History slot of window entry i (the ring wraps at hcap).
+  auto hist_slot = [&](int i) -> int {
+    const int slot = hbase + i;
+    return slot >= a.hcap ? slot - a.hcap : slot;
+  };
+  // Slice-local offset of a window id, or -1 when it is not in the slice (ids
+  // outside [0, V) are stored as -1 by accept).
+  auto id_loc = [&](int id) -> int {
+    const int loc = id - lo;
+    return (id >= 0 && loc >= 0 && loc < len) ? loc : -1;
+  };
+  // The window and bias reads of the common sizes go out first, as buffer
+  // loads without per-lane branches, and the first tiles are requested once
+  // they have returned: behind the tile traffic of the other workgroups these
+  // small reads would wait for several microseconds.  Entries past the window
+  // or the bias list read as 0 and are dropped by index below.
+  constexpr int kOutOfRange = 0x7ffffff0;
+  int hraw[HPT];
+  int braw = 0;
+  float bval = 0.0f;
+  if (n_hist > 0 && one_round) {
+    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(hrow), (short)0, a.hcap * 4, 0x00020000);
 #pragma unroll
-      for (int h = 0; h < HPT; ++h) {
-        const int i = h * NT + tid;
-        hl[h] = (i < n_hist) ? hist_loc(i) : -1;
-      }
+    for (int h = 0; h < HPT; ++h) {
+      const int i = h * NT + tid;
+      hraw[h] = (int)__builtin_amdgcn_raw_buffer_load_b32(hr, i < n_hist ? hist_slot(i) * 4 : kOutOfRange, 0, 0);
     }
+  }
+  if (P.bias_cnt > 0 && bias_one) {
+    const int off = tid < P.bias_cnt ? tid * 4 : kOutOfRange;
+    const __amdgpu_buffer_rsrc_t bi = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(a.bias_ids + P.bias_off), (short)0, P.bias_cnt * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t bv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a.bias_vals + P.bias_off), (short)0, P.bias_cnt * 4, 0x00020000);
+    braw = (int)__builtin_amdgcn_raw_buffer_load_b32(bi, off, 0, 0);
+    bval = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bv, off, 0, 0));
+  }
+  // slice-local offsets of this thread's window entries (one round) and bias
+  // entry (-1: none)
+  int hl[HPT];
+#pragma unroll
+  for (int h = 0; h < HPT; ++h) hl[h] = (one_round && h * NT + tid < n_hist) ? id_loc(hraw[h]) : -1;
+  const int b_loc = (bias_one && tid < P.bias_cnt) ? id_loc(braw) : -1;
+  const float b_val = bval;
+  first_tiles();
+  if (has_patch) {
+    const int nw = (len + 31) >> 5;
     // fn(loc) for every window entry of the slice (loc < 0: not in it)
     auto for_window = [&](auto fn) __attribute__((always_inline)) {
       if (one_round) {
@@ -509,24 +568,13 @@ void stream_kernel(const StreamArgs a) {
 #pragma unroll
           for (int h = 0; h < HPT; ++h) {
             const int i = b0 + h * NT + tid;
-            l[h] = (i < n_hist) ? hist_loc(i) : -1;
+            l[h] = (i < n_hist) ? id_loc(hrow[hist_slot(i)]) : -1;
           }
 #pragma unroll
           for (int h = 0; h < HPT; ++h) fn(l[h]);
         }
       }
     };
-    // bias entries of this thread (one round trip when bias_cnt <= NT)
-    const bool bias_one = P.bias_cnt <= NT;
-    int b_loc = -1;
-    float b_val = 0.0f;
-    if (bias_one && tid < P.bias_cnt) {
-      const int loc = a.bias_ids[P.bias_off + tid] - lo;
-      b_val = a.bias_vals[P.bias_off + tid];
-      b_loc = (loc >= 0 && loc < len) ? loc : -1;
-    }
-    // the first tile follows the window and bias reads into the memory queues
-    load_tile<NT, NV4, VEC>(R0, src, 0, len);
     for (int w = tid; w < nw; w += NT) bitmap[w] = 0u;
     __syncthreads();
     for_window([&](int loc) {
@@ -585,8 +633,6 @@ void stream_kernel(const StreamArgs a) {
         }
       }
     }
-  } else {
-    load_tile<NT, NV4, VEC>(R0, src, 0, len);
   }
   __syncthreads();
   auto patched = [&](int loc) -> bool {  // loc: slice-local offset
@@ -647,23 +693,32 @@ void stream_kernel(const StreamArgs a) {
       uint64_t* wb = cand + (size_t)wv * kWaveCap;
       uint32_t* whist = shist + wv * kWaveBins;
       if (t == 0) {
-        // Block-wide start: the k-th largest of the per-thread maxima of the
-        // first tile (k real elements) bounds the row's k-th largest from below.
-        uint32_t tmax = 0u;
-        bool has = false;
+        // Block-wide start: every wave puts the M largest of its lanes'
+        // maxima (distinct elements) into LDS, and the k-th largest of those
+        // NW * M >= k real elements bounds the row's k-th largest from below.
+        constexpr int M = (kWave + NW - 1) / NW;
+        uint32_t lmax = 0u;  // 0: no unpatched value in this lane
 #pragma unroll
-        for (int q = 0; q < NE; ++q) {
-          if (valid(q) && !patched(loc_of(q))) {
-            tmax = max(tmax, f2key(v[q]));
-            has = true;
+        for (int j = 0; j < NV4; ++j) {
+          const int o = obase + j * NT * 4;
+          const uint32_t word = has_patch && (o < len) ? bitmap[o >> 5] >> (o & 31) : 0u;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int q = 4 * j + e;
+            if (valid(q) && !((word >> e) & 1u)) lmax = max(lmax, f2key(v[q]));
           }
         }
-        // a thread lacks `has` only when its NE values are all patched
-        const bool surely = full && npatch <= NE * (NT - k);
-        if ((surely ? NT : block_sum<NT>(has ? 1 : 0, smem)) >= k) {
-          wtau = block_select<NT>([&](auto fn) { fn(tmax, has); }, k, -1, shist, smem).tau;
-          __syncthreads();  // the select's histogram overlaps the per-wave ones
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+          const uint32_t m = wave_max_u32(lmax);
+          const uint64_t at = __ballot(lmax == m);
+          if (lane == __ffsll((unsigned long long)at) - 1) lmax = 0u;
+          if (lane == 0) s_top[wv * M + i] = m;
         }
+        __syncthreads();
+        // every wave takes the k-th largest of the NW * M maxima itself (key 0,
+        // fewer than k real values, leaves no bound)
+        wtau = wave_kth_largest(lane < NW * M ? s_top[lane] : 0u, k);
       }
       // any wave's threshold is a lower bound of the k-th largest of the row
       wtau = max(wtau, __hip_atomic_load(&s_tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
@@ -874,23 +929,29 @@ void stream_kernel(const StreamArgs a) {
     }
   };
 
-  auto unpack = [&](float (&v)[NE], const f32x4 (&R)[NV4]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < NV4; ++j) {
-      v[4 * j + 0] = R[j].x;
-      v[4 * j + 1] = R[j].y;
-      v[4 * j + 2] = R[j].z;
-      v[4 * j + 3] = R[j].w;
-    }
-  };
   if (!ovf) {
-    // ovf is block-uniform; wovf is set only on the wave path (no barriers there)
+    // One tile is in flight while the previous one is processed: as each
+    // float4 group of tile t lands it is copied out and the same group of
+    // tile t + 1 is requested into its registers, so the memory queue stays
+    // full.  (A workgroup can keep about one tile of requests outstanding;
+    // more only stalls the issuing wave.)  The requests are unconditional
+    // (past the slice they return zeros without reading memory) and the loop
+    // runs on wave-uniform conditions, so the compiler's waits follow the
+    // request order exactly.  ovf and wovf agree over the wave; the scalar
+    // read makes that visible.
+    auto stop = [&]() -> bool { return __builtin_amdgcn_readfirstlane((int)(ovf || wovf)) != 0; };
     for (int t = 0; t < ntiles; ++t) {
       float v[NE];
-      if (t > 0) load_tile<NT, NV4, VEC>(R0, src, t * TE, len);
-      unpack(v, R0);
+#pragma unroll
+      for (int j = 0; j < NV4; ++j) {
+        v[4 * j + 0] = R0[j].x;
+        v[4 * j + 1] = R0[j].y;
+        v[4 * j + 2] = R0[j].z;
+        v[4 * j + 3] = R0[j].w;
+        R0[j] = load_group<NT, VEC>(rs, (t + 1) * TE, j);
+      }
       process(v, t);
-      if (ovf || wovf) break;
+      if (stop()) break;
     }
   }
   // the patched ids' original logits (read back after the stream, likely from

@@ -62,6 +62,33 @@ __device__ __forceinline__ int wave_incl_scan(int x) {
   return x;
 }
 
+// Maximum over the wave (every lane gets it): DPP row shifts within each
+// 16-lane row, then the four row maxima.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, true));  // row_shr:1
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, true));  // row_shr:2
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, true));  // row_shr:4
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, true));  // row_shr:8
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 15);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)x, 31);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 47);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+  return max(max(a, b), max(c, d));
+}
+
+// The k-th largest of the lanes' values (1 <= k <= 64; lanes without a value
+// hold 0): the largest r with at least k values >= r, fixed one bit at a
+// time from the top.
+__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t x, int k) {
+  uint32_t r = 0u;
+#pragma unroll
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t c = r | (1u << b);
+    if (__popcll(__ballot(x >= c)) >= k) r = c;
+  }
+  return r;
+}
+
 // Exclusive and total wave sums of small non-negative counts (x < 2^BITS),
 // from one ballot per bit: no cross-lane data movement.
 template <int BITS>
