@@ -35,8 +35,13 @@ struct RowParams {
   int64_t repeat_last_n;
 };
 
-// Patch flags: which of penalty (:71-74) and bias (:76) touch a logit.
-enum PatchFlags : uint32_t { kPatchPen = 1u, kPatchBias = 2u };
+// Patch flags: which of penalty (:71-74) and bias (:76) touch a logit; in the
+// streaming kernel also whether its original logit was met above the
+// threshold (seen) and whether its patch can raise it (a positive or NaN
+// bias).  The streaming kernel keeps the window count above the flag bits
+// (a count > 0 means the penalty applies) instead of kPatchPen.
+enum PatchFlags : uint32_t { kPatchPen = 1u, kPatchBias = 2u, kPatchSeen = 4u, kPatchRise = 8u };
+constexpr int kPatchCountShift = 4;
 
 // Streaming-kernel geometry.
 constexpr int kStreamVec4 = 4;       // float4 loads per thread per tile

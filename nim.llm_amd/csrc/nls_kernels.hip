@@ -475,6 +475,12 @@ void stream_kernel(const StreamArgs a) {
   float* pbias = pfin + a.pcap;
   uint32_t* pflag = reinterpret_cast<uint32_t*>(pbias + a.pcap);  // flags | count << 2
   int32_t* pid = reinterpret_cast<int32_t*>(pflag + a.pcap);
+  // patch slot of a patched slice-local offset: patched offsets are numbered
+  // in index order (wpre holds the count before each bitmap word)
+  auto slot_of = [&](int loc) -> int {
+    const int w = loc >> 5;
+    return wpre[w] + __popc(bitmap[w] & ((1u << (loc & 31)) - 1u));
+  };
 
   // the row's uniform or RNG state, read now (scalar loads) so the tail
   // does not wait
@@ -606,22 +612,18 @@ void stream_kernel(const StreamArgs a) {
         pflag[p] = 0u;
       }
       __syncthreads();
-      auto pidx = [&](int loc) -> int {
-        const int w = loc >> 5;
-        return wpre[w] + __popc(bitmap[w] & ((1u << (loc & 31)) - 1u));
-      };
       // every writer of pid[p] stores the same value
       for_window([&](int loc) {
         if (loc >= 0) {
-          const int p = pidx(loc);
-          atomicAdd(&pflag[p], 4u);
+          const int p = slot_of(loc);
+          atomicAdd(&pflag[p], 1u << kPatchCountShift);  // the window count
           pid[p] = lo + loc;
         }
       });
       auto put_bias = [&](int loc, float val) {
-        const int p = pidx(loc);
+        const int p = slot_of(loc);
         pbias[p] = val;  // bias ids are unique per row
-        atomicOr(&pflag[p], (uint32_t)kPatchBias);
+        atomicOr(&pflag[p], (uint32_t)kPatchBias | (!(val <= 0.0f) ? (uint32_t)kPatchRise : 0u));
         pid[p] = lo + loc;
       };
       if (bias_one) {
@@ -638,6 +640,39 @@ void stream_kernel(const StreamArgs a) {
   auto patched = [&](int loc) -> bool {  // loc: slice-local offset
     return has_patch && ((bitmap[loc >> 5] >> (loc & 31)) & 1u);
   };
+  // A patched logit met at or above the threshold keeps its original value
+  // for the final pass.  One that stays below it cannot be a member unless
+  // its patch can raise it (a positive or NaN bias, or penalties of the
+  // raising sign): every other patch only lowers a logit (division by
+  // rp >= 1 of a positive value, multiplication of a non-positive one,
+  // subtraction of count * frequency + presence >= 0, a bias <= 0), and so
+  // does the temperature's positive factor, in float rounding too.
+  auto capture = [&](int loc, float raw) {
+    const int p = slot_of(loc);
+    pfin[p] = raw;
+    atomicOr(&pflag[p], (uint32_t)kPatchSeen);
+  };
+  const bool row_rise =
+      (P.rp_active && !(P.rp32 >= 1.0f)) || !(P.freq >= 0.0) || !(P.pres >= 0.0);
+  auto may_rise = [&](uint32_t fl) -> bool {
+    return (fl & kPatchRise) || (row_rise && (fl >> kPatchCountShift) > 0);
+  };
+  // The original logits of the ids whose patch may raise them are requested
+  // now (slots tid + r * NT; the rest, if any, are read after the stream):
+  // requests past the slice return 0 without reading memory, so the slots
+  // without such a patch need no branch around the load.
+  constexpr int RPT = 2;
+  float rraw[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int p = tid + r * NT;
+    const bool want = !ovf && p < npatch && may_rise(pflag[p]);
+    rraw[r] = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(rs, want ? (pid[p] - lo) * 4 : kOutOfRange, 0, 0));
+  }
+  // greedy rows: the original logit at index 0 (argmax stays at 0 when the
+  // final value there is NaN), read from the first tile
+  float x0raw = 0.0f;
 
   // ---- the stream ----
   float bv = -__builtin_inff();
@@ -672,18 +707,26 @@ void stream_kernel(const StreamArgs a) {
         if (valid(q) && v[q] > tmx) tmx = v[q];
       // (nothing chosen yet: equal values still pick the first index, so a
       // row of -inf answers its first id)
+      if (t == 0 && tid == 0) x0raw = v[0];
       if (tmx > bv || (tmx == bv && bi == 0x7fffffff)) {
 #pragma unroll
         for (int q = 0; q < NE; ++q)
-          if (valid(q) && !patched(loc_of(q))) argmax_merge(bv, bi, v[q], lo + loc_of(q));
+          if (valid(q)) {
+            if (patched(loc_of(q)))
+              capture(loc_of(q), v[q]);
+            else
+              argmax_merge(bv, bi, v[q], lo + loc_of(q));
+          }
       }
       return;
     }
-    // temperature (:80-81)
+    // temperature (:80-81); v keeps the original logits for the patched ids
+    // met on the way
+    float sv[NE];
     {
       const float invT = P.invT;
 #pragma unroll
-      for (int q = 0; q < NE; ++q) v[q] = v[q] * invT;
+      for (int q = 0; q < NE; ++q) sv[q] = v[q] * invT;
     }
     auto gid = [&](int q) -> uint32_t { return (uint32_t)(lo + loc_of(q)); };
     if constexpr (WAVE) {
@@ -705,7 +748,7 @@ void stream_kernel(const StreamArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int q = 4 * j + e;
-            if (valid(q) && !((word >> e) & 1u)) lmax = max(lmax, f2key(v[q]));
+            if (valid(q) && !((word >> e) & 1u)) lmax = max(lmax, f2key(sv[q]));
           }
         }
 #pragma unroll
@@ -725,7 +768,7 @@ void stream_kernel(const StreamArgs a) {
       float thr_f = key2f(wtau);
       int npf = 0;  // prefilter passes of this tile, over the wave
 #pragma unroll
-      for (int q = 0; q < NE; ++q) npf += __popcll(__ballot(valid(q) && !(v[q] < thr_f)));
+      for (int q = 0; q < NE; ++q) npf += __popcll(__ballot(valid(q) && !(sv[q] < thr_f)));
       if (npf == 0) return;
       if (wn + npf > kWaveCap) {
         // Raise the threshold to a lower bound of the k-th largest of all this
@@ -742,8 +785,8 @@ void stream_kernel(const StreamArgs a) {
         }
 #pragma unroll
         for (int q = 0; q < NE; ++q) {
-          if (valid(q) && !(v[q] < thr_f) && !patched(loc_of(q))) {
-            const uint32_t kq = f2key(v[q]);
+          if (valid(q) && !(sv[q] < thr_f) && !patched(loc_of(q))) {
+            const uint32_t kq = f2key(sv[q]);
             if (kq >= wtau) {
               topq_insert<2>(tops, kq);
               ++nm;
@@ -782,7 +825,7 @@ void stream_kernel(const StreamArgs a) {
         wn = ktot;
         npf = 0;
 #pragma unroll
-        for (int q = 0; q < NE; ++q) npf += __popcll(__ballot(valid(q) && !(v[q] < thr_f)));
+        for (int q = 0; q < NE; ++q) npf += __popcll(__ballot(valid(q) && !(sv[q] < thr_f)));
         if (wn + npf > kWaveCap) {
           wovf = true;  // ties or an adversarial order crowd the buffer
           return;
@@ -791,9 +834,12 @@ void stream_kernel(const StreamArgs a) {
       // append every unpatched value >= the threshold (each passes the prefilter)
 #pragma unroll
       for (int q = 0; q < NE; ++q) {
-        if (__ballot(valid(q) && !(v[q] < thr_f)) == 0ull) continue;
-        const uint32_t kq = f2key(v[q]);
-        const bool keep = valid(q) && kq >= wtau && !patched(loc_of(q));
+        if (__ballot(valid(q) && !(sv[q] < thr_f)) == 0ull) continue;
+        const uint32_t kq = f2key(sv[q]);
+        const bool pass = valid(q) && kq >= wtau;
+        const bool pat = pass && patched(loc_of(q));
+        if (pat) capture(loc_of(q), v[q]);
+        const bool keep = pass && !pat;
         const uint64_t m = __ballot(keep);
         if (keep) wb[wn + (int)__popcll(m & lanes_below())] = ((uint64_t)kq << 32) | gid(q);
         wn += (int)__popcll(m);
@@ -832,7 +878,10 @@ void stream_kernel(const StreamArgs a) {
       auto use = [&](int q) -> bool { return valid(q) && !patched(loc_of(q)); };
       uint32_t key[NE];
 #pragma unroll
-      for (int q = 0; q < NE; ++q) key[q] = f2key(v[q]);
+      for (int q = 0; q < NE; ++q) key[q] = f2key(sv[q]);
+#pragma unroll
+      for (int q = 0; q < NE; ++q)
+        if (valid(q) && key[q] >= tau && patched(loc_of(q))) capture(loc_of(q), v[q]);
       int mine = 0;
 #pragma unroll
       for (int q = 0; q < NE; ++q) mine += (use(q) && key[q] >= tau);
@@ -957,212 +1006,363 @@ void stream_kernel(const StreamArgs a) {
   // the patched ids' original logits (read back after the stream, likely from
   // cache) and their final values: penalties then bias (:71-76), then
   // temperature (:80-81) on the sampling rows
-  if (!ovf && npatch > 0) {
-    for (int p = tid; p < npatch; p += NT) {
-      const uint32_t fl = pflag[p];
-      const uint32_t cnt = fl >> 2;
-      float v = src[pid[p] - lo];
-      if (cnt) {
-        if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
-        v = v - (float)((double)cnt * P.freq + P.pres);  // float64, one rounding (:74)
-      }
-      if (fl & kPatchBias) v = v + pbias[p];
-      if (!greedy) v = v * P.invT;
-      pfin[p] = v;
+  // The final value of patched slot p from its original logit: penalties then
+  // bias (:71-76), then temperature (:80-81) on the sampling rows.
+  auto patched_final = [&](int p, float v, uint32_t fl) -> float {
+    const uint32_t cnt = fl >> kPatchCountShift;
+    if (cnt) {
+      if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
+      v = v - (float)((double)cnt * P.freq + P.pres);  // float64, one rounding (:74)
     }
-    __syncthreads();
-  }
+    if (fl & kPatchBias) v = v + pbias[p];
+    if (!greedy) v = v * P.invT;
+    return v;
+  };
+  // original logit of slot p for the final pass (met during the stream,
+  // requested before it, or read now)
+  // (the late read goes through the slice's buffer resource, so that the
+  // compiler cannot merge it with the LDS read into one generic-address load)
+  auto patched_raw = [&](int p, uint32_t fl) -> float {
+    const int r = (p - tid) / NT;
+    if (fl & kPatchSeen) return pfin[p];
+    if (r < RPT) return r == 0 ? rraw[0] : rraw[1];
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (pid[p] - lo) * 4, 0, 0));
+  };
 
-  // ---- the slice's candidates: stream buffer(s) + patched values ----
-  uint64_t* ent = cand + (size_t)cur * a.ccap;
-  int N = buf_n;
-  if (topk) {
-    uint32_t tau_all = tau;  // a lower bound of the row's k-th largest, uniform
-    if constexpr (WAVE) {
-      // concatenate the wave buffers into the second buffer
-      if (lane == 0) {
-        s_wn[wv] = wovf ? -1 : wn;
-        s_wt[wv] = wtau;
-      }
-      __syncthreads();
-      int off = 0;
-      N = 0;
-      tau_all = 0u;
-      for (int w = 0; w < NW; ++w) {
-        const int nw_ = s_wn[w];
-        tau_all = max(tau_all, s_wt[w]);
-        if (nw_ < 0) {
-          ovf = true;
-        } else {
-          if (w == wv) off = N;
-          N += nw_;
-        }
-      }
-      ent = cand + a.ccap;
-      if (!ovf) {
-        const uint64_t* wb = cand + (size_t)wv * kWaveCap;
-        for (int i = lane; i < wn; i += kWave) ent[off + i] = wb[i];
-      }
-      __syncthreads();
+  uint64_t* ent;
+  int N;
+  // Top-k rows of the wave path on one slice: the candidates are narrowed
+  // before any select.  Every wave offers its M largest buffer keys (64
+  // distinct real elements in all); the k-th largest of those bounds the
+  // row's k-th largest from below, and typically leaves few more than k
+  // entries above it.  With at most 128 survivors and no excess ties at the
+  // k-th value one wave finishes the row alone.
+  const bool wave_flow = WAVE && topk && a.S == 1;
+  if (wave_flow) {
+    constexpr int M = (kWave + NW - 1) / NW;
+    uint64_t* wb = cand + (size_t)wv * kWaveCap;
+    uint64_t xs[PER];
+    uint32_t ks[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = lane + j * kWave;
+      xs[j] = (!wovf && i < wn) ? wb[i] : 0ull;
+      ks[j] = (uint32_t)(xs[j] >> 32);
     }
-    if (!ovf && npatch > 0) {
-      // patched values >= tau_all join the candidates
-      if (tid == 0) s_cnt = N;
-      __syncthreads();
+    {
+      uint32_t kr[PER];
+#pragma unroll
+      for (int j = 0; j < PER; ++j) kr[j] = ks[j];
+#pragma unroll
+      for (int i = 0; i < M; ++i) {
+        uint32_t lm = 0u;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) lm = max(lm, kr[j]);
+        const uint32_t m = wave_max_u32(lm);
+        const uint64_t at = __ballot(lm == m);
+        if (lane == __ffsll((unsigned long long)at) - 1) {
+          bool done = false;
+#pragma unroll
+          for (int j = 0; j < PER; ++j)
+            if (!done && kr[j] == m) {
+              kr[j] = 0u;
+              done = true;
+            }
+        }
+        if (lane == 0) s_top[wv * M + i] = m;
+      }
+    }
+    if (lane == 0) {
+      s_wn[wv] = wovf ? -1 : wn;
+      s_wt[wv] = wtau;
+    }
+    __syncthreads();  // every wave's stream, captures and offers are in
+    uint32_t tau_all = 0u;
+    for (int w = 0; w < NW; ++w) {
+      ovf = ovf || s_wn[w] < 0;
+      tau_all = max(tau_all, s_wt[w]);
+    }
+    ent = cand + a.ccap;  // free: holds NW * kWaveCap entries and more
+    if (!ovf) {
+      const uint32_t te = max(tau_all, wave_kth_largest(lane < NW * M ? s_top[lane] : 0u, k));
+      // this wave's entries >= te
+      int c = 0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) c += __popcll(__ballot(ks[j] >= te && ks[j] != 0u));
+      int base = 0;
+      if (lane == 0 && c) base = atomicAdd(&s_cnt, c);
+      base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const bool keep = ks[j] >= te && ks[j] != 0u;
+        const uint64_t mk = __ballot(keep);
+        if (keep) ent[base + (int)__popcll(mk & lanes_below())] = xs[j];
+        base += (int)__popcll(mk);
+      }
+      // patched ids: final values, those >= te join
       for (int p = tid; p < npatch; p += NT) {
-        const uint32_t kp = f2key(pfin[p]);
-        if (kp >= tau_all) {
+        const uint32_t fl = pflag[p];
+        if (!(fl & kPatchSeen) && !may_rise(fl)) continue;
+        const float v = patched_final(p, patched_raw(p, fl), fl);
+        const uint32_t kp = f2key(v);
+        if (kp >= te) {
           const int i = atomicAdd(&s_cnt, 1);
           if (i < a.ccap) ent[i] = ((uint64_t)kp << 32) | (uint32_t)pid[p];
         }
       }
-      __syncthreads();
-      N = s_cnt;
-      if (N > a.ccap) ovf = true;  // uniform
-      __syncthreads();
-      if (tid == 0) s_cnt = 0;
     }
-  } else {
-    // greedy: patched final values join the argmax
-    for (int p = tid; p < npatch; p += NT) argmax_merge(bv, bi, pfin[p], pid[p]);
-  }
-  // argmax (:45-49) starts from index 0: when its value is NaN nothing
-  // compares greater and the answer stays 0
-  bool nan0 = false;
-  if (greedy && lo == 0 && len > 0 && tid == 0) {
-    float x0 = src[0];
-    if (patched(0)) x0 = pfin[wpre[0] + 0];
-    nan0 = x0 != x0;
-  }
-
-  // ---- slice argmax (first index on ties) ----
-  wave_argmax(bv, bi);
-  if (lane == 0) {
-    s_rv[wv] = bv;
-    s_ri[wv] = bi;
-  }
-  __syncthreads();
-  float rv = s_rv[0];
-  int ri = s_ri[0];
+    __syncthreads();
+    N = s_cnt;
+    if (!ovf && N > a.ccap) ovf = true;  // uniform
+    if (ovf) {
+      if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
+      return;
+    }
+    if (N >= k && N <= 2 * kWave) {
+      // every wave finds the k-th largest key T of the survivors itself
+      const uint64_t e0 = lane < N ? ent[lane] : 0ull;
+      const uint64_t e1 = lane + kWave < N ? ent[lane + kWave] : 0ull;
+      const uint32_t k0 = (uint32_t)(e0 >> 32), k1 = (uint32_t)(e1 >> 32);
+      uint32_t T = 0u;
 #pragma unroll
-  for (int w = 1; w < NW; ++w) argmax_merge(rv, ri, s_rv[w], s_ri[w]);
-
-  if (a.S > 1) {
-    // ---- publish this slice; the last one to arrive completes the row ----
-    const int64_t part = (int64_t)row * a.S + sl;
-    uint64_t* pdst = a.part_cand + part * a.pc;
-    int nout = 0;
-    int flags = (ovf ? kSliceOverflow : 0) | (nan0 ? kSliceNan0 : 0);
-    if (topk && !ovf) {
-      if (N > a.pc) {
-        const SelectResult r = block_select<NT>(
-            [&](auto fn) {
-              for (int i0 = 0; i0 < N; i0 += NT) {
-                const int i = i0 + tid;
-                const bool in = i < N;
-                fn(in ? (uint32_t)(ent[i] >> 32) : 0u, in);
-              }
-            },
-            k, a.pc, shist, smem);
-        if (r.ge > a.pc) {
-          flags = kSliceOverflow;
-        } else {
-          int mine = 0;
-          for (int i = tid; i < N; i += NT) mine += ((uint32_t)(ent[i] >> 32) >= r.tau);
-          int tot;
-          int pos = block_excl_scan<NT>(mine, smem, tot);
-          for (int i = tid; i < N; i += NT)
-            if ((uint32_t)(ent[i] >> 32) >= r.tau) store_agent(&pdst[pos++], ent[i]);
-          nout = tot;
-        }
-      } else {
-        for (int i = tid; i < N; i += NT) store_agent(&pdst[i], ent[i]);
-        nout = N;
+      for (int b = 31; b >= 0; --b) {
+        const uint32_t c = T | (1u << b);
+        if (__popcll(__ballot(k0 >= c)) + __popcll(__ballot(k1 >= c)) >= k) T = c;
+      }
+      const int ge = __popcll(__ballot(lane < N && k0 >= T)) + __popcll(__ballot(lane + kWave < N && k1 >= T));
+      if (ge == k) {
+        // no excess ties at T: the members are exactly the survivors >= T
+        if (wv != 0) return;
+        uint64_t* mem = reinterpret_cast<uint64_t*>(regA);
+        const bool in0 = lane < N && k0 >= T, in1 = lane + kWave < N && k1 >= T;
+        const uint64_t m0 = __ballot(in0), m1 = __ballot(in1);
+        if (in0) mem[__popcll(m0 & lanes_below())] = e0;
+        if (in1) mem[__popcll(m0) + __popcll(m1 & lanes_below())] = e1;
+        double u = 0.0;
+        if (lane == 0) u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
+        wave_tail(mem, k, P, u, row, a.out, a.dbg);
+        return;
       }
     }
-    if (tid == 0) {
-      store_agent(&a.part_info[part].n, nout);
-      store_agent(&a.part_info[part].flags, flags);
-      store_agent(&a.part_info[part].amax, ri);
-      store_agent(&a.part_info[part].vmax, __float_as_int(rv));
-    }
-    // The slice data above is written with agent-scope stores, which go to
-    // the device's point of coherence; waiting for their completion before
-    // the arrival count is bumped orders them without an L2 writeback.
-    __builtin_amdgcn_s_waitcnt(0);
+    // many survivors or excess ties: the block-wide member selection
     __syncthreads();
-    if (tid == 0)
-      s_last = (__hip_atomic_fetch_add(&a.arrive[row], 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1));
-    __syncthreads();
-    if (!s_last) return;
-    if (tid == 0) __hip_atomic_store(&a.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // slice records: one per thread, then every thread reads them from LDS.
-    // s_off borrows the select histogram (free here; 5 * kMaxSlices words < kSelWords).
-    int* s_off = reinterpret_cast<int*>(shist);
-    static_assert(5 * kMaxSlices <= kSelWords, "slice records must fit the histogram");
-    if (tid < a.S) {
-      const SliceInfo* in = a.part_info + (int64_t)row * a.S + tid;
-      const int nj = load_agent(&in->n);
-      const int fl = load_agent(&in->flags);
-      s_off[kMaxSlices + tid] = (nj < 0 || nj > a.pc) ? -1 : nj;  // never trust a count past the buffer
-      s_off[2 * kMaxSlices + tid] = fl;
-      s_off[3 * kMaxSlices + tid] = load_agent(&in->amax);
-      s_off[4 * kMaxSlices + tid] = load_agent(&in->vmax);
+    if (tid == 0) s_cnt = 0;
+  } else {
+    // Ids that can be members were met during the stream; only the ids whose
+    // patch may raise them are read again here.  The others are left out
+    // (flag kPatchSeen clear).
+    if (!ovf && npatch > 0) {
+      __syncthreads();  // every wave's captures are in
+      for (int p = tid; p < npatch; p += NT) {
+        uint32_t fl = pflag[p];
+        const uint32_t cnt = fl >> kPatchCountShift;
+        if (!(fl & kPatchSeen) && !may_rise(fl)) continue;
+        float v = patched_raw(p, fl);
+        if (cnt) {
+          if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
+          v = v - (float)((double)cnt * P.freq + P.pres);  // float64, one rounding (:74)
+        }
+        if (fl & kPatchBias) v = v + pbias[p];
+        if (!greedy) v = v * P.invT;
+        pfin[p] = v;
+        if (!(fl & kPatchSeen)) pflag[p] = fl | kPatchSeen;
+      }
+      __syncthreads();
     }
-    __syncthreads();
-    int any = 0;
-    N = 0;
-    rv = -__builtin_inff();
-    ri = 0x7fffffff;
-    for (int j = 0; j < a.S; ++j) {
-      const int nj = s_off[kMaxSlices + j];
-      any |= s_off[2 * kMaxSlices + j] | (nj < 0 ? kSliceOverflow : 0);
-      nan0 = nan0 || (s_off[2 * kMaxSlices + j] & kSliceNan0);
-      argmax_merge(rv, ri, __int_as_float(s_off[4 * kMaxSlices + j]), s_off[3 * kMaxSlices + j]);
-      s_off[j] = N;  // start of slice j in the merged buffer
-      if (nj > 0) N += nj;
-    }
-    ovf = (any & kSliceOverflow) != 0;
-    if (topk && !ovf) {
-      ent = cand;  // both ping-pong buffers: 2 * ccap >= S * pc entries
-      constexpr int MR = 8;  // loads in flight per thread
-      for (int b0 = 0; b0 < N; b0 += NT * MR) {
-        uint64_t xv[MR];
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-          const int i = b0 + r * NT + tid;
-          xv[r] = 0ull;
-          if (i < N) {
-            int j = 0;
-            while (j + 1 < a.S && s_off[j + 1] <= i) ++j;
-            xv[r] = load_agent(a.part_cand + ((int64_t)row * a.S + j) * a.pc + (i - s_off[j]));
+
+    // ---- the slice's candidates: stream buffer(s) + patched values ----
+    ent = cand + (size_t)cur * a.ccap;
+    N = buf_n;
+    if (topk) {
+      uint32_t tau_all = tau;  // a lower bound of the row's k-th largest, uniform
+      if constexpr (WAVE) {
+        // concatenate the wave buffers into the second buffer
+        if (lane == 0) {
+          s_wn[wv] = wovf ? -1 : wn;
+          s_wt[wv] = wtau;
+        }
+        __syncthreads();
+        int off = 0;
+        N = 0;
+        tau_all = 0u;
+        for (int w = 0; w < NW; ++w) {
+          const int nw_ = s_wn[w];
+          tau_all = max(tau_all, s_wt[w]);
+          if (nw_ < 0) {
+            ovf = true;
+          } else {
+            if (w == wv) off = N;
+            N += nw_;
           }
         }
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-          const int i = b0 + r * NT + tid;
-          if (i < N) ent[i] = xv[r];
+        ent = cand + a.ccap;
+        if (!ovf) {
+          const uint64_t* wb = cand + (size_t)wv * kWaveCap;
+          for (int i = lane; i < wn; i += kWave) ent[off + i] = wb[i];
+        }
+        __syncthreads();
+      }
+      if (!ovf && npatch > 0) {
+        // patched values >= tau_all join the candidates
+        if (tid == 0) s_cnt = N;
+        __syncthreads();
+        for (int p = tid; p < npatch; p += NT) {
+          if (!(pflag[p] & kPatchSeen)) continue;
+          const uint32_t kp = f2key(pfin[p]);
+          if (kp >= tau_all) {
+            const int i = atomicAdd(&s_cnt, 1);
+            if (i < a.ccap) ent[i] = ((uint64_t)kp << 32) | (uint32_t)pid[p];
+          }
+        }
+        __syncthreads();
+        N = s_cnt;
+        if (N > a.ccap) ovf = true;  // uniform
+        __syncthreads();
+        if (tid == 0) s_cnt = 0;
+      }
+    } else {
+      // greedy: patched final values join the argmax
+      for (int p = tid; p < npatch; p += NT)
+        if (pflag[p] & kPatchSeen) argmax_merge(bv, bi, pfin[p], pid[p]);
+    }
+    // argmax (:45-49) starts from index 0: when its value is NaN nothing
+    // compares greater and the answer stays 0
+    bool nan0 = false;
+    if (greedy && lo == 0 && len > 0 && tid == 0) {
+      float x0 = x0raw;
+      if (patched(0)) x0 = pfin[wpre[0] + 0];
+      nan0 = x0 != x0;
+    }
+
+    // ---- slice argmax (first index on ties) ----
+    wave_argmax(bv, bi);
+    if (lane == 0) {
+      s_rv[wv] = bv;
+      s_ri[wv] = bi;
+    }
+    __syncthreads();
+    float rv = s_rv[0];
+    int ri = s_ri[0];
+  #pragma unroll
+    for (int w = 1; w < NW; ++w) argmax_merge(rv, ri, s_rv[w], s_ri[w]);
+
+    if (a.S > 1) {
+      // ---- publish this slice; the last one to arrive completes the row ----
+      const int64_t part = (int64_t)row * a.S + sl;
+      uint64_t* pdst = a.part_cand + part * a.pc;
+      int nout = 0;
+      int flags = (ovf ? kSliceOverflow : 0) | (nan0 ? kSliceNan0 : 0);
+      if (topk && !ovf) {
+        if (N > a.pc) {
+          const SelectResult r = block_select<NT>(
+              [&](auto fn) {
+                for (int i0 = 0; i0 < N; i0 += NT) {
+                  const int i = i0 + tid;
+                  const bool in = i < N;
+                  fn(in ? (uint32_t)(ent[i] >> 32) : 0u, in);
+                }
+              },
+              k, a.pc, shist, smem);
+          if (r.ge > a.pc) {
+            flags = kSliceOverflow;
+          } else {
+            int mine = 0;
+            for (int i = tid; i < N; i += NT) mine += ((uint32_t)(ent[i] >> 32) >= r.tau);
+            int tot;
+            int pos = block_excl_scan<NT>(mine, smem, tot);
+            for (int i = tid; i < N; i += NT)
+              if ((uint32_t)(ent[i] >> 32) >= r.tau) store_agent(&pdst[pos++], ent[i]);
+            nout = tot;
+          }
+        } else {
+          for (int i = tid; i < N; i += NT) store_agent(&pdst[i], ent[i]);
+          nout = N;
         }
       }
+      if (tid == 0) {
+        store_agent(&a.part_info[part].n, nout);
+        store_agent(&a.part_info[part].flags, flags);
+        store_agent(&a.part_info[part].amax, ri);
+        store_agent(&a.part_info[part].vmax, __float_as_int(rv));
+      }
+      // The slice data above is written with agent-scope stores, which go to
+      // the device's point of coherence; waiting for their completion before
+      // the arrival count is bumped orders them without an L2 writeback.
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0)
+        s_last = (__hip_atomic_fetch_add(&a.arrive[row], 1u, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1));
+      __syncthreads();
+      if (!s_last) return;
+      if (tid == 0) __hip_atomic_store(&a.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // slice records: one per thread, then every thread reads them from LDS.
+      // s_off borrows the select histogram (free here; 5 * kMaxSlices words < kSelWords).
+      int* s_off = reinterpret_cast<int*>(shist);
+      static_assert(5 * kMaxSlices <= kSelWords, "slice records must fit the histogram");
+      if (tid < a.S) {
+        const SliceInfo* in = a.part_info + (int64_t)row * a.S + tid;
+        const int nj = load_agent(&in->n);
+        const int fl = load_agent(&in->flags);
+        s_off[kMaxSlices + tid] = (nj < 0 || nj > a.pc) ? -1 : nj;  // never trust a count past the buffer
+        s_off[2 * kMaxSlices + tid] = fl;
+        s_off[3 * kMaxSlices + tid] = load_agent(&in->amax);
+        s_off[4 * kMaxSlices + tid] = load_agent(&in->vmax);
+      }
+      __syncthreads();
+      int any = 0;
+      N = 0;
+      rv = -__builtin_inff();
+      ri = 0x7fffffff;
+      for (int j = 0; j < a.S; ++j) {
+        const int nj = s_off[kMaxSlices + j];
+        any |= s_off[2 * kMaxSlices + j] | (nj < 0 ? kSliceOverflow : 0);
+        nan0 = nan0 || (s_off[2 * kMaxSlices + j] & kSliceNan0);
+        argmax_merge(rv, ri, __int_as_float(s_off[4 * kMaxSlices + j]), s_off[3 * kMaxSlices + j]);
+        s_off[j] = N;  // start of slice j in the merged buffer
+        if (nj > 0) N += nj;
+      }
+      ovf = (any & kSliceOverflow) != 0;
+      if (topk && !ovf) {
+        ent = cand;  // both ping-pong buffers: 2 * ccap >= S * pc entries
+        constexpr int MR = 8;  // loads in flight per thread
+        for (int b0 = 0; b0 < N; b0 += NT * MR) {
+          uint64_t xv[MR];
+  #pragma unroll
+          for (int r = 0; r < MR; ++r) {
+            const int i = b0 + r * NT + tid;
+            xv[r] = 0ull;
+            if (i < N) {
+              int j = 0;
+              while (j + 1 < a.S && s_off[j + 1] <= i) ++j;
+              xv[r] = load_agent(a.part_cand + ((int64_t)row * a.S + j) * a.pc + (i - s_off[j]));
+            }
+          }
+  #pragma unroll
+          for (int r = 0; r < MR; ++r) {
+            const int i = b0 + r * NT + tid;
+            if (i < N) ent[i] = xv[r];
+          }
+        }
+      }
+      __syncthreads();
+      for (int q = tid; q < 5 * kMaxSlices; q += NT) s_off[q] = 0;  // restore the zeroed histogram
+      __syncthreads();
     }
-    __syncthreads();
-    for (int q = tid; q < 5 * kMaxSlices; q += NT) s_off[q] = 0;  // restore the zeroed histogram
-    __syncthreads();
-  }
-  if (ovf) {
-    if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
-    return;
-  }
-  if (!topk) {
-    if (tid == 0) {
-      a.out[row] = nan0 ? 0 : ri;
-      if (a.dbg.n) a.dbg.n[row] = 0;
-      if (a.dbg.ncand) a.dbg.ncand[row] = 0;
-      if (a.dbg.total) a.dbg.total[row] = 0.0f;
-      if (a.dbg.path) a.dbg.path[row] = 1;
+    if (ovf) {
+      if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
+      return;
     }
-    return;
+    if (!topk) {
+      if (tid == 0) {
+        a.out[row] = nan0 ? 0 : ri;
+        if (a.dbg.n) a.dbg.n[row] = 0;
+        if (a.dbg.ncand) a.dbg.ncand[row] = 0;
+        if (a.dbg.total) a.dbg.total[row] = 0.0f;
+        if (a.dbg.path) a.dbg.path[row] = 1;
+      }
+      return;
+    }
   }
   // ---- the row's heap-path members, then the reference's tail ----
   uint64_t* mem = reinterpret_cast<uint64_t*>(regA);

@@ -120,6 +120,77 @@ def test_small_random_rows(pkg, torch, V):
     compare_rows(x, plist, [list(h) for h in hist], biases, u, ids, dbg, f"V={V}")
 
 
+def patch_designs(rng, x):
+    """Rows whose penalised or biased ids fall below the threshold, rise above
+    it, or sit on it (sampler.nim:64-76): one design per row, cycling."""
+    B, V = x.shape
+    plist, hists, biases = [], [], []
+    base = dict(temperature=1.0, topK=50, topP=1.0, minP=0.0, repeatPenalty=1.0, repeatLastN=0,
+                presencePenalty=0.0, frequencyPenalty=0.0, seed=3)
+    for b in range(B):
+        order = np.argsort(-x[b], kind="stable")
+        top, low = [int(i) for i in order[:200]], [int(i) for i in order[-200:]]
+        d, h, bias = dict(base), [], {}
+        kind = b % 16
+        if kind == 0:    # the top ids penalised: met above the threshold, then fall
+            d.update(repeatPenalty=1.5); h = top[:30]
+        elif kind == 1:  # negative presence: penalised ids rise
+            d.update(temperature=0.7, presencePenalty=-3.0); h = list(rng.choice(V, 20, replace=False))
+        elif kind == 2:  # negative frequency on repeated ids
+            d.update(frequencyPenalty=-1.0); h = [int(i) for i in rng.choice(V, 5, replace=False)] * 8
+        elif kind == 3:  # rp < 1 lifts negative logits towards 0
+            d.update(repeatPenalty=0.5); h = low[:30]
+        elif kind == 4:  # a large positive bias on the lowest id
+            bias = {low[0]: 30.0}
+        elif kind == 5:  # greedy: a low id lifted to the top
+            d.update(temperature=0.0, presencePenalty=-50.0); h = [low[3]]
+        elif kind == 6:  # greedy: the top ids pushed down
+            d.update(temperature=0.0, repeatPenalty=2.0, presencePenalty=5.0); h = top[:3]
+        elif kind == 7:  # greedy with a NaN bias: skipped by argmax, except at index 0
+            d.update(temperature=0.0)
+            bias = {top[0]: math.nan} if (b // 16) % 2 == 0 else {0: math.nan, top[1]: 5.0}
+        elif kind == 8:  # the top ten banned
+            bias = {i: -math.inf for i in top[:10]}
+        elif kind == 9:  # the common mixture
+            d.update(topK=20, topP=0.9, minP=0.05, repeatPenalty=1.3, presencePenalty=0.5,
+                     frequencyPenalty=0.5)
+            h = top[:10] + [int(i) for i in rng.choice(V, 40)]
+        elif kind == 10:  # a tiny penalty on the whole top 64
+            d.update(topK=64, presencePenalty=0.01); h = top[:64]
+        elif kind == 11:  # positive bias on random ids at a high temperature
+            d.update(temperature=2.0); bias = {int(i): 2.0 for i in rng.choice(V, 30, replace=False)}
+        elif kind == 12:  # greedy with both
+            d.update(temperature=0.0, presencePenalty=1.0); h = top[:5]
+            bias = {int(i): 1.0 for i in rng.choice(V, 10, replace=False)}
+        elif kind == 13:  # k = 1 with the top penalised
+            d.update(topK=1, frequencyPenalty=2.0); h = top[:2] * 3
+        elif kind == 14:  # k > 64 with the top penalised
+            d.update(topK=300, repeatPenalty=1.5); h = top[:100]
+        else:            # k > 64 with a raising presence penalty
+            d.update(topK=300, presencePenalty=-2.0); h = list(rng.choice(V, 50, replace=False))
+        plist.append(d)
+        hists.append([int(i) for i in h])
+        biases.append(bias)
+    return plist, hists, biases
+
+
+@pytest.mark.parametrize("B,V", [(16, 70000), (16, 70001), (256, 50000)])
+def test_patched_ids_that_fall_or_rise(pkg, torch, B, V):
+    rng = np.random.default_rng(B * 7 + V)
+    say(f"[patched_fall_rise] B={B} V={V}")
+    x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
+    plist, hists, biases = patch_designs(rng, x)
+    u = rng.random(B)
+    H = max(len(h) for h in hists)
+    hist = np.full((B, H), -1, dtype=np.int64)
+    for b, h in enumerate(hists):
+        hist[b, :len(h)] = h
+    params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
+    ids, dbg = run_gpu(pkg, torch, x, params, hist, u, debug_cap=64,
+                       accept_rows=[len(h) for h in hists])
+    compare_rows(x, plist, hists, biases, u, ids, dbg, f"B={B} V={V}")
+
+
 def test_golden_fixtures(pkg, torch):
     import json
     import os
