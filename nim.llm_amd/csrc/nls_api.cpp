@@ -98,6 +98,7 @@ struct nls_sampler {
   int64_t V = 0;
   hipStream_t stream = nullptr;
   int max_bias = 0;
+  int bstride = 0;  // > 0: bias lists at a fixed stride (row b at b * bstride)
 
   std::vector<RowParams> h_rp;
   std::vector<int64_t> h_len;     // accepted ids per row
@@ -431,6 +432,24 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
     const hipError_t e = set_kernel_attributes();
     if (e != hipSuccess) return fail(hip_fail(e, "hipFuncSetAttribute"));
   }
+  // Bias lists of at most one workgroup's width go to a fixed stride, so the
+  // streaming kernel can request them before it has read the row constants.
+  if (s->max_bias > 0 && s->max_bias <= 256 && (int64_t)B * s->max_bias <= (1 << 24)) {
+    const int st = s->max_bias;
+    std::vector<int32_t> sid((size_t)B * st, -1);
+    std::vector<float> sval((size_t)B * st, 0.0f);
+    for (int b = 0; b < B; ++b) {
+      RowParams& r = s->h_rp[b];
+      for (int j = 0; j < r.bias_cnt; ++j) {
+        sid[(size_t)b * st + j] = bid[(size_t)r.bias_off + j];
+        sval[(size_t)b * st + j] = bval[(size_t)r.bias_off + j];
+      }
+      r.bias_off = b * st;
+    }
+    bid.swap(sid);
+    bval.swap(sval);
+    s->bstride = st;
+  }
   if ((rc = dalloc(&s->rp, B))) return fail(rc);
   if ((rc = dalloc(&s->bias_ids, std::max<size_t>(bid.size(), 1)))) return fail(rc);
   if ((rc = dalloc(&s->bias_vals, std::max<size_t>(bval.size(), 1)))) return fail(rc);
@@ -579,6 +598,7 @@ int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t
   a.hcap = s->hcap;
   a.bias_ids = s->bias_ids;
   a.bias_vals = s->bias_vals;
+  a.bstride = s->bstride;
   a.ccap = s->ccap;
   a.nwords = s->nwords;
   a.pcap = s->pcap;

@@ -84,6 +84,7 @@ struct StreamArgs {
   int hcap;
   const int32_t* bias_ids;
   const float* bias_vals;
+  int bstride;  // > 0: row b's bias entries start at b * bstride
   // dynamic LDS layout: cand[2][ccap] u64 | region A
   int ccap;     // candidate buffer entries (each of two ping-pong buffers)
   int nwords;   // patch bitmap words, ceil(L / 32)

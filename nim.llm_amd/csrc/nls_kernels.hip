@@ -60,14 +60,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const float* src, i
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), (short)0, len * 4, kRsrcWord3);
 }
 
-// Loads float4 group j of tile `toff` of a slice: thread t owns the groups
-// (j * NT + t), so each wave's load covers 1 KB contiguously.  Elements at or
-// beyond the slice read as 0 and are masked by the caller.  Loads are
-// nontemporal: every logit is read once.
-template <int NT, bool VEC>
-__device__ __forceinline__ f32x4 load_group(__amdgpu_buffer_rsrc_t rs, int toff, int j) {
+// Loads float4 group j of the unit at `toff` of a slice: thread `th` of the
+// unit owns the groups at toff + j * GS + th * 4 (GS floats apart), so each
+// wave's load covers 1 KB contiguously.  Elements at or beyond the slice read
+// as 0 and are masked by the caller.  Loads are nontemporal: every logit is
+// read once.
+template <int GS, bool VEC>
+__device__ __forceinline__ f32x4 load_group(__amdgpu_buffer_rsrc_t rs, int toff, int j, int th) {
   constexpr int kNT = 2;  // cache policy: nt
-  const int b = (toff + (j * NT + (int)threadIdx.x) * 4) * 4;
+  const int b = (toff + j * GS + th * 4) * 4;
   if (VEC) {
     // VEC implies len % 4 == 0: a group is either whole or absent
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, b, 0, kNT));
@@ -346,7 +347,8 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
   const float v = key2f((uint32_t)(x >> 32));
   const float mx = lane_fc(v, 0);
   const float e = valid ? expf_cr(v - mx) : 0.0f;
-  // s = e_0 + e_1 + ... in order; the zero tail past k leaves s unchanged
+  // s = e_0 + e_1 + ... in order
+  // (unrolled over the wave: the zero tail past k leaves the sums unchanged)
   float ssum = 0.0f;
 #pragma unroll
   for (int i = 0; i < kWave; ++i) ssum = ssum + lane_fc(e, i);
@@ -371,7 +373,7 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
   const double u = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(u_lane0), 0),
                                     __builtin_amdgcn_readlane(__double2loint(u_lane0), 0));
   float r = (float)u * total;
-  float rl = 0.0f;
+  float rl = 0.0f;  // (lanes past n are not read)
 #pragma unroll
   for (int i = 0; i < kWave; ++i) {
     r = r - lane_fc(p, i);
@@ -416,6 +418,13 @@ void stream_kernel(const StreamArgs a) {
   constexpr int NV4 = kStreamVec4;
   constexpr int NE = NV4 * 4;
   constexpr int TE = NT * NE;
+  // Units of the stream.  The wave path works in chunks of kWave * NE floats,
+  // one wave each: every wave takes the chunk of tile 0, then further chunks
+  // in index order from a shared counter, so that waves which get their data
+  // early take more and all finish together.  The block path works in tiles
+  // of TE floats, all threads together.
+  constexpr int UE = WAVE ? kWave * NE : TE;  // floats per unit
+  constexpr int GS = WAVE ? kWave * 4 : NT * 4;  // floats between a thread's groups
   constexpr int PER = kWaveCap / kWave;  // wave path: buffer entries per lane
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ int smem[NW + 4];
@@ -428,6 +437,7 @@ void stream_kernel(const StreamArgs a) {
   __shared__ uint32_t s_top[kWave];  // wave path: the lane maxima of tile 0
   __shared__ int s_tile_cnt[3];
   __shared__ int s_cnt;
+  __shared__ int s_next;  // wave path: the next unclaimed chunk
   __shared__ float s_rv[NW];
   __shared__ int s_ri[NW];
   __shared__ int s_last;
@@ -445,6 +455,44 @@ void stream_kernel(const StreamArgs a) {
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wv = tid >> 6;
+  // The row's history ring and bias entries are requested first: they do not
+  // depend on the row constants, so they go out while those load, before any
+  // tile traffic.  Thread tid reads ring slots h * NT + tid and bias entry
+  // tid (the bias lists sit at a fixed stride); whether a slot lies in the
+  // penalty window, or an entry in the row's list, is decided once the row
+  // constants are in.  Requests past the ring or the list read 0 and are
+  // dropped by index.
+  constexpr int HPT = 8;  // ring slots per thread
+  constexpr int kOutOfRange = 0x7ffffff0;
+  // (the requests are unconditional: a resource of zero records makes all of
+  // them read 0, so no branch, and no wait, surrounds them)
+  const bool ring_early = a.hcap > 0 && a.hcap <= NT * HPT;
+  int hraw[HPT];
+  {
+    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(a.hist + (ring_early ? (int64_t)row * a.hcap : 0)), (short)0,
+        ring_early ? a.hcap * 4 : 0, 0x00020000);
+#pragma unroll
+    for (int h = 0; h < HPT; ++h) {
+      const int slot = h * NT + tid;
+      hraw[h] = (int)__builtin_amdgcn_raw_buffer_load_b32(hr, slot < a.hcap ? slot * 4 : kOutOfRange, 0, 0);
+    }
+  }
+  const bool bias_early = a.bstride > 0 && a.bstride <= NT;
+  int braw;
+  float bval;
+  {
+    const int off = tid < a.bstride ? tid * 4 : kOutOfRange;
+    const int64_t base = bias_early ? (int64_t)row * a.bstride : 0;
+    const int nrec = bias_early ? a.bstride * 4 : 0;
+    const __amdgpu_buffer_rsrc_t bi = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(a.bias_ids + base), (short)0, nrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t bv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a.bias_vals + base), (short)0, nrec, 0x00020000);
+    braw = (int)__builtin_amdgcn_raw_buffer_load_b32(bi, off, 0, 0);
+    bval = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bv, off, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the requests here, ahead of the row constants
   // Row constants through the scalar unit: the constant address space tells
   // the compiler that nothing in this kernel writes them.
   const RowParams P = load_const(a.rp + row);
@@ -459,12 +507,13 @@ void stream_kernel(const StreamArgs a) {
   const int lo = sl * a.L;
   const int len = (int)min((int64_t)a.L, a.V - (int64_t)lo);
   const float* __restrict__ src = a.logits + (int64_t)row * a.V + lo;
-  const int ntiles = (len + TE - 1) / TE;
   const __amdgpu_buffer_rsrc_t rs = slice_rsrc(src, len);
   f32x4 R0[NV4];  // the tile in flight
+  const int uth = WAVE ? lane : tid;        // this thread's place in a unit
+  const int u0 = WAVE ? wv : 0;             // its first unit
   auto first_tiles = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < NV4; ++j) R0[j] = load_group<NT, VEC>(rs, 0, j);
+    for (int j = 0; j < NV4; ++j) R0[j] = load_group<GS, VEC>(rs, u0 * UE, j, uth);
   };
 
   uint64_t* cand = reinterpret_cast<uint64_t*>(lds);
@@ -501,6 +550,7 @@ void stream_kernel(const StreamArgs a) {
     s_tile_cnt[2] = 0;
     s_cnt = 0;
     s_tau = 0u;
+    s_next = NW;
   }
 
   // ---- patched ids (penalties :64-74, bias :75-76) ----
@@ -510,8 +560,8 @@ void stream_kernel(const StreamArgs a) {
   if (P.pen_active && hlen > 0)
     n_hist = (int)((P.repeat_last_n > 0 && P.repeat_last_n < hlen) ? P.repeat_last_n : hlen);
   const bool has_patch = n_hist > 0 || P.bias_cnt > 0;
-  constexpr int HPT = 8;  // window ids per thread per round trip
-  const bool one_round = n_hist <= NT * HPT;
+  // the whole window from the ring slots read above (else in rounds below)
+  const bool one_round = ring_early;
   const bool bias_one = P.bias_cnt <= NT;  // one bias entry per thread at most
   const int hbase = n_hist > 0 ? (int)((hlen - n_hist) % a.hcap) : 0;
   const int32_t* __restrict__ hrow = a.hist + (int64_t)row * a.hcap;
@@ -526,25 +576,11 @@ void stream_kernel(const StreamArgs a) {
     const int loc = id - lo;
     return (id >= 0 && loc >= 0 && loc < len) ? loc : -1;
   };
-  // The window and bias reads of the common sizes go out first, as buffer
-  // loads without per-lane branches, and the first tiles are requested once
-  // they have returned: behind the tile traffic of the other workgroups these
-  // small reads would wait for several microseconds.  Entries past the window
-  // or the bias list read as 0 and are dropped by index below.
-  constexpr int kOutOfRange = 0x7ffffff0;
-  int hraw[HPT];
-  int braw = 0;
-  float bval = 0.0f;
-  if (n_hist > 0 && one_round) {
-    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int32_t*>(hrow), (short)0, a.hcap * 4, 0x00020000);
-#pragma unroll
-    for (int h = 0; h < HPT; ++h) {
-      const int i = h * NT + tid;
-      hraw[h] = (int)__builtin_amdgcn_raw_buffer_load_b32(hr, i < n_hist ? hist_slot(i) * 4 : kOutOfRange, 0, 0);
-    }
-  }
-  if (P.bias_cnt > 0 && bias_one) {
+  // Without the fixed bias stride the entries are read now, after the row
+  // constants.  The first tiles are requested once all these reads have
+  // returned: behind the tile traffic of the other workgroups such small
+  // reads wait for several microseconds.
+  if (!bias_early && P.bias_cnt > 0 && bias_one) {
     const int off = tid < P.bias_cnt ? tid * 4 : kOutOfRange;
     const __amdgpu_buffer_rsrc_t bi = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int32_t*>(a.bias_ids + P.bias_off), (short)0, P.bias_cnt * 4, 0x00020000);
@@ -554,10 +590,15 @@ void stream_kernel(const StreamArgs a) {
     bval = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bv, off, 0, 0));
   }
   // slice-local offsets of this thread's window entries (one round) and bias
-  // entry (-1: none)
+  // entry (-1: none): ring slot s holds window entry (s - hbase) mod hcap
   int hl[HPT];
 #pragma unroll
-  for (int h = 0; h < HPT; ++h) hl[h] = (one_round && h * NT + tid < n_hist) ? id_loc(hraw[h]) : -1;
+  for (int h = 0; h < HPT; ++h) {
+    const int slot = h * NT + tid;
+    int i = slot - hbase;
+    if (i < 0) i += a.hcap;
+    hl[h] = (one_round && n_hist > 0 && slot < a.hcap && i < n_hist) ? id_loc(hraw[h]) : -1;
+  }
   const int b_loc = (bias_one && tid < P.bias_cnt) ? id_loc(braw) : -1;
   const float b_val = bval;
   first_tiles();
@@ -684,18 +725,19 @@ void stream_kernel(const StreamArgs a) {
   uint32_t wtau = 0u;
   bool wovf = false;
 
-  auto process = [&](float (&v)[NE], int t) __attribute__((always_inline)) {
-    const int toff = t * TE;
-    const bool full = toff + TE <= len;  // no element of the tile lies past the slice
-    // This thread's first element of the tile, made opaque so that the
-    // per-element offsets below are formed here, not hoisted out of the tile
+  // t: the unit; first: the first unit of every thread (tile 0 of the row)
+  auto process = [&](float (&v)[NE], int t, bool first) __attribute__((always_inline)) {
+    const int toff = t * UE;
+    const bool full = toff + UE <= len;  // no element of the unit lies past the slice
+    // This thread's first element of the unit, made opaque so that the
+    // per-element offsets below are formed here, not hoisted out of the
     // loop into one register each.
-    int obase = toff + tid * 4;
+    int obase = toff + uth * 4;
     asm volatile("" : "+v"(obase));
     // With 16-byte loads len % 4 == 0, so a float4 group is wholly in or out.
-    auto loc_of = [&](int q) -> int { return obase + (q >> 2) * NT * 4 + (q & 3); };
+    auto loc_of = [&](int q) -> int { return obase + (q >> 2) * GS + (q & 3); };
     auto valid = [&](int q) -> bool {
-      const int o = obase + (q >> 2) * NT * 4;
+      const int o = obase + (q >> 2) * GS;
       return full || (VEC ? o < len : o + (q & 3) < len);
     };
     if (greedy) {
@@ -707,7 +749,7 @@ void stream_kernel(const StreamArgs a) {
         if (valid(q) && v[q] > tmx) tmx = v[q];
       // (nothing chosen yet: equal values still pick the first index, so a
       // row of -inf answers its first id)
-      if (t == 0 && tid == 0) x0raw = v[0];
+      if (first && tid == 0) x0raw = v[0];
       if (tmx > bv || (tmx == bv && bi == 0x7fffffff)) {
 #pragma unroll
         for (int q = 0; q < NE; ++q)
@@ -735,20 +777,30 @@ void stream_kernel(const StreamArgs a) {
       // (NaN passes too), so keys are formed only where some lane passes.
       uint64_t* wb = cand + (size_t)wv * kWaveCap;
       uint32_t* whist = shist + wv * kWaveBins;
-      if (t == 0) {
+      if (first) {
         // Block-wide start: every wave puts the M largest of its lanes'
         // maxima (distinct elements) into LDS, and the k-th largest of those
         // NW * M >= k real elements bounds the row's k-th largest from below.
         constexpr int M = (kWave + NW - 1) / NW;
         uint32_t lmax = 0u;  // 0: no unpatched value in this lane
+        // (every lane reads a bitmap word, clamped into the slice, so that no
+        // branch surrounds the LDS reads; the patch bits of each float4 group
+        // sit in one word)
+        uint32_t pbits[NV4];
 #pragma unroll
         for (int j = 0; j < NV4; ++j) {
-          const int o = obase + j * NT * 4;
-          const uint32_t word = has_patch && (o < len) ? bitmap[o >> 5] >> (o & 31) : 0u;
+          const int o = obase + j * GS;
+          pbits[j] = bitmap[min(o, len - 1) >> 5] >> (o & 31);
+        }
+#pragma unroll
+        for (int j = 0; j < NV4; ++j) {
+          const uint32_t pb = has_patch ? pbits[j] : 0u;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int q = 4 * j + e;
-            if (valid(q) && !((word >> e) & 1u)) lmax = max(lmax, f2key(sv[q]));
+            const uint32_t kq = f2key(sv[q]);
+            const bool ok = valid(q) & !((pb >> e) & 1u);
+            lmax = ok ? max(lmax, kq) : lmax;
           }
         }
 #pragma unroll
@@ -979,9 +1031,9 @@ void stream_kernel(const StreamArgs a) {
   };
 
   if (!ovf) {
-    // One tile is in flight while the previous one is processed: as each
-    // float4 group of tile t lands it is copied out and the same group of
-    // tile t + 1 is requested into its registers, so the memory queue stays
+    // One unit is in flight while the previous one is processed: as each
+    // float4 group of unit t lands it is copied out and the same group of the
+    // next unit is requested into its registers, so the memory queue stays
     // full.  (A workgroup can keep about one tile of requests outstanding;
     // more only stalls the issuing wave.)  The requests are unconditional
     // (past the slice they return zeros without reading memory) and the loop
@@ -989,7 +1041,16 @@ void stream_kernel(const StreamArgs a) {
     // request order exactly.  ovf and wovf agree over the wave; the scalar
     // read makes that visible.
     auto stop = [&]() -> bool { return __builtin_amdgcn_readfirstlane((int)(ovf || wovf)) != 0; };
-    for (int t = 0; t < ntiles; ++t) {
+    const int nunits = (len + UE - 1) / UE;
+    int t = u0;
+    for (bool first = true;; first = false) {
+      int tn = t + 1;
+      if constexpr (WAVE) {
+        // the next chunk for this wave
+        int c = 0;
+        if (lane == 0) c = atomicAdd(&s_next, 1);
+        tn = __builtin_amdgcn_readfirstlane(c);
+      }
       float v[NE];
 #pragma unroll
       for (int j = 0; j < NV4; ++j) {
@@ -997,15 +1058,13 @@ void stream_kernel(const StreamArgs a) {
         v[4 * j + 1] = R0[j].y;
         v[4 * j + 2] = R0[j].z;
         v[4 * j + 3] = R0[j].w;
-        R0[j] = load_group<NT, VEC>(rs, (t + 1) * TE, j);
+        R0[j] = load_group<GS, VEC>(rs, tn * UE, j, uth);
       }
-      process(v, t);
-      if (stop()) break;
+      process(v, t, first);
+      if (stop() || tn >= nunits) break;
+      t = tn;
     }
   }
-  // the patched ids' original logits (read back after the stream, likely from
-  // cache) and their final values: penalties then bias (:71-76), then
-  // temperature (:80-81) on the sampling rows
   // The final value of patched slot p from its original logit: penalties then
   // bias (:71-76), then temperature (:80-81) on the sampling rows.
   auto patched_final = [&](int p, float v, uint32_t fl) -> float {
@@ -1077,11 +1136,9 @@ void stream_kernel(const StreamArgs a) {
       s_wt[wv] = wtau;
     }
     __syncthreads();  // every wave's stream, captures and offers are in
-    uint32_t tau_all = 0u;
-    for (int w = 0; w < NW; ++w) {
-      ovf = ovf || s_wn[w] < 0;
-      tau_all = max(tau_all, s_wt[w]);
-    }
+    // lane w reads wave w's record
+    ovf = ovf || __ballot(lane < NW && s_wn[min(lane, NW - 1)] < 0) != 0ull;
+    const uint32_t tau_all = wave_max_u32(lane < NW ? s_wt[min(lane, NW - 1)] : 0u);
     ent = cand + a.ccap;  // free: holds NW * kWaveCap entries and more
     if (!ovf) {
       const uint32_t te = max(tau_all, wave_kth_largest(lane < NW * M ? s_top[lane] : 0u, k));
@@ -1124,10 +1181,14 @@ void stream_kernel(const StreamArgs a) {
       const uint64_t e1 = lane + kWave < N ? ent[lane + kWave] : 0ull;
       const uint32_t k0 = (uint32_t)(e0 >> 32), k1 = (uint32_t)(e1 >> 32);
       uint32_t T = 0u;
+      if (N <= kWave) {
+        T = wave_kth_largest(k0, k);
+      } else {
 #pragma unroll
-      for (int b = 31; b >= 0; --b) {
-        const uint32_t c = T | (1u << b);
-        if (__popcll(__ballot(k0 >= c)) + __popcll(__ballot(k1 >= c)) >= k) T = c;
+        for (int b = 31; b >= 0; --b) {
+          const uint32_t c = T | (1u << b);
+          if (__popcll(__ballot(k0 >= c)) + __popcll(__ballot(k1 >= c)) >= k) T = c;
+        }
       }
       const int ge = __popcll(__ballot(lane < N && k0 >= T)) + __popcll(__ballot(lane + kWave < N && k1 >= T));
       if (ge == k) {
