@@ -122,6 +122,8 @@ struct nls_sampler {
   uint64_t* rng = nullptr;
   int32_t* generic_list = nullptr;
   int32_t* generic_count = nullptr;  // [2]
+  uint32_t* done = nullptr;          // workgroups finished (whole-row rows served inline)
+  int gen_inline = 0;
   uint32_t* gen_scratch = nullptr;
   int64_t gen_vpad = 0;
   int32_t* stage_ids = nullptr;
@@ -144,6 +146,7 @@ struct nls_sampler {
     dfree(rng);
     dfree(generic_list);
     dfree(generic_count);
+    dfree(done);
     dfree(gen_scratch);
     dfree(stage_ids);
     dfree(tmp_logits);
@@ -422,6 +425,8 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   // Without full-sort rows the whole-row kernel only serves the rare row the
   // streaming kernel hands on: one workgroup keeps that launch cheap.
   s->plan.gen_blocks = any_full ? std::min(B, 256) : 1;
+  // ... and then its last workgroup serves that row itself, saving a launch
+  s->gen_inline = any_full ? 0 : 1;
 
   int rc = NLS_OK;
   auto fail = [&](int code) {
@@ -462,6 +467,7 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   if ((rc = dalloc(&s->rng, (size_t)2 * B))) return fail(rc);
   if ((rc = dalloc(&s->generic_list, B))) return fail(rc);
   if ((rc = dalloc(&s->generic_count, 2))) return fail(rc);
+  if ((rc = dalloc(&s->done, 1))) return fail(rc);
   int64_t vpad = 1;
   while (vpad < vocab) vpad <<= 1;
   s->gen_vpad = vpad;
@@ -486,6 +492,8 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   if ((e = up(s->rng, rng_h.data(), sizeof(NimRand) * B)) != hipSuccess)
     return fail(hip_fail(e, "upload rng"));
   if ((e = hipMemsetAsync(s->arrive, 0, sizeof(uint32_t) * B, st)) != hipSuccess)
+    return fail(hip_fail(e, "clear counters"));
+  if ((e = hipMemsetAsync(s->done, 0, sizeof(uint32_t), st)) != hipSuccess)
     return fail(hip_fail(e, "clear counters"));
   if ((e = hipMemsetAsync(s->generic_count, 0, sizeof(int32_t) * 2, st)) != hipSuccess)
     return fail(hip_fail(e, "clear counters"));
@@ -634,6 +642,9 @@ int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t
   ga.rng = s->rng;
   ga.out = d_out;
   ga.dbg = dp;
+  a.gen_inline = s->gen_inline;
+  a.done = s->done;
+  a.ga = ga;
   LaunchPlan lp = s->plan;
   lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
   hipEvent_t e0 = s->prof_start, e1 = s->prof_stop;

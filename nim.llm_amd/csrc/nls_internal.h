@@ -71,6 +71,26 @@ struct DebugPtrs {
   int32_t cap;
 };
 
+struct GenericArgs {
+  const float* logits;
+  int64_t V;
+  const RowParams* rp;
+  const int32_t* hist;
+  const int64_t* hist_len;
+  int hcap;
+  const int32_t* bias_ids;
+  const float* bias_vals;
+  const int32_t* generic_list;
+  const int32_t* generic_count;  // this call's counter
+  int32_t* next_count;           // the next call's counter, zeroed here
+  uint32_t* scratch;             // per workgroup: 5 x vpad uint32
+  int64_t vpad;
+  const double* d_u;
+  uint64_t* rng;
+  int32_t* out;
+  DebugPtrs dbg;
+};
+
 struct StreamArgs {
   const float* logits;
   int64_t V;
@@ -104,27 +124,13 @@ struct StreamArgs {
   int32_t* generic_list;
   int32_t* generic_count;  // this call's counter (zero on entry)
   DebugPtrs dbg;
+  // gen_inline: rows handed on are served by the last workgroup of this
+  // kernel (counted in `done`, zero between calls) instead of a second launch
+  int gen_inline;
+  uint32_t* done;
+  GenericArgs ga;
 };
 
-struct GenericArgs {
-  const float* logits;
-  int64_t V;
-  const RowParams* rp;
-  const int32_t* hist;
-  const int64_t* hist_len;
-  int hcap;
-  const int32_t* bias_ids;
-  const float* bias_vals;
-  const int32_t* generic_list;
-  const int32_t* generic_count;  // this call's counter
-  int32_t* next_count;           // the next call's counter, zeroed here
-  uint32_t* scratch;             // per workgroup: 5 x vpad uint32
-  int64_t vpad;
-  const double* d_u;
-  uint64_t* rng;
-  int32_t* out;
-  DebugPtrs dbg;
-};
 
 struct LaunchPlan {
   int nt;        // streaming workgroup size: 256 or 1024

@@ -224,8 +224,9 @@ __device__ __forceinline__ T load_agent(const T* p) {
 }
 
 __device__ __forceinline__ void push_generic(int32_t* list, int32_t* count, int row) {
-  list[atomicAdd(count, 1)] = row;
+  store_agent(&list[atomicAdd(count, 1)], row);
 }
+
 
 // ---------------------------------------------------------------------------
 // Heap-path members (sampler.nim:85-95) from a candidate set
@@ -395,6 +396,11 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
   }
 }
 
+template <int NT>
+__device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int nw, int count, uint32_t* wcnt,
+                                             uint32_t* dbase, uint32_t* drun, int* smem, double* s_u_p,
+                                             int* s_i, float* s_rv, int* s_ri);
+
 // ---------------------------------------------------------------------------
 // 1. stream_kernel
 // ---------------------------------------------------------------------------
@@ -437,1024 +443,1052 @@ void stream_kernel(const StreamArgs a) {
   __shared__ uint32_t s_top[kWave];  // wave path: the lane maxima of tile 0
   __shared__ int s_tile_cnt[3];
   __shared__ int s_cnt;
-  __shared__ int s_next;  // wave path: the next unclaimed chunk
+  __shared__ int s_next;  // wave path: the next unclaimed chunk (after the first two of every wave)
   __shared__ float s_rv[NW];
   __shared__ int s_ri[NW];
   __shared__ int s_last;
   __shared__ double s_u;
 
-  int row, sl;
-  if (a.xcd_map) {
-    const int x = (int)(blockIdx.x & 7u), slot = (int)(blockIdx.x >> 3);
-    row = (slot / a.S) * 8 + x;
-    sl = slot - (slot / a.S) * a.S;
-  } else {
-    row = (int)blockIdx.x / a.S;
-    sl = (int)blockIdx.x - row * a.S;
-  }
-  const int tid = threadIdx.x;
-  const int lane = lane_id();
-  const int wv = tid >> 6;
-  // The row's history ring and bias entries are requested first: they do not
-  // depend on the row constants, so they go out while those load, before any
-  // tile traffic.  Thread tid reads ring slots h * NT + tid and bias entry
-  // tid (the bias lists sit at a fixed stride); whether a slot lies in the
-  // penalty window, or an entry in the row's list, is decided once the row
-  // constants are in.  Requests past the ring or the list read 0 and are
-  // dropped by index.
-  constexpr int HPT = 8;  // ring slots per thread
-  constexpr int kOutOfRange = 0x7ffffff0;
-  // (the requests are unconditional: a resource of zero records makes all of
-  // them read 0, so no branch, and no wait, surrounds them)
-  const bool ring_early = a.hcap > 0 && a.hcap <= NT * HPT;
-  int hraw[HPT];
-  {
-    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int32_t*>(a.hist + (ring_early ? (int64_t)row * a.hcap : 0)), (short)0,
-        ring_early ? a.hcap * 4 : 0, 0x00020000);
-#pragma unroll
+  // The row's work; every exit of it leads to the final section below.
+  auto run = [&]() __attribute__((always_inline)) {
+    int row, sl;
+    if (a.xcd_map) {
+      const int x = (int)(blockIdx.x & 7u), slot = (int)(blockIdx.x >> 3);
+      row = (slot / a.S) * 8 + x;
+      sl = slot - (slot / a.S) * a.S;
+    } else {
+      row = (int)blockIdx.x / a.S;
+      sl = (int)blockIdx.x - row * a.S;
+    }
+    const int tid = threadIdx.x;
+    const int lane = lane_id();
+    const int wv = tid >> 6;
+    // The row's history ring and bias entries are requested first: they do not
+    // depend on the row constants, so they go out while those load, before any
+    // tile traffic.  Thread tid reads ring slots h * NT + tid and bias entry
+    // tid (the bias lists sit at a fixed stride); whether a slot lies in the
+    // penalty window, or an entry in the row's list, is decided once the row
+    // constants are in.  Requests past the ring or the list read 0 and are
+    // dropped by index.
+    constexpr int HPT = 8;  // ring slots per thread
+    constexpr int kOutOfRange = 0x7ffffff0;
+    // (the requests are unconditional: a resource of zero records makes all of
+    // them read 0, so no branch, and no wait, surrounds them)
+    const bool ring_early = a.hcap > 0 && a.hcap <= NT * HPT;
+    int hraw[HPT];
+    {
+      const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<int32_t*>(a.hist + (ring_early ? (int64_t)row * a.hcap : 0)), (short)0,
+          ring_early ? a.hcap * 4 : 0, 0x00020000);
+  #pragma unroll
+      for (int h = 0; h < HPT; ++h) {
+        const int slot = h * NT + tid;
+        hraw[h] = (int)__builtin_amdgcn_raw_buffer_load_b32(hr, slot < a.hcap ? slot * 4 : kOutOfRange, 0, 0);
+      }
+    }
+    const bool bias_early = a.bstride > 0 && a.bstride <= NT;
+    int braw;
+    float bval;
+    {
+      const int off = tid < a.bstride ? tid * 4 : kOutOfRange;
+      const int64_t base = bias_early ? (int64_t)row * a.bstride : 0;
+      const int nrec = bias_early ? a.bstride * 4 : 0;
+      const __amdgpu_buffer_rsrc_t bi = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<int32_t*>(a.bias_ids + base), (short)0, nrec, 0x00020000);
+      const __amdgpu_buffer_rsrc_t bv = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(a.bias_vals + base), (short)0, nrec, 0x00020000);
+      braw = (int)__builtin_amdgcn_raw_buffer_load_b32(bi, off, 0, 0);
+      bval = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bv, off, 0, 0));
+    }
+    // The first unit of the slice follows at once (it needs no row constant);
+    // the reads above return before it.
+    const int lo = sl * a.L;
+    const int len = (int)min((int64_t)a.L, a.V - (int64_t)lo);
+    const float* __restrict__ src = a.logits + (int64_t)row * a.V + lo;
+    const __amdgpu_buffer_rsrc_t rs = slice_rsrc(src, len);
+    f32x4 R0[NV4];  // the unit in flight
+    const int uth = WAVE ? lane : tid;        // this thread's place in a unit
+    const int u0 = WAVE ? wv : 0;             // its first unit
+  #pragma unroll
+    for (int j = 0; j < NV4; ++j) R0[j] = load_group<GS, VEC>(rs, u0 * UE, j, uth);
+    __builtin_amdgcn_sched_barrier(0);  // keep the requests here, ahead of the row constants
+    // Row constants through the scalar unit: the constant address space tells
+    // the compiler that nothing in this kernel writes them.
+    const RowParams P = load_const(a.rp + row);
+    const int64_t hlen = load_const(a.hist_len + row);
+    if (P.mode == kModeFull || !P.fast) {
+      if (sl == 0 && tid == 0) push_generic(a.generic_list, a.generic_count, row);
+      return;
+    }
+    const bool greedy = P.mode == kModeGreedy;
+    const bool topk = P.mode == kModeTopK;
+    const int k = P.k;
+
+    uint64_t* cand = reinterpret_cast<uint64_t*>(lds);
+    unsigned char* regA = lds + a.offA;
+    uint32_t* bitmap = reinterpret_cast<uint32_t*>(regA);
+    uint16_t* wpre = reinterpret_cast<uint16_t*>(regA + (size_t)a.nwords * 4);
+    float* pfin = reinterpret_cast<float*>(regA + (size_t)a.nwords * 4 + (((size_t)a.nwords * 2 + 3) & ~(size_t)3));
+    float* pbias = pfin + a.pcap;
+    uint32_t* pflag = reinterpret_cast<uint32_t*>(pbias + a.pcap);  // flags | count << 2
+    int32_t* pid = reinterpret_cast<int32_t*>(pflag + a.pcap);
+    // patch slot of a patched slice-local offset: patched offsets are numbered
+    // in index order (wpre holds the count before each bitmap word)
+    auto slot_of = [&](int loc) -> int {
+      const int w = loc >> 5;
+      return wpre[w] + __popc(bitmap[w] & ((1u << (loc & 31)) - 1u));
+    };
+
+    // the row's uniform or RNG state, read now (scalar loads) so the tail
+    // does not wait
+    double u_in = 0.0;
+    uint64_t st0 = 0ull, st1 = 0ull;
+    if (!greedy) {
+      if (a.d_u) {
+        u_in = load_const(a.d_u + row);
+      } else {
+        st0 = load_const(a.rng + 2 * row);
+        st1 = load_const(a.rng + 2 * row + 1);
+      }
+    }
+    for (int q = tid; q < kHistWords; q += NT) shist[q] = 0u;  // the selects need it zeroed
+    if (tid == 0) {
+      s_tile_cnt[0] = 0;
+      s_tile_cnt[1] = 0;
+      s_tile_cnt[2] = 0;
+      s_cnt = 0;
+      s_tau = 0u;
+      s_next = 2 * NW;
+    }
+
+    // ---- patched ids (penalties :64-74, bias :75-76) ----
+    bool ovf = false;
+    int npatch = 0;
+    int n_hist = 0;
+    if (P.pen_active && hlen > 0)
+      n_hist = (int)((P.repeat_last_n > 0 && P.repeat_last_n < hlen) ? P.repeat_last_n : hlen);
+    const bool has_patch = n_hist > 0 || P.bias_cnt > 0;
+    // the whole window from the ring slots read above (else in rounds below)
+    const bool one_round = ring_early;
+    const bool bias_one = P.bias_cnt <= NT;  // one bias entry per thread at most
+    const int hbase = n_hist > 0 ? (int)((hlen - n_hist) % a.hcap) : 0;
+    const int32_t* __restrict__ hrow = a.hist + (int64_t)row * a.hcap;
+    // History slot of window entry i (the ring wraps at hcap).
+    auto hist_slot = [&](int i) -> int {
+      const int slot = hbase + i;
+      return slot >= a.hcap ? slot - a.hcap : slot;
+    };
+    // Slice-local offset of a window id, or -1 when it is not in the slice (ids
+    // outside [0, V) are stored as -1 by accept).
+    auto id_loc = [&](int id) -> int {
+      const int loc = id - lo;
+      return (id >= 0 && loc >= 0 && loc < len) ? loc : -1;
+    };
+    // Without the fixed bias stride the entries are read now, after the row
+    // constants (and behind the first unit's traffic).
+    if (!bias_early && P.bias_cnt > 0 && bias_one) {
+      const int off = tid < P.bias_cnt ? tid * 4 : kOutOfRange;
+      const __amdgpu_buffer_rsrc_t bi = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<int32_t*>(a.bias_ids + P.bias_off), (short)0, P.bias_cnt * 4, 0x00020000);
+      const __amdgpu_buffer_rsrc_t bv = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(a.bias_vals + P.bias_off), (short)0, P.bias_cnt * 4, 0x00020000);
+      braw = (int)__builtin_amdgcn_raw_buffer_load_b32(bi, off, 0, 0);
+      bval = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bv, off, 0, 0));
+    }
+    // slice-local offsets of this thread's window entries (one round) and bias
+    // entry (-1: none): ring slot s holds window entry (s - hbase) mod hcap
+    int hl[HPT];
+  #pragma unroll
     for (int h = 0; h < HPT; ++h) {
       const int slot = h * NT + tid;
-      hraw[h] = (int)__builtin_amdgcn_raw_buffer_load_b32(hr, slot < a.hcap ? slot * 4 : kOutOfRange, 0, 0);
+      int i = slot - hbase;
+      if (i < 0) i += a.hcap;
+      hl[h] = (one_round && n_hist > 0 && slot < a.hcap && i < n_hist) ? id_loc(hraw[h]) : -1;
     }
-  }
-  const bool bias_early = a.bstride > 0 && a.bstride <= NT;
-  int braw;
-  float bval;
-  {
-    const int off = tid < a.bstride ? tid * 4 : kOutOfRange;
-    const int64_t base = bias_early ? (int64_t)row * a.bstride : 0;
-    const int nrec = bias_early ? a.bstride * 4 : 0;
-    const __amdgpu_buffer_rsrc_t bi = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int32_t*>(a.bias_ids + base), (short)0, nrec, 0x00020000);
-    const __amdgpu_buffer_rsrc_t bv = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(a.bias_vals + base), (short)0, nrec, 0x00020000);
-    braw = (int)__builtin_amdgcn_raw_buffer_load_b32(bi, off, 0, 0);
-    bval = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bv, off, 0, 0));
-  }
-  __builtin_amdgcn_sched_barrier(0);  // keep the requests here, ahead of the row constants
-  // Row constants through the scalar unit: the constant address space tells
-  // the compiler that nothing in this kernel writes them.
-  const RowParams P = load_const(a.rp + row);
-  const int64_t hlen = load_const(a.hist_len + row);
-  if (P.mode == kModeFull || !P.fast) {
-    if (sl == 0 && tid == 0) push_generic(a.generic_list, a.generic_count, row);
-    return;
-  }
-  const bool greedy = P.mode == kModeGreedy;
-  const bool topk = P.mode == kModeTopK;
-  const int k = P.k;
-  const int lo = sl * a.L;
-  const int len = (int)min((int64_t)a.L, a.V - (int64_t)lo);
-  const float* __restrict__ src = a.logits + (int64_t)row * a.V + lo;
-  const __amdgpu_buffer_rsrc_t rs = slice_rsrc(src, len);
-  f32x4 R0[NV4];  // the tile in flight
-  const int uth = WAVE ? lane : tid;        // this thread's place in a unit
-  const int u0 = WAVE ? wv : 0;             // its first unit
-  auto first_tiles = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < NV4; ++j) R0[j] = load_group<GS, VEC>(rs, u0 * UE, j, uth);
-  };
-
-  uint64_t* cand = reinterpret_cast<uint64_t*>(lds);
-  unsigned char* regA = lds + a.offA;
-  uint32_t* bitmap = reinterpret_cast<uint32_t*>(regA);
-  uint16_t* wpre = reinterpret_cast<uint16_t*>(regA + (size_t)a.nwords * 4);
-  float* pfin = reinterpret_cast<float*>(regA + (size_t)a.nwords * 4 + (((size_t)a.nwords * 2 + 3) & ~(size_t)3));
-  float* pbias = pfin + a.pcap;
-  uint32_t* pflag = reinterpret_cast<uint32_t*>(pbias + a.pcap);  // flags | count << 2
-  int32_t* pid = reinterpret_cast<int32_t*>(pflag + a.pcap);
-  // patch slot of a patched slice-local offset: patched offsets are numbered
-  // in index order (wpre holds the count before each bitmap word)
-  auto slot_of = [&](int loc) -> int {
-    const int w = loc >> 5;
-    return wpre[w] + __popc(bitmap[w] & ((1u << (loc & 31)) - 1u));
-  };
-
-  // the row's uniform or RNG state, read now (scalar loads) so the tail
-  // does not wait
-  double u_in = 0.0;
-  uint64_t st0 = 0ull, st1 = 0ull;
-  if (!greedy) {
-    if (a.d_u) {
-      u_in = load_const(a.d_u + row);
-    } else {
-      st0 = load_const(a.rng + 2 * row);
-      st1 = load_const(a.rng + 2 * row + 1);
-    }
-  }
-  for (int q = tid; q < kHistWords; q += NT) shist[q] = 0u;  // the selects need it zeroed
-  if (tid == 0) {
-    s_tile_cnt[0] = 0;
-    s_tile_cnt[1] = 0;
-    s_tile_cnt[2] = 0;
-    s_cnt = 0;
-    s_tau = 0u;
-    s_next = NW;
-  }
-
-  // ---- patched ids (penalties :64-74, bias :75-76) ----
-  bool ovf = false;
-  int npatch = 0;
-  int n_hist = 0;
-  if (P.pen_active && hlen > 0)
-    n_hist = (int)((P.repeat_last_n > 0 && P.repeat_last_n < hlen) ? P.repeat_last_n : hlen);
-  const bool has_patch = n_hist > 0 || P.bias_cnt > 0;
-  // the whole window from the ring slots read above (else in rounds below)
-  const bool one_round = ring_early;
-  const bool bias_one = P.bias_cnt <= NT;  // one bias entry per thread at most
-  const int hbase = n_hist > 0 ? (int)((hlen - n_hist) % a.hcap) : 0;
-  const int32_t* __restrict__ hrow = a.hist + (int64_t)row * a.hcap;
-  // History slot of window entry i (the ring wraps at hcap).
-  auto hist_slot = [&](int i) -> int {
-    const int slot = hbase + i;
-    return slot >= a.hcap ? slot - a.hcap : slot;
-  };
-  // Slice-local offset of a window id, or -1 when it is not in the slice (ids
-  // outside [0, V) are stored as -1 by accept).
-  auto id_loc = [&](int id) -> int {
-    const int loc = id - lo;
-    return (id >= 0 && loc >= 0 && loc < len) ? loc : -1;
-  };
-  // Without the fixed bias stride the entries are read now, after the row
-  // constants.  The first tiles are requested once all these reads have
-  // returned: behind the tile traffic of the other workgroups such small
-  // reads wait for several microseconds.
-  if (!bias_early && P.bias_cnt > 0 && bias_one) {
-    const int off = tid < P.bias_cnt ? tid * 4 : kOutOfRange;
-    const __amdgpu_buffer_rsrc_t bi = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int32_t*>(a.bias_ids + P.bias_off), (short)0, P.bias_cnt * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t bv = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(a.bias_vals + P.bias_off), (short)0, P.bias_cnt * 4, 0x00020000);
-    braw = (int)__builtin_amdgcn_raw_buffer_load_b32(bi, off, 0, 0);
-    bval = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bv, off, 0, 0));
-  }
-  // slice-local offsets of this thread's window entries (one round) and bias
-  // entry (-1: none): ring slot s holds window entry (s - hbase) mod hcap
-  int hl[HPT];
-#pragma unroll
-  for (int h = 0; h < HPT; ++h) {
-    const int slot = h * NT + tid;
-    int i = slot - hbase;
-    if (i < 0) i += a.hcap;
-    hl[h] = (one_round && n_hist > 0 && slot < a.hcap && i < n_hist) ? id_loc(hraw[h]) : -1;
-  }
-  const int b_loc = (bias_one && tid < P.bias_cnt) ? id_loc(braw) : -1;
-  const float b_val = bval;
-  first_tiles();
-  if (has_patch) {
-    const int nw = (len + 31) >> 5;
-    // fn(loc) for every window entry of the slice (loc < 0: not in it)
-    auto for_window = [&](auto fn) __attribute__((always_inline)) {
-      if (one_round) {
-#pragma unroll
-        for (int h = 0; h < HPT; ++h) fn(hl[h]);
-      } else {
-        for (int b0 = 0; b0 < n_hist; b0 += NT * HPT) {
-          int l[HPT];
-#pragma unroll
-          for (int h = 0; h < HPT; ++h) {
-            const int i = b0 + h * NT + tid;
-            l[h] = (i < n_hist) ? id_loc(hrow[hist_slot(i)]) : -1;
+    const int b_loc = (bias_one && tid < P.bias_cnt) ? id_loc(braw) : -1;
+    const float b_val = bval;
+    if (has_patch) {
+      const int nw = (len + 31) >> 5;
+      // fn(loc) for every window entry of the slice (loc < 0: not in it)
+      auto for_window = [&](auto fn) __attribute__((always_inline)) {
+        if (one_round) {
+  #pragma unroll
+          for (int h = 0; h < HPT; ++h) fn(hl[h]);
+        } else {
+          for (int b0 = 0; b0 < n_hist; b0 += NT * HPT) {
+            int l[HPT];
+  #pragma unroll
+            for (int h = 0; h < HPT; ++h) {
+              const int i = b0 + h * NT + tid;
+              l[h] = (i < n_hist) ? id_loc(hrow[hist_slot(i)]) : -1;
+            }
+  #pragma unroll
+            for (int h = 0; h < HPT; ++h) fn(l[h]);
           }
-#pragma unroll
-          for (int h = 0; h < HPT; ++h) fn(l[h]);
         }
-      }
-    };
-    for (int w = tid; w < nw; w += NT) bitmap[w] = 0u;
-    __syncthreads();
-    for_window([&](int loc) {
-      if (loc >= 0) atomicOr(&bitmap[loc >> 5], 1u << (loc & 31));
-    });
-    if (bias_one) {
-      if (b_loc >= 0) atomicOr(&bitmap[b_loc >> 5], 1u << (b_loc & 31));
-    } else {
-      for (int j = tid; j < P.bias_cnt; j += NT) {
-        const int loc = a.bias_ids[P.bias_off + j] - lo;
-        if (loc >= 0 && loc < len) atomicOr(&bitmap[loc >> 5], 1u << (loc & 31));
-      }
-    }
-    __syncthreads();
-    const int wpt = (nw + NT - 1) / NT;
-    const int w0 = min(nw, tid * wpt), w1 = min(nw, w0 + wpt);
-    int c = 0;
-    for (int w = w0; w < w1; ++w) c += __popc(bitmap[w]);
-    int pre = block_excl_scan<NT>(c, smem, npatch);
-    if (npatch > a.pcap) {
-      ovf = true;  // uniform
-    } else {
-      for (int w = w0; w < w1; ++w) {
-        wpre[w] = (uint16_t)pre;
-        pre += __popc(bitmap[w]);
-      }
-      for (int p = tid; p < npatch; p += NT) {
-        pbias[p] = 0.0f;
-        pflag[p] = 0u;
-      }
-      __syncthreads();
-      // every writer of pid[p] stores the same value
-      for_window([&](int loc) {
-        if (loc >= 0) {
-          const int p = slot_of(loc);
-          atomicAdd(&pflag[p], 1u << kPatchCountShift);  // the window count
-          pid[p] = lo + loc;
-        }
-      });
-      auto put_bias = [&](int loc, float val) {
-        const int p = slot_of(loc);
-        pbias[p] = val;  // bias ids are unique per row
-        atomicOr(&pflag[p], (uint32_t)kPatchBias | (!(val <= 0.0f) ? (uint32_t)kPatchRise : 0u));
-        pid[p] = lo + loc;
       };
+      for (int w = tid; w < nw; w += NT) bitmap[w] = 0u;
+      __syncthreads();
+      for_window([&](int loc) {
+        if (loc >= 0) atomicOr(&bitmap[loc >> 5], 1u << (loc & 31));
+      });
       if (bias_one) {
-        if (b_loc >= 0) put_bias(b_loc, b_val);
+        if (b_loc >= 0) atomicOr(&bitmap[b_loc >> 5], 1u << (b_loc & 31));
       } else {
         for (int j = tid; j < P.bias_cnt; j += NT) {
           const int loc = a.bias_ids[P.bias_off + j] - lo;
-          if (loc >= 0 && loc < len) put_bias(loc, a.bias_vals[P.bias_off + j]);
+          if (loc >= 0 && loc < len) atomicOr(&bitmap[loc >> 5], 1u << (loc & 31));
         }
       }
-    }
-  }
-  __syncthreads();
-  auto patched = [&](int loc) -> bool {  // loc: slice-local offset
-    return has_patch && ((bitmap[loc >> 5] >> (loc & 31)) & 1u);
-  };
-  // A patched logit met at or above the threshold keeps its original value
-  // for the final pass.  One that stays below it cannot be a member unless
-  // its patch can raise it (a positive or NaN bias, or penalties of the
-  // raising sign): every other patch only lowers a logit (division by
-  // rp >= 1 of a positive value, multiplication of a non-positive one,
-  // subtraction of count * frequency + presence >= 0, a bias <= 0), and so
-  // does the temperature's positive factor, in float rounding too.
-  auto capture = [&](int loc, float raw) {
-    const int p = slot_of(loc);
-    pfin[p] = raw;
-    atomicOr(&pflag[p], (uint32_t)kPatchSeen);
-  };
-  const bool row_rise =
-      (P.rp_active && !(P.rp32 >= 1.0f)) || !(P.freq >= 0.0) || !(P.pres >= 0.0);
-  auto may_rise = [&](uint32_t fl) -> bool {
-    return (fl & kPatchRise) || (row_rise && (fl >> kPatchCountShift) > 0);
-  };
-  // The original logits of the ids whose patch may raise them are requested
-  // now (slots tid + r * NT; the rest, if any, are read after the stream):
-  // requests past the slice return 0 without reading memory, so the slots
-  // without such a patch need no branch around the load.
-  constexpr int RPT = 2;
-  float rraw[RPT];
-#pragma unroll
-  for (int r = 0; r < RPT; ++r) {
-    const int p = tid + r * NT;
-    const bool want = !ovf && p < npatch && may_rise(pflag[p]);
-    rraw[r] = __builtin_bit_cast(
-        float, __builtin_amdgcn_raw_buffer_load_b32(rs, want ? (pid[p] - lo) * 4 : kOutOfRange, 0, 0));
-  }
-  // greedy rows: the original logit at index 0 (argmax stays at 0 when the
-  // final value there is NaN), read from the first tile
-  float x0raw = 0.0f;
-
-  // ---- the stream ----
-  float bv = -__builtin_inff();
-  int bi = 0x7fffffff;
-  int buf_n = 0, cur = 0;
-  uint32_t tau = 0u;
-  // wave path (k <= 64): this wave's buffer count, threshold and overflow
-  int wn = 0;
-  uint32_t wtau = 0u;
-  bool wovf = false;
-
-  // t: the unit; first: the first unit of every thread (tile 0 of the row)
-  auto process = [&](float (&v)[NE], int t, bool first) __attribute__((always_inline)) {
-    const int toff = t * UE;
-    const bool full = toff + UE <= len;  // no element of the unit lies past the slice
-    // This thread's first element of the unit, made opaque so that the
-    // per-element offsets below are formed here, not hoisted out of the
-    // loop into one register each.
-    int obase = toff + uth * 4;
-    asm volatile("" : "+v"(obase));
-    // With 16-byte loads len % 4 == 0, so a float4 group is wholly in or out.
-    auto loc_of = [&](int q) -> int { return obase + (q >> 2) * GS + (q & 3); };
-    auto valid = [&](int q) -> bool {
-      const int o = obase + (q >> 2) * GS;
-      return full || (VEC ? o < len : o + (q & 3) < len);
-    };
-    if (greedy) {
-      // argmax (:45-49): only a lane whose tile maximum beats its running
-      // best walks the tile in index order (strict >, so the first index wins)
-      float tmx = -__builtin_inff();
-#pragma unroll
-      for (int q = 0; q < NE; ++q)
-        if (valid(q) && v[q] > tmx) tmx = v[q];
-      // (nothing chosen yet: equal values still pick the first index, so a
-      // row of -inf answers its first id)
-      if (first && tid == 0) x0raw = v[0];
-      if (tmx > bv || (tmx == bv && bi == 0x7fffffff)) {
-#pragma unroll
-        for (int q = 0; q < NE; ++q)
-          if (valid(q)) {
-            if (patched(loc_of(q)))
-              capture(loc_of(q), v[q]);
-            else
-              argmax_merge(bv, bi, v[q], lo + loc_of(q));
-          }
-      }
-      return;
-    }
-    // temperature (:80-81); v keeps the original logits for the patched ids
-    // met on the way
-    float sv[NE];
-    {
-      const float invT = P.invT;
-#pragma unroll
-      for (int q = 0; q < NE; ++q) sv[q] = v[q] * invT;
-    }
-    auto gid = [&](int q) -> uint32_t { return (uint32_t)(lo + loc_of(q)); };
-    if constexpr (WAVE) {
-      // ---- wave path: this wave's own buffer, no barrier ----
-      // Prefilter in the float domain: key(v) >= t implies !(v < key2f(t))
-      // (NaN passes too), so keys are formed only where some lane passes.
-      uint64_t* wb = cand + (size_t)wv * kWaveCap;
-      uint32_t* whist = shist + wv * kWaveBins;
-      if (first) {
-        // Block-wide start: every wave puts the M largest of its lanes'
-        // maxima (distinct elements) into LDS, and the k-th largest of those
-        // NW * M >= k real elements bounds the row's k-th largest from below.
-        constexpr int M = (kWave + NW - 1) / NW;
-        uint32_t lmax = 0u;  // 0: no unpatched value in this lane
-        // (every lane reads a bitmap word, clamped into the slice, so that no
-        // branch surrounds the LDS reads; the patch bits of each float4 group
-        // sit in one word)
-        uint32_t pbits[NV4];
-#pragma unroll
-        for (int j = 0; j < NV4; ++j) {
-          const int o = obase + j * GS;
-          pbits[j] = bitmap[min(o, len - 1) >> 5] >> (o & 31);
+      __syncthreads();
+      const int wpt = (nw + NT - 1) / NT;
+      const int w0 = min(nw, tid * wpt), w1 = min(nw, w0 + wpt);
+      int c = 0;
+      for (int w = w0; w < w1; ++w) c += __popc(bitmap[w]);
+      int pre = block_excl_scan<NT>(c, smem, npatch);
+      if (npatch > a.pcap) {
+        ovf = true;  // uniform
+      } else {
+        for (int w = w0; w < w1; ++w) {
+          wpre[w] = (uint16_t)pre;
+          pre += __popc(bitmap[w]);
         }
-#pragma unroll
-        for (int j = 0; j < NV4; ++j) {
-          const uint32_t pb = has_patch ? pbits[j] : 0u;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int q = 4 * j + e;
-            const uint32_t kq = f2key(sv[q]);
-            const bool ok = valid(q) & !((pb >> e) & 1u);
-            lmax = ok ? max(lmax, kq) : lmax;
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < M; ++i) {
-          const uint32_t m = wave_max_u32(lmax);
-          const uint64_t at = __ballot(lmax == m);
-          if (lane == __ffsll((unsigned long long)at) - 1) lmax = 0u;
-          if (lane == 0) s_top[wv * M + i] = m;
+        for (int p = tid; p < npatch; p += NT) {
+          pbias[p] = 0.0f;
+          pflag[p] = 0u;
         }
         __syncthreads();
-        // every wave takes the k-th largest of the NW * M maxima itself (key 0,
-        // fewer than k real values, leaves no bound)
-        wtau = wave_kth_largest(lane < NW * M ? s_top[lane] : 0u, k);
-      }
-      // any wave's threshold is a lower bound of the k-th largest of the row
-      wtau = max(wtau, __hip_atomic_load(&s_tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-      float thr_f = key2f(wtau);
-      int npf = 0;  // prefilter passes of this tile, over the wave
-#pragma unroll
-      for (int q = 0; q < NE; ++q) npf += __popcll(__ballot(valid(q) && !(sv[q] < thr_f)));
-      if (npf == 0) return;
-      if (wn + npf > kWaveCap) {
-        // Raise the threshold to a lower bound of the k-th largest of all this
-        // wave has seen (buffer + tile): the k-th largest of the per-lane top-2.
-        uint32_t tops[2] = {0u, 0u};
-        int nm = 0;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-          const int i = lane + j * kWave;
-          if (i < wn) {
-            topq_insert<2>(tops, (uint32_t)(wb[i] >> 32));
-            ++nm;
+        // every writer of pid[p] stores the same value
+        for_window([&](int loc) {
+          if (loc >= 0) {
+            const int p = slot_of(loc);
+            atomicAdd(&pflag[p], 1u << kPatchCountShift);  // the window count
+            pid[p] = lo + loc;
+          }
+        });
+        auto put_bias = [&](int loc, float val) {
+          const int p = slot_of(loc);
+          pbias[p] = val;  // bias ids are unique per row
+          atomicOr(&pflag[p], (uint32_t)kPatchBias | (!(val <= 0.0f) ? (uint32_t)kPatchRise : 0u));
+          pid[p] = lo + loc;
+        };
+        if (bias_one) {
+          if (b_loc >= 0) put_bias(b_loc, b_val);
+        } else {
+          for (int j = tid; j < P.bias_cnt; j += NT) {
+            const int loc = a.bias_ids[P.bias_off + j] - lo;
+            if (loc >= 0 && loc < len) put_bias(loc, a.bias_vals[P.bias_off + j]);
           }
         }
-#pragma unroll
-        for (int q = 0; q < NE; ++q) {
-          if (valid(q) && !(sv[q] < thr_f) && !patched(loc_of(q))) {
-            const uint32_t kq = f2key(sv[q]);
-            if (kq >= wtau) {
-              topq_insert<2>(tops, kq);
+      }
+    }
+    __syncthreads();
+    auto patched = [&](int loc) -> bool {  // loc: slice-local offset
+      return has_patch && ((bitmap[loc >> 5] >> (loc & 31)) & 1u);
+    };
+    // A patched logit met at or above the threshold keeps its original value
+    // for the final pass.  One that stays below it cannot be a member unless
+    // its patch can raise it (a positive or NaN bias, or penalties of the
+    // raising sign): every other patch only lowers a logit (division by
+    // rp >= 1 of a positive value, multiplication of a non-positive one,
+    // subtraction of count * frequency + presence >= 0, a bias <= 0), and so
+    // does the temperature's positive factor, in float rounding too.
+    auto capture = [&](int loc, float raw) {
+      const int p = slot_of(loc);
+      pfin[p] = raw;
+      atomicOr(&pflag[p], (uint32_t)kPatchSeen);
+    };
+    const bool row_rise =
+        (P.rp_active && !(P.rp32 >= 1.0f)) || !(P.freq >= 0.0) || !(P.pres >= 0.0);
+    auto may_rise = [&](uint32_t fl) -> bool {
+      return (fl & kPatchRise) || (row_rise && (fl >> kPatchCountShift) > 0);
+    };
+    // The original logits of the ids whose patch may raise them are requested
+    // now (slots tid + r * NT; the rest, if any, are read after the stream):
+    // requests past the slice return 0 without reading memory, so the slots
+    // without such a patch need no branch around the load.
+    constexpr int RPT = 2;
+    float rraw[RPT];
+  #pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const int p = tid + r * NT;
+      const bool want = !ovf && p < npatch && may_rise(pflag[p]);
+      rraw[r] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rs, want ? (pid[p] - lo) * 4 : kOutOfRange, 0, 0));
+    }
+    // greedy rows: the original logit at index 0 (argmax stays at 0 when the
+    // final value there is NaN), read from the first tile
+    float x0raw = 0.0f;
+
+    // ---- the stream ----
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    int buf_n = 0, cur = 0;
+    uint32_t tau = 0u;
+    // wave path (k <= 64): this wave's buffer count, threshold and overflow
+    int wn = 0;
+    uint32_t wtau = 0u;
+    bool wovf = false;
+
+    // t: the unit; first: the first unit of every thread (tile 0 of the row)
+    auto process = [&](float (&v)[NE], int t, bool first) __attribute__((always_inline)) {
+      const int toff = t * UE;
+      const bool full = toff + UE <= len;  // no element of the unit lies past the slice
+      // This thread's first element of the unit, made opaque so that the
+      // per-element offsets below are formed here, not hoisted out of the
+      // loop into one register each.
+      int obase = toff + uth * 4;
+      asm volatile("" : "+v"(obase));
+      // With 16-byte loads len % 4 == 0, so a float4 group is wholly in or out.
+      auto loc_of = [&](int q) -> int { return obase + (q >> 2) * GS + (q & 3); };
+      auto valid = [&](int q) -> bool {
+        const int o = obase + (q >> 2) * GS;
+        return full || (VEC ? o < len : o + (q & 3) < len);
+      };
+      if (greedy) {
+        // argmax (:45-49): only a lane whose tile maximum beats its running
+        // best walks the tile in index order (strict >, so the first index wins)
+        float tmx = -__builtin_inff();
+  #pragma unroll
+        for (int q = 0; q < NE; ++q)
+          if (valid(q) && v[q] > tmx) tmx = v[q];
+        // (nothing chosen yet: equal values still pick the first index, so a
+        // row of -inf answers its first id)
+        if (first && tid == 0) x0raw = v[0];
+        if (tmx > bv || (tmx == bv && bi == 0x7fffffff)) {
+  #pragma unroll
+          for (int q = 0; q < NE; ++q)
+            if (valid(q)) {
+              if (patched(loc_of(q)))
+                capture(loc_of(q), v[q]);
+              else
+                argmax_merge(bv, bi, v[q], lo + loc_of(q));
+            }
+        }
+        return;
+      }
+      // temperature (:80-81); v keeps the original logits for the patched ids
+      // met on the way
+      float sv[NE];
+      {
+        const float invT = P.invT;
+  #pragma unroll
+        for (int q = 0; q < NE; ++q) sv[q] = v[q] * invT;
+      }
+      auto gid = [&](int q) -> uint32_t { return (uint32_t)(lo + loc_of(q)); };
+      if constexpr (WAVE) {
+        // ---- wave path: this wave's own buffer, no barrier ----
+        // Prefilter in the float domain: key(v) >= t implies !(v < key2f(t))
+        // (NaN passes too), so keys are formed only where some lane passes.
+        uint64_t* wb = cand + (size_t)wv * kWaveCap;
+        uint32_t* whist = shist + wv * kWaveBins;
+        if (first) {
+          // Block-wide start: every wave puts the M largest of its lanes'
+          // maxima (distinct elements) into LDS, and the k-th largest of those
+          // NW * M >= k real elements bounds the row's k-th largest from below.
+          constexpr int M = (kWave + NW - 1) / NW;
+          uint32_t lmax = 0u;  // 0: no unpatched value in this lane
+          // (every lane reads a bitmap word, clamped into the slice, so that no
+          // branch surrounds the LDS reads; the patch bits of each float4 group
+          // sit in one word)
+          uint32_t pbits[NV4];
+  #pragma unroll
+          for (int j = 0; j < NV4; ++j) {
+            const int o = obase + j * GS;
+            pbits[j] = bitmap[min(o, len - 1) >> 5] >> (o & 31);
+          }
+  #pragma unroll
+          for (int j = 0; j < NV4; ++j) {
+            const uint32_t pb = has_patch ? pbits[j] : 0u;
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int q = 4 * j + e;
+              const uint32_t kq = f2key(sv[q]);
+              const bool ok = valid(q) & !((pb >> e) & 1u);
+              lmax = ok ? max(lmax, kq) : lmax;
+            }
+          }
+  #pragma unroll
+          for (int i = 0; i < M; ++i) {
+            const uint32_t m = wave_max_u32(lmax);
+            const uint64_t at = __ballot(lmax == m);
+            if (lane == __ffsll((unsigned long long)at) - 1) lmax = 0u;
+            if (lane == 0) s_top[wv * M + i] = m;
+          }
+          __syncthreads();
+          // every wave takes the k-th largest of the NW * M maxima itself (key 0,
+          // fewer than k real values, leaves no bound)
+          wtau = wave_kth_largest(lane < NW * M ? s_top[lane] : 0u, k);
+        }
+        // any wave's threshold is a lower bound of the k-th largest of the row
+        wtau = max(wtau, __hip_atomic_load(&s_tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        float thr_f = key2f(wtau);
+        int npf = 0;  // prefilter passes of this tile, over the wave
+  #pragma unroll
+        for (int q = 0; q < NE; ++q) npf += __popcll(__ballot(valid(q) && !(sv[q] < thr_f)));
+        if (npf == 0) return;
+        if (wn + npf > kWaveCap) {
+          // Raise the threshold to a lower bound of the k-th largest of all this
+          // wave has seen (buffer + tile): the k-th largest of the per-lane top-2.
+          uint32_t tops[2] = {0u, 0u};
+          int nm = 0;
+  #pragma unroll
+          for (int j = 0; j < PER; ++j) {
+            const int i = lane + j * kWave;
+            if (i < wn) {
+              topq_insert<2>(tops, (uint32_t)(wb[i] >> 32));
               ++nm;
             }
           }
-        }
-        const int nv = min(nm, 2);
-        int tv;
-        (void)wave_excl_sum_small<2>(nv, tv);
-        if (tv >= k) {
-          wtau = wave_select(
-                     [&](auto fn) {
-#pragma unroll
-                       for (int q = 0; q < 2; ++q) fn(tops[q], q < nv);
-                     },
-                     k, k + k / 2, whist)
-                     .tau;
-          thr_f = key2f(wtau);
-        }
-        // compact the buffer to the new threshold
-        uint64_t xs[PER];
-        int keep = 0;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-          const int i = lane + j * kWave;
-          xs[j] = (i < wn) ? wb[i] : 0ull;
-          keep += (i < wn && (uint32_t)(xs[j] >> 32) >= wtau);
-        }
-        int ktot;
-        int pos = wave_excl_sum_small<3>(keep, ktot);  // keep <= PER = 4
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-          const int i = lane + j * kWave;
-          if (i < wn && (uint32_t)(xs[j] >> 32) >= wtau) wb[pos++] = xs[j];
-        }
-        wn = ktot;
-        npf = 0;
-#pragma unroll
-        for (int q = 0; q < NE; ++q) npf += __popcll(__ballot(valid(q) && !(sv[q] < thr_f)));
-        if (wn + npf > kWaveCap) {
-          wovf = true;  // ties or an adversarial order crowd the buffer
-          return;
-        }
-      }
-      // append every unpatched value >= the threshold (each passes the prefilter)
-#pragma unroll
-      for (int q = 0; q < NE; ++q) {
-        if (__ballot(valid(q) && !(sv[q] < thr_f)) == 0ull) continue;
-        const uint32_t kq = f2key(sv[q]);
-        const bool pass = valid(q) && kq >= wtau;
-        const bool pat = pass && patched(loc_of(q));
-        if (pat) capture(loc_of(q), v[q]);
-        const bool keep = pass && !pat;
-        const uint64_t m = __ballot(keep);
-        if (keep) wb[wn + (int)__popcll(m & lanes_below())] = ((uint64_t)kq << 32) | gid(q);
-        wn += (int)__popcll(m);
-      }
-      if (wn >= 2 * k + kWave) {
-        // tighten: the k-th largest of the buffer (which holds every value >=
-        // the old threshold) is a lower bound of the k-th largest of the row
-        uint64_t xs[PER];
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-          const int i = lane + j * kWave;
-          xs[j] = (i < wn) ? wb[i] : 0ull;
-        }
-        const int n0 = wn;
-        const SelectResult r = wave_select(
-            [&](auto fn) {
-#pragma unroll
-              for (int j = 0; j < PER; ++j) fn((uint32_t)(xs[j] >> 32), lane + j * kWave < n0);
-            },
-            k, k + k / 4, whist);
-        int keep = 0;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) keep += (lane + j * kWave < n0 && (uint32_t)(xs[j] >> 32) >= r.tau);
-        int ktot;
-        int pos = wave_excl_sum_small<3>(keep, ktot);
-#pragma unroll
-        for (int j = 0; j < PER; ++j)
-          if (lane + j * kWave < n0 && (uint32_t)(xs[j] >> 32) >= r.tau) wb[pos++] = xs[j];
-        wn = ktot;
-        wtau = r.tau;
-        if (lane == 0) atomicMax(&s_tau, wtau);
-      }
-      return;
-    } else {
-      // ---- block path (k > 64): one buffer, a barrier per tile ----
-      auto use = [&](int q) -> bool { return valid(q) && !patched(loc_of(q)); };
-      uint32_t key[NE];
-#pragma unroll
-      for (int q = 0; q < NE; ++q) key[q] = f2key(sv[q]);
-#pragma unroll
-      for (int q = 0; q < NE; ++q)
-        if (valid(q) && key[q] >= tau && patched(loc_of(q))) capture(loc_of(q), v[q]);
-      int mine = 0;
-#pragma unroll
-      for (int q = 0; q < NE; ++q) mine += (use(q) && key[q] >= tau);
-      int wtot;
-      const int wex = wave_excl_sum_small<5>(mine, wtot);  // mine <= NE = 16
-      const int slot = t % 3;
-      int wbase = 0;
-      if (lane == 0 && wtot) wbase = atomicAdd(&s_tile_cnt[slot], wtot);
-      wbase = __shfl(wbase, 0, kWave);
-      __syncthreads();
-      const int ttot = s_tile_cnt[slot];
-      if (tid == 0) s_tile_cnt[(t + 2) % 3] = 0;
-      uint64_t* cb = cand + (size_t)cur * a.ccap;
-      if (buf_n + ttot <= a.ccap) {
-        int pos = buf_n + wbase + wex;
-#pragma unroll
-        for (int q = 0; q < NE; ++q)
-          if (use(q) && key[q] >= tau) cb[pos++] = ((uint64_t)key[q] << 32) | gid(q);
-        buf_n += ttot;
-        return;
-      }
-      // threshold refresh (uniform): raise tau, compact into the other buffer
-      uint64_t* nb = cand + (size_t)(cur ^ 1) * a.ccap;
-      uint32_t tops[Q];
-#pragma unroll
-      for (int q = 0; q < Q; ++q) tops[q] = 0u;
-      int nmine = 0;
-      for (int i = tid; i < buf_n; i += NT) {
-        topq_insert<Q>(tops, (uint32_t)(cb[i] >> 32));
-        ++nmine;
-      }
-#pragma unroll
-      for (int q = 0; q < NE; ++q) {
-        if (use(q) && key[q] >= tau) {
-          topq_insert<Q>(tops, key[q]);
-          ++nmine;
-        }
-      }
-      const int nv = min(nmine, Q);
-      const int tv = block_sum<NT>(nv, smem);
-      // t1 <= the k-th largest of the per-thread tops (k real elements), so t1
-      // is a lower bound of the k-th largest of everything seen.  A coarse
-      // digit prefix is enough while it admits few elements; otherwise refine
-      // to the exact k-th largest of the tops.
-      auto tops_select = [&](int fit) -> uint32_t {
-        return block_select<NT>(
-                   [&](auto fn) {
-#pragma unroll
-                     for (int q = 0; q < Q; ++q) fn(tops[q], q < nv);
-                   },
-                   k, fit, shist, smem)
-            .tau;
-      };
-      auto count_ge = [&](uint32_t th) -> int {
-        int c = 0;
-        for (int i = tid; i < buf_n; i += NT) c += ((uint32_t)(cb[i] >> 32) >= th);
-#pragma unroll
-        for (int q = 0; q < NE; ++q) c += (use(q) && key[q] >= th);
-        return block_sum<NT>(c, smem);
-      };
-      uint32_t t1 = tau;
-      int cnt = buf_n + ttot;
-      if (tv >= k) {
-        t1 = tops_select(2 * k);
-        cnt = count_ge(t1);
-        if (cnt > a.ccap / 2) {
-          t1 = tops_select(-1);
-          cnt = count_ge(t1);
-        }
-      }
-      if (cnt > a.ccap) {
-        // only ties at t1, or values crowded into few threads, get here: the
-        // whole-row kernel takes the row
-        ovf = true;
-        return;
-      }
-      int c1 = 0;
-      for (int i = tid; i < buf_n; i += NT) c1 += ((uint32_t)(cb[i] >> 32) >= t1);
-#pragma unroll
-      for (int q = 0; q < NE; ++q) c1 += (use(q) && key[q] >= t1);
-      int tot;
-      int pos = block_excl_scan<NT>(c1, smem, tot);
-      for (int i = tid; i < buf_n; i += NT) {
-        const uint64_t x = cb[i];
-        if ((uint32_t)(x >> 32) >= t1) nb[pos++] = x;
-      }
-#pragma unroll
-      for (int q = 0; q < NE; ++q)
-        if (use(q) && key[q] >= t1) nb[pos++] = ((uint64_t)key[q] << 32) | gid(q);
-      __syncthreads();
-      cur ^= 1;
-      buf_n = tot;
-      tau = t1;
-    }
-  };
-
-  if (!ovf) {
-    // One unit is in flight while the previous one is processed: as each
-    // float4 group of unit t lands it is copied out and the same group of the
-    // next unit is requested into its registers, so the memory queue stays
-    // full.  (A workgroup can keep about one tile of requests outstanding;
-    // more only stalls the issuing wave.)  The requests are unconditional
-    // (past the slice they return zeros without reading memory) and the loop
-    // runs on wave-uniform conditions, so the compiler's waits follow the
-    // request order exactly.  ovf and wovf agree over the wave; the scalar
-    // read makes that visible.
-    auto stop = [&]() -> bool { return __builtin_amdgcn_readfirstlane((int)(ovf || wovf)) != 0; };
-    const int nunits = (len + UE - 1) / UE;
-    int t = u0;
-    for (bool first = true;; first = false) {
-      int tn = t + 1;
-      if constexpr (WAVE) {
-        // the next chunk for this wave
-        int c = 0;
-        if (lane == 0) c = atomicAdd(&s_next, 1);
-        tn = __builtin_amdgcn_readfirstlane(c);
-      }
-      float v[NE];
-#pragma unroll
-      for (int j = 0; j < NV4; ++j) {
-        v[4 * j + 0] = R0[j].x;
-        v[4 * j + 1] = R0[j].y;
-        v[4 * j + 2] = R0[j].z;
-        v[4 * j + 3] = R0[j].w;
-        R0[j] = load_group<GS, VEC>(rs, tn * UE, j, uth);
-      }
-      process(v, t, first);
-      if (stop() || tn >= nunits) break;
-      t = tn;
-    }
-  }
-  // The final value of patched slot p from its original logit: penalties then
-  // bias (:71-76), then temperature (:80-81) on the sampling rows.
-  auto patched_final = [&](int p, float v, uint32_t fl) -> float {
-    const uint32_t cnt = fl >> kPatchCountShift;
-    if (cnt) {
-      if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
-      v = v - (float)((double)cnt * P.freq + P.pres);  // float64, one rounding (:74)
-    }
-    if (fl & kPatchBias) v = v + pbias[p];
-    if (!greedy) v = v * P.invT;
-    return v;
-  };
-  // original logit of slot p for the final pass (met during the stream,
-  // requested before it, or read now)
-  // (the late read goes through the slice's buffer resource, so that the
-  // compiler cannot merge it with the LDS read into one generic-address load)
-  auto patched_raw = [&](int p, uint32_t fl) -> float {
-    const int r = (p - tid) / NT;
-    if (fl & kPatchSeen) return pfin[p];
-    if (r < RPT) return r == 0 ? rraw[0] : rraw[1];
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (pid[p] - lo) * 4, 0, 0));
-  };
-
-  uint64_t* ent;
-  int N;
-  // Top-k rows of the wave path on one slice: the candidates are narrowed
-  // before any select.  Every wave offers its M largest buffer keys (64
-  // distinct real elements in all); the k-th largest of those bounds the
-  // row's k-th largest from below, and typically leaves few more than k
-  // entries above it.  With at most 128 survivors and no excess ties at the
-  // k-th value one wave finishes the row alone.
-  const bool wave_flow = WAVE && topk && a.S == 1;
-  if (wave_flow) {
-    constexpr int M = (kWave + NW - 1) / NW;
-    uint64_t* wb = cand + (size_t)wv * kWaveCap;
-    uint64_t xs[PER];
-    uint32_t ks[PER];
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = lane + j * kWave;
-      xs[j] = (!wovf && i < wn) ? wb[i] : 0ull;
-      ks[j] = (uint32_t)(xs[j] >> 32);
-    }
-    {
-      uint32_t kr[PER];
-#pragma unroll
-      for (int j = 0; j < PER; ++j) kr[j] = ks[j];
-#pragma unroll
-      for (int i = 0; i < M; ++i) {
-        uint32_t lm = 0u;
-#pragma unroll
-        for (int j = 0; j < PER; ++j) lm = max(lm, kr[j]);
-        const uint32_t m = wave_max_u32(lm);
-        const uint64_t at = __ballot(lm == m);
-        if (lane == __ffsll((unsigned long long)at) - 1) {
-          bool done = false;
-#pragma unroll
-          for (int j = 0; j < PER; ++j)
-            if (!done && kr[j] == m) {
-              kr[j] = 0u;
-              done = true;
+  #pragma unroll
+          for (int q = 0; q < NE; ++q) {
+            if (valid(q) && !(sv[q] < thr_f) && !patched(loc_of(q))) {
+              const uint32_t kq = f2key(sv[q]);
+              if (kq >= wtau) {
+                topq_insert<2>(tops, kq);
+                ++nm;
+              }
             }
-        }
-        if (lane == 0) s_top[wv * M + i] = m;
-      }
-    }
-    if (lane == 0) {
-      s_wn[wv] = wovf ? -1 : wn;
-      s_wt[wv] = wtau;
-    }
-    __syncthreads();  // every wave's stream, captures and offers are in
-    // lane w reads wave w's record
-    ovf = ovf || __ballot(lane < NW && s_wn[min(lane, NW - 1)] < 0) != 0ull;
-    const uint32_t tau_all = wave_max_u32(lane < NW ? s_wt[min(lane, NW - 1)] : 0u);
-    ent = cand + a.ccap;  // free: holds NW * kWaveCap entries and more
-    if (!ovf) {
-      const uint32_t te = max(tau_all, wave_kth_largest(lane < NW * M ? s_top[lane] : 0u, k));
-      // this wave's entries >= te
-      int c = 0;
-#pragma unroll
-      for (int j = 0; j < PER; ++j) c += __popcll(__ballot(ks[j] >= te && ks[j] != 0u));
-      int base = 0;
-      if (lane == 0 && c) base = atomicAdd(&s_cnt, c);
-      base = __builtin_amdgcn_readfirstlane(base);
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        const bool keep = ks[j] >= te && ks[j] != 0u;
-        const uint64_t mk = __ballot(keep);
-        if (keep) ent[base + (int)__popcll(mk & lanes_below())] = xs[j];
-        base += (int)__popcll(mk);
-      }
-      // patched ids: final values, those >= te join
-      for (int p = tid; p < npatch; p += NT) {
-        const uint32_t fl = pflag[p];
-        if (!(fl & kPatchSeen) && !may_rise(fl)) continue;
-        const float v = patched_final(p, patched_raw(p, fl), fl);
-        const uint32_t kp = f2key(v);
-        if (kp >= te) {
-          const int i = atomicAdd(&s_cnt, 1);
-          if (i < a.ccap) ent[i] = ((uint64_t)kp << 32) | (uint32_t)pid[p];
-        }
-      }
-    }
-    __syncthreads();
-    N = s_cnt;
-    if (!ovf && N > a.ccap) ovf = true;  // uniform
-    if (ovf) {
-      if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
-      return;
-    }
-    if (N >= k && N <= 2 * kWave) {
-      // every wave finds the k-th largest key T of the survivors itself
-      const uint64_t e0 = lane < N ? ent[lane] : 0ull;
-      const uint64_t e1 = lane + kWave < N ? ent[lane + kWave] : 0ull;
-      const uint32_t k0 = (uint32_t)(e0 >> 32), k1 = (uint32_t)(e1 >> 32);
-      uint32_t T = 0u;
-      if (N <= kWave) {
-        T = wave_kth_largest(k0, k);
-      } else {
-#pragma unroll
-        for (int b = 31; b >= 0; --b) {
-          const uint32_t c = T | (1u << b);
-          if (__popcll(__ballot(k0 >= c)) + __popcll(__ballot(k1 >= c)) >= k) T = c;
-        }
-      }
-      const int ge = __popcll(__ballot(lane < N && k0 >= T)) + __popcll(__ballot(lane + kWave < N && k1 >= T));
-      if (ge == k) {
-        // no excess ties at T: the members are exactly the survivors >= T
-        if (wv != 0) return;
-        uint64_t* mem = reinterpret_cast<uint64_t*>(regA);
-        const bool in0 = lane < N && k0 >= T, in1 = lane + kWave < N && k1 >= T;
-        const uint64_t m0 = __ballot(in0), m1 = __ballot(in1);
-        if (in0) mem[__popcll(m0 & lanes_below())] = e0;
-        if (in1) mem[__popcll(m0) + __popcll(m1 & lanes_below())] = e1;
-        double u = 0.0;
-        if (lane == 0) u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
-        wave_tail(mem, k, P, u, row, a.out, a.dbg);
-        return;
-      }
-    }
-    // many survivors or excess ties: the block-wide member selection
-    __syncthreads();
-    if (tid == 0) s_cnt = 0;
-  } else {
-    // Ids that can be members were met during the stream; only the ids whose
-    // patch may raise them are read again here.  The others are left out
-    // (flag kPatchSeen clear).
-    if (!ovf && npatch > 0) {
-      __syncthreads();  // every wave's captures are in
-      for (int p = tid; p < npatch; p += NT) {
-        uint32_t fl = pflag[p];
-        const uint32_t cnt = fl >> kPatchCountShift;
-        if (!(fl & kPatchSeen) && !may_rise(fl)) continue;
-        float v = patched_raw(p, fl);
-        if (cnt) {
-          if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
-          v = v - (float)((double)cnt * P.freq + P.pres);  // float64, one rounding (:74)
-        }
-        if (fl & kPatchBias) v = v + pbias[p];
-        if (!greedy) v = v * P.invT;
-        pfin[p] = v;
-        if (!(fl & kPatchSeen)) pflag[p] = fl | kPatchSeen;
-      }
-      __syncthreads();
-    }
-
-    // ---- the slice's candidates: stream buffer(s) + patched values ----
-    ent = cand + (size_t)cur * a.ccap;
-    N = buf_n;
-    if (topk) {
-      uint32_t tau_all = tau;  // a lower bound of the row's k-th largest, uniform
-      if constexpr (WAVE) {
-        // concatenate the wave buffers into the second buffer
-        if (lane == 0) {
-          s_wn[wv] = wovf ? -1 : wn;
-          s_wt[wv] = wtau;
-        }
-        __syncthreads();
-        int off = 0;
-        N = 0;
-        tau_all = 0u;
-        for (int w = 0; w < NW; ++w) {
-          const int nw_ = s_wn[w];
-          tau_all = max(tau_all, s_wt[w]);
-          if (nw_ < 0) {
-            ovf = true;
-          } else {
-            if (w == wv) off = N;
-            N += nw_;
+          }
+          const int nv = min(nm, 2);
+          int tv;
+          (void)wave_excl_sum_small<2>(nv, tv);
+          if (tv >= k) {
+            wtau = wave_select(
+                       [&](auto fn) {
+  #pragma unroll
+                         for (int q = 0; q < 2; ++q) fn(tops[q], q < nv);
+                       },
+                       k, k + k / 2, whist)
+                       .tau;
+            thr_f = key2f(wtau);
+          }
+          // compact the buffer to the new threshold
+          uint64_t xs[PER];
+          int keep = 0;
+  #pragma unroll
+          for (int j = 0; j < PER; ++j) {
+            const int i = lane + j * kWave;
+            xs[j] = (i < wn) ? wb[i] : 0ull;
+            keep += (i < wn && (uint32_t)(xs[j] >> 32) >= wtau);
+          }
+          int ktot;
+          int pos = wave_excl_sum_small<3>(keep, ktot);  // keep <= PER = 4
+  #pragma unroll
+          for (int j = 0; j < PER; ++j) {
+            const int i = lane + j * kWave;
+            if (i < wn && (uint32_t)(xs[j] >> 32) >= wtau) wb[pos++] = xs[j];
+          }
+          wn = ktot;
+          npf = 0;
+  #pragma unroll
+          for (int q = 0; q < NE; ++q) npf += __popcll(__ballot(valid(q) && !(sv[q] < thr_f)));
+          if (wn + npf > kWaveCap) {
+            wovf = true;  // ties or an adversarial order crowd the buffer
+            return;
           }
         }
-        ent = cand + a.ccap;
-        if (!ovf) {
-          const uint64_t* wb = cand + (size_t)wv * kWaveCap;
-          for (int i = lane; i < wn; i += kWave) ent[off + i] = wb[i];
+        // append every unpatched value >= the threshold (each passes the prefilter)
+  #pragma unroll
+        for (int q = 0; q < NE; ++q) {
+          if (__ballot(valid(q) && !(sv[q] < thr_f)) == 0ull) continue;
+          const uint32_t kq = f2key(sv[q]);
+          const bool pass = valid(q) && kq >= wtau;
+          const bool pat = pass && patched(loc_of(q));
+          if (pat) capture(loc_of(q), v[q]);
+          const bool keep = pass && !pat;
+          const uint64_t m = __ballot(keep);
+          if (keep) wb[wn + (int)__popcll(m & lanes_below())] = ((uint64_t)kq << 32) | gid(q);
+          wn += (int)__popcll(m);
         }
+        if (wn >= 2 * k + kWave) {
+          // tighten: the k-th largest of the buffer (which holds every value >=
+          // the old threshold) is a lower bound of the k-th largest of the row
+          uint64_t xs[PER];
+  #pragma unroll
+          for (int j = 0; j < PER; ++j) {
+            const int i = lane + j * kWave;
+            xs[j] = (i < wn) ? wb[i] : 0ull;
+          }
+          const int n0 = wn;
+          const SelectResult r = wave_select(
+              [&](auto fn) {
+  #pragma unroll
+                for (int j = 0; j < PER; ++j) fn((uint32_t)(xs[j] >> 32), lane + j * kWave < n0);
+              },
+              k, k + k / 4, whist);
+          int keep = 0;
+  #pragma unroll
+          for (int j = 0; j < PER; ++j) keep += (lane + j * kWave < n0 && (uint32_t)(xs[j] >> 32) >= r.tau);
+          int ktot;
+          int pos = wave_excl_sum_small<3>(keep, ktot);
+  #pragma unroll
+          for (int j = 0; j < PER; ++j)
+            if (lane + j * kWave < n0 && (uint32_t)(xs[j] >> 32) >= r.tau) wb[pos++] = xs[j];
+          wn = ktot;
+          wtau = r.tau;
+          if (lane == 0) atomicMax(&s_tau, wtau);
+        }
+        return;
+      } else {
+        // ---- block path (k > 64): one buffer, a barrier per tile ----
+        auto use = [&](int q) -> bool { return valid(q) && !patched(loc_of(q)); };
+        uint32_t key[NE];
+  #pragma unroll
+        for (int q = 0; q < NE; ++q) key[q] = f2key(sv[q]);
+  #pragma unroll
+        for (int q = 0; q < NE; ++q)
+          if (valid(q) && key[q] >= tau && patched(loc_of(q))) capture(loc_of(q), v[q]);
+        int mine = 0;
+  #pragma unroll
+        for (int q = 0; q < NE; ++q) mine += (use(q) && key[q] >= tau);
+        int wtot;
+        const int wex = wave_excl_sum_small<5>(mine, wtot);  // mine <= NE = 16
+        const int slot = t % 3;
+        int wbase = 0;
+        if (lane == 0 && wtot) wbase = atomicAdd(&s_tile_cnt[slot], wtot);
+        wbase = __shfl(wbase, 0, kWave);
         __syncthreads();
+        const int ttot = s_tile_cnt[slot];
+        if (tid == 0) s_tile_cnt[(t + 2) % 3] = 0;
+        uint64_t* cb = cand + (size_t)cur * a.ccap;
+        if (buf_n + ttot <= a.ccap) {
+          int pos = buf_n + wbase + wex;
+  #pragma unroll
+          for (int q = 0; q < NE; ++q)
+            if (use(q) && key[q] >= tau) cb[pos++] = ((uint64_t)key[q] << 32) | gid(q);
+          buf_n += ttot;
+          return;
+        }
+        // threshold refresh (uniform): raise tau, compact into the other buffer
+        uint64_t* nb = cand + (size_t)(cur ^ 1) * a.ccap;
+        uint32_t tops[Q];
+  #pragma unroll
+        for (int q = 0; q < Q; ++q) tops[q] = 0u;
+        int nmine = 0;
+        for (int i = tid; i < buf_n; i += NT) {
+          topq_insert<Q>(tops, (uint32_t)(cb[i] >> 32));
+          ++nmine;
+        }
+  #pragma unroll
+        for (int q = 0; q < NE; ++q) {
+          if (use(q) && key[q] >= tau) {
+            topq_insert<Q>(tops, key[q]);
+            ++nmine;
+          }
+        }
+        const int nv = min(nmine, Q);
+        const int tv = block_sum<NT>(nv, smem);
+        // t1 <= the k-th largest of the per-thread tops (k real elements), so t1
+        // is a lower bound of the k-th largest of everything seen.  A coarse
+        // digit prefix is enough while it admits few elements; otherwise refine
+        // to the exact k-th largest of the tops.
+        auto tops_select = [&](int fit) -> uint32_t {
+          return block_select<NT>(
+                     [&](auto fn) {
+  #pragma unroll
+                       for (int q = 0; q < Q; ++q) fn(tops[q], q < nv);
+                     },
+                     k, fit, shist, smem)
+              .tau;
+        };
+        auto count_ge = [&](uint32_t th) -> int {
+          int c = 0;
+          for (int i = tid; i < buf_n; i += NT) c += ((uint32_t)(cb[i] >> 32) >= th);
+  #pragma unroll
+          for (int q = 0; q < NE; ++q) c += (use(q) && key[q] >= th);
+          return block_sum<NT>(c, smem);
+        };
+        uint32_t t1 = tau;
+        int cnt = buf_n + ttot;
+        if (tv >= k) {
+          t1 = tops_select(2 * k);
+          cnt = count_ge(t1);
+          if (cnt > a.ccap / 2) {
+            t1 = tops_select(-1);
+            cnt = count_ge(t1);
+          }
+        }
+        if (cnt > a.ccap) {
+          // only ties at t1, or values crowded into few threads, get here: the
+          // whole-row kernel takes the row
+          ovf = true;
+          return;
+        }
+        int c1 = 0;
+        for (int i = tid; i < buf_n; i += NT) c1 += ((uint32_t)(cb[i] >> 32) >= t1);
+  #pragma unroll
+        for (int q = 0; q < NE; ++q) c1 += (use(q) && key[q] >= t1);
+        int tot;
+        int pos = block_excl_scan<NT>(c1, smem, tot);
+        for (int i = tid; i < buf_n; i += NT) {
+          const uint64_t x = cb[i];
+          if ((uint32_t)(x >> 32) >= t1) nb[pos++] = x;
+        }
+  #pragma unroll
+        for (int q = 0; q < NE; ++q)
+          if (use(q) && key[q] >= t1) nb[pos++] = ((uint64_t)key[q] << 32) | gid(q);
+        __syncthreads();
+        cur ^= 1;
+        buf_n = tot;
+        tau = t1;
       }
-      if (!ovf && npatch > 0) {
-        // patched values >= tau_all join the candidates
-        if (tid == 0) s_cnt = N;
-        __syncthreads();
+    };
+
+    if (!ovf) {
+      // One unit is in flight while the previous one is processed: as each
+      // float4 group of unit t lands it is copied out and the same group of the
+      // next unit is requested into its registers, so the memory queue stays
+      // full.  (A workgroup can keep about one tile of requests outstanding;
+      // more only stalls the issuing wave.)  The requests are unconditional
+      // (past the slice they return zeros without reading memory) and the loop
+      // runs on wave-uniform conditions, so the compiler's waits follow the
+      // request order exactly.  ovf and wovf agree over the wave; the scalar
+      // read makes that visible.
+      auto stop = [&]() -> bool { return __builtin_amdgcn_readfirstlane((int)(ovf || wovf)) != 0; };
+      const int nunits = (len + UE - 1) / UE;
+      int t = u0;
+      for (bool first = true;; first = false) {
+        int tn = t + 1;
+        if constexpr (WAVE) {
+          // the next chunk for this wave: the second is fixed (NW + wv), the
+          // later ones are claimed
+          if (first) {
+            tn = NW + wv;
+          } else {
+            int c = 0;
+            if (lane == 0) c = atomicAdd(&s_next, 1);
+            tn = __builtin_amdgcn_readfirstlane(c);
+          }
+        }
+        float v[NE];
+  #pragma unroll
+        for (int j = 0; j < NV4; ++j) {
+          v[4 * j + 0] = R0[j].x;
+          v[4 * j + 1] = R0[j].y;
+          v[4 * j + 2] = R0[j].z;
+          v[4 * j + 3] = R0[j].w;
+          R0[j] = load_group<GS, VEC>(rs, tn * UE, j, uth);
+        }
+        process(v, t, first);
+        if (stop() || tn >= nunits) break;
+        t = tn;
+      }
+    }
+    // The final value of patched slot p from its original logit: penalties then
+    // bias (:71-76), then temperature (:80-81) on the sampling rows.
+    auto patched_final = [&](int p, float v, uint32_t fl) -> float {
+      const uint32_t cnt = fl >> kPatchCountShift;
+      if (cnt) {
+        if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
+        v = v - (float)((double)cnt * P.freq + P.pres);  // float64, one rounding (:74)
+      }
+      if (fl & kPatchBias) v = v + pbias[p];
+      if (!greedy) v = v * P.invT;
+      return v;
+    };
+    // original logit of slot p for the final pass (met during the stream,
+    // requested before it, or read now)
+    // (the late read goes through the slice's buffer resource, so that the
+    // compiler cannot merge it with the LDS read into one generic-address load)
+    auto patched_raw = [&](int p, uint32_t fl) -> float {
+      const int r = (p - tid) / NT;
+      if (fl & kPatchSeen) return pfin[p];
+      if (r < RPT) return r == 0 ? rraw[0] : rraw[1];
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (pid[p] - lo) * 4, 0, 0));
+    };
+
+    uint64_t* ent;
+    int N;
+    // Top-k rows of the wave path on one slice: the candidates are narrowed
+    // before any select.  Every wave offers its M largest buffer keys (64
+    // distinct real elements in all); the k-th largest of those bounds the
+    // row's k-th largest from below, and typically leaves few more than k
+    // entries above it.  With at most 128 survivors and no excess ties at the
+    // k-th value one wave finishes the row alone.
+    const bool wave_flow = WAVE && topk && a.S == 1;
+    if (wave_flow) {
+      constexpr int M = (kWave + NW - 1) / NW;
+      uint64_t* wb = cand + (size_t)wv * kWaveCap;
+      uint64_t xs[PER];
+      uint32_t ks[PER];
+  #pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int i = lane + j * kWave;
+        xs[j] = (!wovf && i < wn) ? wb[i] : 0ull;
+        ks[j] = (uint32_t)(xs[j] >> 32);
+      }
+      {
+        uint32_t kr[PER];
+  #pragma unroll
+        for (int j = 0; j < PER; ++j) kr[j] = ks[j];
+  #pragma unroll
+        for (int i = 0; i < M; ++i) {
+          uint32_t lm = 0u;
+  #pragma unroll
+          for (int j = 0; j < PER; ++j) lm = max(lm, kr[j]);
+          const uint32_t m = wave_max_u32(lm);
+          const uint64_t at = __ballot(lm == m);
+          if (lane == __ffsll((unsigned long long)at) - 1) {
+            bool done = false;
+  #pragma unroll
+            for (int j = 0; j < PER; ++j)
+              if (!done && kr[j] == m) {
+                kr[j] = 0u;
+                done = true;
+              }
+          }
+          if (lane == 0) s_top[wv * M + i] = m;
+        }
+      }
+      if (lane == 0) {
+        s_wn[wv] = wovf ? -1 : wn;
+        s_wt[wv] = wtau;
+      }
+      __syncthreads();  // every wave's stream, captures and offers are in
+      // lane w reads wave w's record
+      ovf = ovf || __ballot(lane < NW && s_wn[min(lane, NW - 1)] < 0) != 0ull;
+      const uint32_t tau_all = wave_max_u32(lane < NW ? s_wt[min(lane, NW - 1)] : 0u);
+      ent = cand + a.ccap;  // free: holds NW * kWaveCap entries and more
+      if (!ovf) {
+        const uint32_t te = max(tau_all, wave_kth_largest(lane < NW * M ? s_top[lane] : 0u, k));
+        // this wave's entries >= te
+        int c = 0;
+  #pragma unroll
+        for (int j = 0; j < PER; ++j) c += __popcll(__ballot(ks[j] >= te && ks[j] != 0u));
+        int base = 0;
+        if (lane == 0 && c) base = atomicAdd(&s_cnt, c);
+        base = __builtin_amdgcn_readfirstlane(base);
+  #pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const bool keep = ks[j] >= te && ks[j] != 0u;
+          const uint64_t mk = __ballot(keep);
+          if (keep) ent[base + (int)__popcll(mk & lanes_below())] = xs[j];
+          base += (int)__popcll(mk);
+        }
+        // patched ids: final values, those >= te join
         for (int p = tid; p < npatch; p += NT) {
-          if (!(pflag[p] & kPatchSeen)) continue;
-          const uint32_t kp = f2key(pfin[p]);
-          if (kp >= tau_all) {
+          const uint32_t fl = pflag[p];
+          if (!(fl & kPatchSeen) && !may_rise(fl)) continue;
+          const float v = patched_final(p, patched_raw(p, fl), fl);
+          const uint32_t kp = f2key(v);
+          if (kp >= te) {
             const int i = atomicAdd(&s_cnt, 1);
             if (i < a.ccap) ent[i] = ((uint64_t)kp << 32) | (uint32_t)pid[p];
           }
         }
-        __syncthreads();
-        N = s_cnt;
-        if (N > a.ccap) ovf = true;  // uniform
-        __syncthreads();
-        if (tid == 0) s_cnt = 0;
       }
-    } else {
-      // greedy: patched final values join the argmax
-      for (int p = tid; p < npatch; p += NT)
-        if (pflag[p] & kPatchSeen) argmax_merge(bv, bi, pfin[p], pid[p]);
-    }
-    // argmax (:45-49) starts from index 0: when its value is NaN nothing
-    // compares greater and the answer stays 0
-    bool nan0 = false;
-    if (greedy && lo == 0 && len > 0 && tid == 0) {
-      float x0 = x0raw;
-      if (patched(0)) x0 = pfin[wpre[0] + 0];
-      nan0 = x0 != x0;
-    }
-
-    // ---- slice argmax (first index on ties) ----
-    wave_argmax(bv, bi);
-    if (lane == 0) {
-      s_rv[wv] = bv;
-      s_ri[wv] = bi;
-    }
-    __syncthreads();
-    float rv = s_rv[0];
-    int ri = s_ri[0];
-  #pragma unroll
-    for (int w = 1; w < NW; ++w) argmax_merge(rv, ri, s_rv[w], s_ri[w]);
-
-    if (a.S > 1) {
-      // ---- publish this slice; the last one to arrive completes the row ----
-      const int64_t part = (int64_t)row * a.S + sl;
-      uint64_t* pdst = a.part_cand + part * a.pc;
-      int nout = 0;
-      int flags = (ovf ? kSliceOverflow : 0) | (nan0 ? kSliceNan0 : 0);
-      if (topk && !ovf) {
-        if (N > a.pc) {
-          const SelectResult r = block_select<NT>(
-              [&](auto fn) {
-                for (int i0 = 0; i0 < N; i0 += NT) {
-                  const int i = i0 + tid;
-                  const bool in = i < N;
-                  fn(in ? (uint32_t)(ent[i] >> 32) : 0u, in);
-                }
-              },
-              k, a.pc, shist, smem);
-          if (r.ge > a.pc) {
-            flags = kSliceOverflow;
-          } else {
-            int mine = 0;
-            for (int i = tid; i < N; i += NT) mine += ((uint32_t)(ent[i] >> 32) >= r.tau);
-            int tot;
-            int pos = block_excl_scan<NT>(mine, smem, tot);
-            for (int i = tid; i < N; i += NT)
-              if ((uint32_t)(ent[i] >> 32) >= r.tau) store_agent(&pdst[pos++], ent[i]);
-            nout = tot;
-          }
+      __syncthreads();
+      N = s_cnt;
+      if (!ovf && N > a.ccap) ovf = true;  // uniform
+      if (ovf) {
+        if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
+        return;
+      }
+      if (N >= k && N <= 2 * kWave) {
+        // every wave finds the k-th largest key T of the survivors itself
+        const uint64_t e0 = lane < N ? ent[lane] : 0ull;
+        const uint64_t e1 = lane + kWave < N ? ent[lane + kWave] : 0ull;
+        const uint32_t k0 = (uint32_t)(e0 >> 32), k1 = (uint32_t)(e1 >> 32);
+        uint32_t T = 0u;
+        if (N <= kWave) {
+          T = wave_kth_largest(k0, k);
         } else {
-          for (int i = tid; i < N; i += NT) store_agent(&pdst[i], ent[i]);
-          nout = N;
+  #pragma unroll
+          for (int b = 31; b >= 0; --b) {
+            const uint32_t c = T | (1u << b);
+            if (__popcll(__ballot(k0 >= c)) + __popcll(__ballot(k1 >= c)) >= k) T = c;
+          }
+        }
+        const int ge = __popcll(__ballot(lane < N && k0 >= T)) + __popcll(__ballot(lane + kWave < N && k1 >= T));
+        if (ge == k) {
+          // no excess ties at T: the members are exactly the survivors >= T
+          if (wv != 0) return;
+          uint64_t* mem = reinterpret_cast<uint64_t*>(regA);
+          const bool in0 = lane < N && k0 >= T, in1 = lane + kWave < N && k1 >= T;
+          const uint64_t m0 = __ballot(in0), m1 = __ballot(in1);
+          if (in0) mem[__popcll(m0 & lanes_below())] = e0;
+          if (in1) mem[__popcll(m0) + __popcll(m1 & lanes_below())] = e1;
+          double u = 0.0;
+          if (lane == 0) u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
+          wave_tail(mem, k, P, u, row, a.out, a.dbg);
+          return;
         }
       }
-      if (tid == 0) {
-        store_agent(&a.part_info[part].n, nout);
-        store_agent(&a.part_info[part].flags, flags);
-        store_agent(&a.part_info[part].amax, ri);
-        store_agent(&a.part_info[part].vmax, __float_as_int(rv));
-      }
-      // The slice data above is written with agent-scope stores, which go to
-      // the device's point of coherence; waiting for their completion before
-      // the arrival count is bumped orders them without an L2 writeback.
-      __builtin_amdgcn_s_waitcnt(0);
+      // many survivors or excess ties: the block-wide member selection
       __syncthreads();
-      if (tid == 0)
-        s_last = (__hip_atomic_fetch_add(&a.arrive[row], 1u, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1));
-      __syncthreads();
-      if (!s_last) return;
-      if (tid == 0) __hip_atomic_store(&a.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // slice records: one per thread, then every thread reads them from LDS.
-      // s_off borrows the select histogram (free here; 5 * kMaxSlices words < kSelWords).
-      int* s_off = reinterpret_cast<int*>(shist);
-      static_assert(5 * kMaxSlices <= kSelWords, "slice records must fit the histogram");
-      if (tid < a.S) {
-        const SliceInfo* in = a.part_info + (int64_t)row * a.S + tid;
-        const int nj = load_agent(&in->n);
-        const int fl = load_agent(&in->flags);
-        s_off[kMaxSlices + tid] = (nj < 0 || nj > a.pc) ? -1 : nj;  // never trust a count past the buffer
-        s_off[2 * kMaxSlices + tid] = fl;
-        s_off[3 * kMaxSlices + tid] = load_agent(&in->amax);
-        s_off[4 * kMaxSlices + tid] = load_agent(&in->vmax);
+      if (tid == 0) s_cnt = 0;
+    } else {
+      // Ids that can be members were met during the stream; only the ids whose
+      // patch may raise them are read again here.  The others are left out
+      // (flag kPatchSeen clear).
+      if (!ovf && npatch > 0) {
+        __syncthreads();  // every wave's captures are in
+        for (int p = tid; p < npatch; p += NT) {
+          uint32_t fl = pflag[p];
+          const uint32_t cnt = fl >> kPatchCountShift;
+          if (!(fl & kPatchSeen) && !may_rise(fl)) continue;
+          float v = patched_raw(p, fl);
+          if (cnt) {
+            if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
+            v = v - (float)((double)cnt * P.freq + P.pres);  // float64, one rounding (:74)
+          }
+          if (fl & kPatchBias) v = v + pbias[p];
+          if (!greedy) v = v * P.invT;
+          pfin[p] = v;
+          if (!(fl & kPatchSeen)) pflag[p] = fl | kPatchSeen;
+        }
+        __syncthreads();
       }
-      __syncthreads();
-      int any = 0;
-      N = 0;
-      rv = -__builtin_inff();
-      ri = 0x7fffffff;
-      for (int j = 0; j < a.S; ++j) {
-        const int nj = s_off[kMaxSlices + j];
-        any |= s_off[2 * kMaxSlices + j] | (nj < 0 ? kSliceOverflow : 0);
-        nan0 = nan0 || (s_off[2 * kMaxSlices + j] & kSliceNan0);
-        argmax_merge(rv, ri, __int_as_float(s_off[4 * kMaxSlices + j]), s_off[3 * kMaxSlices + j]);
-        s_off[j] = N;  // start of slice j in the merged buffer
-        if (nj > 0) N += nj;
-      }
-      ovf = (any & kSliceOverflow) != 0;
-      if (topk && !ovf) {
-        ent = cand;  // both ping-pong buffers: 2 * ccap >= S * pc entries
-        constexpr int MR = 8;  // loads in flight per thread
-        for (int b0 = 0; b0 < N; b0 += NT * MR) {
-          uint64_t xv[MR];
-  #pragma unroll
-          for (int r = 0; r < MR; ++r) {
-            const int i = b0 + r * NT + tid;
-            xv[r] = 0ull;
-            if (i < N) {
-              int j = 0;
-              while (j + 1 < a.S && s_off[j + 1] <= i) ++j;
-              xv[r] = load_agent(a.part_cand + ((int64_t)row * a.S + j) * a.pc + (i - s_off[j]));
+
+      // ---- the slice's candidates: stream buffer(s) + patched values ----
+      ent = cand + (size_t)cur * a.ccap;
+      N = buf_n;
+      if (topk) {
+        uint32_t tau_all = tau;  // a lower bound of the row's k-th largest, uniform
+        if constexpr (WAVE) {
+          // concatenate the wave buffers into the second buffer
+          if (lane == 0) {
+            s_wn[wv] = wovf ? -1 : wn;
+            s_wt[wv] = wtau;
+          }
+          __syncthreads();
+          int off = 0;
+          N = 0;
+          tau_all = 0u;
+          for (int w = 0; w < NW; ++w) {
+            const int nw_ = s_wn[w];
+            tau_all = max(tau_all, s_wt[w]);
+            if (nw_ < 0) {
+              ovf = true;
+            } else {
+              if (w == wv) off = N;
+              N += nw_;
             }
           }
-  #pragma unroll
-          for (int r = 0; r < MR; ++r) {
-            const int i = b0 + r * NT + tid;
-            if (i < N) ent[i] = xv[r];
+          ent = cand + a.ccap;
+          if (!ovf) {
+            const uint64_t* wb = cand + (size_t)wv * kWaveCap;
+            for (int i = lane; i < wn; i += kWave) ent[off + i] = wb[i];
           }
+          __syncthreads();
         }
+        if (!ovf && npatch > 0) {
+          // patched values >= tau_all join the candidates
+          if (tid == 0) s_cnt = N;
+          __syncthreads();
+          for (int p = tid; p < npatch; p += NT) {
+            if (!(pflag[p] & kPatchSeen)) continue;
+            const uint32_t kp = f2key(pfin[p]);
+            if (kp >= tau_all) {
+              const int i = atomicAdd(&s_cnt, 1);
+              if (i < a.ccap) ent[i] = ((uint64_t)kp << 32) | (uint32_t)pid[p];
+            }
+          }
+          __syncthreads();
+          N = s_cnt;
+          if (N > a.ccap) ovf = true;  // uniform
+          __syncthreads();
+          if (tid == 0) s_cnt = 0;
+        }
+      } else {
+        // greedy: patched final values join the argmax
+        for (int p = tid; p < npatch; p += NT)
+          if (pflag[p] & kPatchSeen) argmax_merge(bv, bi, pfin[p], pid[p]);
+      }
+      // argmax (:45-49) starts from index 0: when its value is NaN nothing
+      // compares greater and the answer stays 0
+      bool nan0 = false;
+      if (greedy && lo == 0 && len > 0 && tid == 0) {
+        float x0 = x0raw;
+        if (patched(0)) x0 = pfin[wpre[0] + 0];
+        nan0 = x0 != x0;
+      }
+
+      // ---- slice argmax (first index on ties) ----
+      wave_argmax(bv, bi);
+      if (lane == 0) {
+        s_rv[wv] = bv;
+        s_ri[wv] = bi;
       }
       __syncthreads();
-      for (int q = tid; q < 5 * kMaxSlices; q += NT) s_off[q] = 0;  // restore the zeroed histogram
-      __syncthreads();
+      float rv = s_rv[0];
+      int ri = s_ri[0];
+    #pragma unroll
+      for (int w = 1; w < NW; ++w) argmax_merge(rv, ri, s_rv[w], s_ri[w]);
+
+      if (a.S > 1) {
+        // ---- publish this slice; the last one to arrive completes the row ----
+        const int64_t part = (int64_t)row * a.S + sl;
+        uint64_t* pdst = a.part_cand + part * a.pc;
+        int nout = 0;
+        int flags = (ovf ? kSliceOverflow : 0) | (nan0 ? kSliceNan0 : 0);
+        if (topk && !ovf) {
+          if (N > a.pc) {
+            const SelectResult r = block_select<NT>(
+                [&](auto fn) {
+                  for (int i0 = 0; i0 < N; i0 += NT) {
+                    const int i = i0 + tid;
+                    const bool in = i < N;
+                    fn(in ? (uint32_t)(ent[i] >> 32) : 0u, in);
+                  }
+                },
+                k, a.pc, shist, smem);
+            if (r.ge > a.pc) {
+              flags = kSliceOverflow;
+            } else {
+              int mine = 0;
+              for (int i = tid; i < N; i += NT) mine += ((uint32_t)(ent[i] >> 32) >= r.tau);
+              int tot;
+              int pos = block_excl_scan<NT>(mine, smem, tot);
+              for (int i = tid; i < N; i += NT)
+                if ((uint32_t)(ent[i] >> 32) >= r.tau) store_agent(&pdst[pos++], ent[i]);
+              nout = tot;
+            }
+          } else {
+            for (int i = tid; i < N; i += NT) store_agent(&pdst[i], ent[i]);
+            nout = N;
+          }
+        }
+        if (tid == 0) {
+          store_agent(&a.part_info[part].n, nout);
+          store_agent(&a.part_info[part].flags, flags);
+          store_agent(&a.part_info[part].amax, ri);
+          store_agent(&a.part_info[part].vmax, __float_as_int(rv));
+        }
+        // The slice data above is written with agent-scope stores, which go to
+        // the device's point of coherence; waiting for their completion before
+        // the arrival count is bumped orders them without an L2 writeback.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0)
+          s_last = (__hip_atomic_fetch_add(&a.arrive[row], 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.S - 1));
+        __syncthreads();
+        if (!s_last) return;
+        if (tid == 0) __hip_atomic_store(&a.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // slice records: one per thread, then every thread reads them from LDS.
+        // s_off borrows the select histogram (free here; 5 * kMaxSlices words < kSelWords).
+        int* s_off = reinterpret_cast<int*>(shist);
+        static_assert(5 * kMaxSlices <= kSelWords, "slice records must fit the histogram");
+        if (tid < a.S) {
+          const SliceInfo* in = a.part_info + (int64_t)row * a.S + tid;
+          const int nj = load_agent(&in->n);
+          const int fl = load_agent(&in->flags);
+          s_off[kMaxSlices + tid] = (nj < 0 || nj > a.pc) ? -1 : nj;  // never trust a count past the buffer
+          s_off[2 * kMaxSlices + tid] = fl;
+          s_off[3 * kMaxSlices + tid] = load_agent(&in->amax);
+          s_off[4 * kMaxSlices + tid] = load_agent(&in->vmax);
+        }
+        __syncthreads();
+        int any = 0;
+        N = 0;
+        rv = -__builtin_inff();
+        ri = 0x7fffffff;
+        for (int j = 0; j < a.S; ++j) {
+          const int nj = s_off[kMaxSlices + j];
+          any |= s_off[2 * kMaxSlices + j] | (nj < 0 ? kSliceOverflow : 0);
+          nan0 = nan0 || (s_off[2 * kMaxSlices + j] & kSliceNan0);
+          argmax_merge(rv, ri, __int_as_float(s_off[4 * kMaxSlices + j]), s_off[3 * kMaxSlices + j]);
+          s_off[j] = N;  // start of slice j in the merged buffer
+          if (nj > 0) N += nj;
+        }
+        ovf = (any & kSliceOverflow) != 0;
+        if (topk && !ovf) {
+          ent = cand;  // both ping-pong buffers: 2 * ccap >= S * pc entries
+          constexpr int MR = 8;  // loads in flight per thread
+          for (int b0 = 0; b0 < N; b0 += NT * MR) {
+            uint64_t xv[MR];
+    #pragma unroll
+            for (int r = 0; r < MR; ++r) {
+              const int i = b0 + r * NT + tid;
+              xv[r] = 0ull;
+              if (i < N) {
+                int j = 0;
+                while (j + 1 < a.S && s_off[j + 1] <= i) ++j;
+                xv[r] = load_agent(a.part_cand + ((int64_t)row * a.S + j) * a.pc + (i - s_off[j]));
+              }
+            }
+    #pragma unroll
+            for (int r = 0; r < MR; ++r) {
+              const int i = b0 + r * NT + tid;
+              if (i < N) ent[i] = xv[r];
+            }
+          }
+        }
+        __syncthreads();
+        for (int q = tid; q < 5 * kMaxSlices; q += NT) s_off[q] = 0;  // restore the zeroed histogram
+        __syncthreads();
+      }
+      if (ovf) {
+        if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
+        return;
+      }
+      if (!topk) {
+        if (tid == 0) {
+          a.out[row] = nan0 ? 0 : ri;
+          if (a.dbg.n) a.dbg.n[row] = 0;
+          if (a.dbg.ncand) a.dbg.ncand[row] = 0;
+          if (a.dbg.total) a.dbg.total[row] = 0.0f;
+          if (a.dbg.path) a.dbg.path[row] = 1;
+        }
+        return;
+      }
     }
-    if (ovf) {
+    // ---- the row's heap-path members, then the reference's tail ----
+    uint64_t* mem = reinterpret_cast<uint64_t*>(regA);
+    if (!topk_members<NT>(ent, N, k, mem, a.mcap, shist, smem, &s_cnt)) {
       if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
       return;
     }
-    if (!topk) {
-      if (tid == 0) {
-        a.out[row] = nan0 ? 0 : ri;
-        if (a.dbg.n) a.dbg.n[row] = 0;
-        if (a.dbg.ncand) a.dbg.ncand[row] = 0;
-        if (a.dbg.total) a.dbg.total[row] = 0.0f;
-        if (a.dbg.path) a.dbg.path[row] = 1;
-      }
+    if (k <= kWave) {
+      if (wv != 0) return;
+      double u = 0.0;
+      if (lane == 0) u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
+      wave_tail(mem, k, P, u, row, a.out, a.dbg);
       return;
     }
+    // k > 64: block-wide sort of the members, then the block tail
+    float* vals = reinterpret_cast<float*>(mem + a.mcap);
+    int32_t* ids = reinterpret_cast<int32_t*>(vals + a.kcap);
+    float* ebuf = reinterpret_cast<float*>(ids + a.kcap);
+    const int kpow = next_pow2(k);
+    for (int i = k + tid; i < kpow; i += NT) mem[i] = 0ull;
+    __syncthreads();
+    bitonic_sort_u64<NT>(mem, kpow, true);
+    for (int i = tid; i < k; i += NT) {
+      vals[i] = key2f((uint32_t)(mem[i] >> 32));
+      ids[i] = (int32_t)(uint32_t)mem[i];
+    }
+    if (tid == 0) s_u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
+    __syncthreads();
+    const TailOut to = softmax_cutoff_draw<NT>(vals, ids, ebuf, k, P, s_u, smem);
+    if (tid == 0) a.out[row] = to.id;
+    write_debug<NT>(a.dbg, row, 2, to.n, k, to.total, ids, ebuf);
+  };
+  run();
+  if (a.gen_inline) {
+    // The last workgroup to finish serves the rows handed on to the
+    // whole-row path (their pushes precede every count below).
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __builtin_amdgcn_s_waitcnt(0);
+      s_last = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               gridDim.x - 1;
+    }
+    __syncthreads();
+    if (s_last) {
+      const int count = load_agent(a.ga.generic_count);
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        store_agent(a.done, 0u);
+        store_agent(a.ga.next_count, 0);
+      }
+      uint32_t* dl = reinterpret_cast<uint32_t*>(lds);
+      generic_rows<NT>(a.ga, 0, 1, count, shist, dl, dl + 256, smem, &s_u, reinterpret_cast<int*>(dl + 512),
+                       s_rv, s_ri);
+    }
   }
-  // ---- the row's heap-path members, then the reference's tail ----
-  uint64_t* mem = reinterpret_cast<uint64_t*>(regA);
-  if (!topk_members<NT>(ent, N, k, mem, a.mcap, shist, smem, &s_cnt)) {
-    if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
-    return;
-  }
-  if (k <= kWave) {
-    if (wv != 0) return;
-    double u = 0.0;
-    if (lane == 0) u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
-    wave_tail(mem, k, P, u, row, a.out, a.dbg);
-    return;
-  }
-  // k > 64: block-wide sort of the members, then the block tail
-  float* vals = reinterpret_cast<float*>(mem + a.mcap);
-  int32_t* ids = reinterpret_cast<int32_t*>(vals + a.kcap);
-  float* ebuf = reinterpret_cast<float*>(ids + a.kcap);
-  const int kpow = next_pow2(k);
-  for (int i = k + tid; i < kpow; i += NT) mem[i] = 0ull;
-  __syncthreads();
-  bitonic_sort_u64<NT>(mem, kpow, true);
-  for (int i = tid; i < k; i += NT) {
-    vals[i] = key2f((uint32_t)(mem[i] >> 32));
-    ids[i] = (int32_t)(uint32_t)mem[i];
-  }
-  if (tid == 0) s_u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
-  __syncthreads();
-  const TailOut to = softmax_cutoff_draw<NT>(vals, ids, ebuf, k, P, s_u, smem);
-  if (tid == 0) a.out[row] = to.id;
-  write_debug<NT>(a.dbg, row, 2, to.n, k, to.total, ids, ebuf);
 }
 
 // ---------------------------------------------------------------------------
@@ -1568,28 +1602,23 @@ __device__ __forceinline__ int upper_bound_u32(const uint32_t* a, int n, uint32_
 }
 
 
+// Rows of the list from index w0 on, every nw-th: the whole-row path.  LDS
+// scratch is passed in (wcnt: NW * 256 words, dbase and drun: 256 each), so
+// that the streaming kernel's last workgroup can run it too.
 template <int NT>
-__global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
+__device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int nw, int count, uint32_t* wcnt,
+                                             uint32_t* dbase, uint32_t* drun, int* smem, double* s_u_p,
+                                             int* s_i, float* s_rv, int* s_ri) {
   constexpr int NW = NT / kWave;
-  __shared__ uint32_t wcnt[NW * 256];
-  __shared__ uint32_t dbase[256];
-  __shared__ uint32_t drun[256];
-  __shared__ int smem[NW + 4];
-  __shared__ double s_u;
-  __shared__ int s_i[4];
-  __shared__ float s_rv[NW];
-  __shared__ int s_ri[NW];
   const int n = (int)a.V;
   const int tid = threadIdx.x;
-  uint32_t* kA = a.scratch + (int64_t)blockIdx.x * a.vpad * 5;
+  uint32_t* kA = a.scratch + (int64_t)w0 * a.vpad * 5;
   uint32_t* iA = kA + a.vpad;
   uint32_t* kB = iA + a.vpad;
   uint32_t* iB = kB + a.vpad;
   float* work = reinterpret_cast<float*>(iB + a.vpad);
-  if (blockIdx.x == 0 && tid == 0) *a.next_count = 0;
-  const int count = *a.generic_count;
-  for (int li = blockIdx.x; li < count; li += gridDim.x) {
-    const int row = a.generic_list[li];
+  for (int li = w0; li < count; li += nw) {
+    const int row = load_agent(&a.generic_list[li]);
     const RowParams P = a.rp[row];
     const float* __restrict__ src = a.logits + (int64_t)row * a.V;
     // window counts (kB) and bias slots + 1 (iB) per id (:64-76)
@@ -1666,13 +1695,13 @@ __global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
     radix_sort_pass<NT>(kA, iA, kB, iB, n, 16, wcnt, dbase, drun);
     radix_sort_pass<NT>(kB, iB, kA, iA, n, 24, wcnt, dbase, drun);
     // kA: ~key ascending (value descending, index ascending on ties)
-    if (tid == 0) s_u = row_uniform(a.d_u, a.rng, row);
+    if (tid == 0) *s_u_p = row_uniform(a.d_u, a.rng, row);
     __syncthreads();
     if (P.mode == kModeFull) {
       // candidates = the whole sorted row (:96-97); values into work, ids stay in iA
       for (int i = tid; i < n; i += NT) work[i] = key2f(~kA[i]);
       __syncthreads();
-      const TailOut t = softmax_cutoff_draw<NT>(work, iA, reinterpret_cast<float*>(kB), n, P, s_u,
+      const TailOut t = softmax_cutoff_draw<NT>(work, iA, reinterpret_cast<float*>(kB), n, P, *s_u_p,
                                                 smem);
       if (tid == 0) a.out[row] = t.id;
       write_debug<NT>(a.dbg, row, 4, t.n, n, t.total, iA, reinterpret_cast<float*>(kB));
@@ -1734,12 +1763,28 @@ __global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
     }
     __syncthreads();
     const TailOut t = softmax_cutoff_draw<NT>(work, reinterpret_cast<int32_t*>(kB),
-                                              reinterpret_cast<float*>(iB), k, P, s_u, smem);
+                                              reinterpret_cast<float*>(iB), k, P, *s_u_p, smem);
     if (tid == 0) a.out[row] = t.id;
     write_debug<NT>(a.dbg, row, 4, t.n, k, t.total, reinterpret_cast<int32_t*>(kB),
                     reinterpret_cast<float*>(iB));
     __syncthreads();
   }
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
+  constexpr int NW = NT / kWave;
+  __shared__ uint32_t wcnt[NW * 256];
+  __shared__ uint32_t dbase[256];
+  __shared__ uint32_t drun[256];
+  __shared__ int smem[NW + 4];
+  __shared__ double s_u;
+  __shared__ int s_i[4];
+  __shared__ float s_rv[NW];
+  __shared__ int s_ri[NW];
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.next_count = 0;
+  const int count = *a.generic_count;
+  generic_rows<NT>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri);
 }
 
 // ---------------------------------------------------------------------------
@@ -1810,8 +1855,9 @@ hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const Laun
   if (ev_start && (e = hipEventRecord(ev_start, s)) != hipSuccess) return e;
   if ((e = launch_stream(sa, lp, s)) != hipSuccess) return e;
   if (ev_stop && (e = hipEventRecord(ev_stop, s)) != hipSuccess) return e;
-  hipLaunchKernelGGL(generic_kernel<kGenericThreads>, dim3(lp.gen_blocks), dim3(kGenericThreads),
-                     0, s, ga);
+  if (!sa.gen_inline)
+    hipLaunchKernelGGL(generic_kernel<kGenericThreads>, dim3(lp.gen_blocks), dim3(kGenericThreads),
+                       0, s, ga);
   return hipGetLastError();
 }
 
