@@ -440,13 +440,14 @@ void stream_kernel(const StreamArgs a) {
   __shared__ int s_wn[NW];
   __shared__ uint32_t s_wt[NW];
   __shared__ uint32_t s_tau;  // wave path: the highest published wave threshold
-  __shared__ uint32_t s_top[kWave];  // wave path: the lane maxima of tile 0
+  __shared__ uint32_t s_top[kWave];  // wave path: the lane maxima of tile 0, then the buffer maxima
   __shared__ int s_tile_cnt[3];
   __shared__ int s_cnt;
   __shared__ int s_next;  // wave path: the next unclaimed chunk (after the first two of every wave)
   __shared__ float s_rv[NW];
   __shared__ int s_ri[NW];
   __shared__ int s_last;
+  __shared__ uint32_t s_te;  // wave path: the lead wave's bound, then its verdict
   __shared__ double s_u;
 
   // The row's work; every exit of it leads to the final section below.
@@ -1148,10 +1149,19 @@ void stream_kernel(const StreamArgs a) {
       __syncthreads();  // every wave's stream, captures and offers are in
       // lane w reads wave w's record
       ovf = ovf || __ballot(lane < NW && s_wn[min(lane, NW - 1)] < 0) != 0ull;
-      const uint32_t tau_all = wave_max_u32(lane < NW ? s_wt[min(lane, NW - 1)] : 0u);
       ent = cand + a.ccap;  // free: holds NW * kWaveCap entries and more
-      if (!ovf) {
-        const uint32_t te = max(tau_all, wave_kth_largest(lane < NW * M ? s_top[lane] : 0u, k));
+      // One wave computes what every wave needs next (the scalar unit and the
+      // SIMDs are shared: sixteen waves computing the same bound take longer
+      // than one); the others wait at the barrier.
+      const bool lead = __builtin_amdgcn_readfirstlane(wv) == 0;
+      if (!ovf) {  // uniform
+        if (lead) {
+          const uint32_t tau_all = wave_max_u32(lane < NW ? s_wt[min(lane, NW - 1)] : 0u);
+          const uint32_t t = max(tau_all, wave_kth_largest(lane < NW * M ? s_top[lane] : 0u, k));
+          if (lane == 0) s_te = t;
+        }
+        __syncthreads();
+        const uint32_t te = __builtin_amdgcn_readfirstlane(s_te);
         // this wave's entries >= te
         int c = 0;
   #pragma unroll
@@ -1186,24 +1196,30 @@ void stream_kernel(const StreamArgs a) {
         return;
       }
       if (N >= k && N <= 2 * kWave) {
-        // every wave finds the k-th largest key T of the survivors itself
-        const uint64_t e0 = lane < N ? ent[lane] : 0ull;
-        const uint64_t e1 = lane + kWave < N ? ent[lane + kWave] : 0ull;
-        const uint32_t k0 = (uint32_t)(e0 >> 32), k1 = (uint32_t)(e1 >> 32);
-        uint32_t T = 0u;
-        if (N <= kWave) {
-          T = wave_kth_largest(k0, k);
-        } else {
+        // the lead wave finds the k-th largest key T of the survivors
+        uint64_t e0 = 0ull, e1 = 0ull;
+        uint32_t k0 = 0u, k1 = 0u, T = 0u;
+        if (lead) {
+          e0 = lane < N ? ent[lane] : 0ull;
+          e1 = lane + kWave < N ? ent[lane + kWave] : 0ull;
+          k0 = (uint32_t)(e0 >> 32);
+          k1 = (uint32_t)(e1 >> 32);
+          if (N <= kWave) {
+            T = wave_kth_largest(k0, k);
+          } else {
   #pragma unroll
-          for (int b = 31; b >= 0; --b) {
-            const uint32_t c = T | (1u << b);
-            if (__popcll(__ballot(k0 >= c)) + __popcll(__ballot(k1 >= c)) >= k) T = c;
+            for (int b = 31; b >= 0; --b) {
+              const uint32_t c = T | (1u << b);
+              if (__popcll(__ballot(k0 >= c)) + __popcll(__ballot(k1 >= c)) >= k) T = c;
+            }
           }
+          const int ge = __popcll(__ballot(lane < N && k0 >= T)) + __popcll(__ballot(lane + kWave < N && k1 >= T));
+          if (lane == 0) s_te = (ge == k) ? 1u : 0u;
         }
-        const int ge = __popcll(__ballot(lane < N && k0 >= T)) + __popcll(__ballot(lane + kWave < N && k1 >= T));
-        if (ge == k) {
+        __syncthreads();
+        if (__builtin_amdgcn_readfirstlane(s_te) != 0u) {
           // no excess ties at T: the members are exactly the survivors >= T
-          if (wv != 0) return;
+          if (!lead) return;
           uint64_t* mem = reinterpret_cast<uint64_t*>(regA);
           const bool in0 = lane < N && k0 >= T, in1 = lane + kWave < N && k1 >= T;
           const uint64_t m0 = __ballot(in0), m1 = __ballot(in1);
