@@ -432,6 +432,8 @@ void stream_kernel(const StreamArgs a) {
   constexpr int UE = WAVE ? kWave * NE : TE;  // floats per unit
   constexpr int GS = WAVE ? kWave * 4 : NT * 4;  // floats between a thread's groups
   constexpr int PER = kWaveCap / kWave;  // wave path: buffer entries per lane
+  constexpr int M0 = (kWave + NW - 1) / NW;  // wave path: offers per wave (NW * M0 >= 64 >= k)
+  constexpr int kMidUnits = 3;  // wave path: units before every wave offers its buffer maxima
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ int smem[NW + 4];
   // block_select histogram; while streaming, the wave path's per-wave ones
@@ -448,6 +450,8 @@ void stream_kernel(const StreamArgs a) {
   __shared__ int s_ri[NW];
   __shared__ int s_last;
   __shared__ uint32_t s_te;  // wave path: the lead wave's bound, then its verdict
+  __shared__ uint32_t s_mid[kWave];  // wave path: every wave's largest buffer keys after its first units
+  __shared__ int s_midn;             // wave path: the waves that have written theirs
   __shared__ double s_u;
 
   // The row's work; every exit of it leads to the final section below.
@@ -553,12 +557,14 @@ void stream_kernel(const StreamArgs a) {
       }
     }
     for (int q = tid; q < kHistWords; q += NT) shist[q] = 0u;  // the selects need it zeroed
+    if (tid < kWave) s_mid[tid] = 0u;
     if (tid == 0) {
       s_tile_cnt[0] = 0;
       s_tile_cnt[1] = 0;
       s_tile_cnt[2] = 0;
       s_cnt = 0;
       s_tau = 0u;
+      s_midn = 0;
       s_next = 2 * NW;
     }
 
@@ -730,6 +736,7 @@ void stream_kernel(const StreamArgs a) {
     int wn = 0;
     uint32_t wtau = 0u;
     bool wovf = false;
+    int nu = 0;  // wave path: units this wave has processed after its first
 
     // t: the unit; first: the first unit of every thread (tile 0 of the row)
     auto process = [&](float (&v)[NE], int t, bool first) __attribute__((always_inline)) {
@@ -783,6 +790,45 @@ void stream_kernel(const StreamArgs a) {
         // (NaN passes too), so keys are formed only where some lane passes.
         uint64_t* wb = cand + (size_t)wv * kWaveCap;
         uint32_t* whist = shist + wv * kWaveBins;
+        if (!first && nu++ == kMidUnits - 1) {
+          // After its first kMidUnits units every wave offers the M largest
+          // keys of its buffer (distinct elements at or above the threshold),
+          // and the last to do so takes the k-th largest of all NW * M offers:
+          // a bound from NW * kMidUnits units rather than the first tile,
+          // published through s_tau.  (An offer not yet written reads 0, which
+          // only lowers the bound.)
+          uint32_t kr[PER];
+  #pragma unroll
+          for (int j = 0; j < PER; ++j) {
+            const int i = lane + j * kWave;
+            kr[j] = i < wn ? (uint32_t)(wb[i] >> 32) : 0u;
+          }
+  #pragma unroll
+          for (int i = 0; i < M0; ++i) {
+            uint32_t lm = 0u;
+  #pragma unroll
+            for (int j = 0; j < PER; ++j) lm = max(lm, kr[j]);
+            const uint32_t m = wave_max_u32(lm);
+            const uint64_t at = __ballot(lm == m);
+            if (lane == __ffsll((unsigned long long)at) - 1) {
+              bool done = false;
+  #pragma unroll
+              for (int j = 0; j < PER; ++j)
+                if (!done && kr[j] == m) {
+                  kr[j] = 0u;
+                  done = true;
+                }
+            }
+            if (lane == 0) s_mid[wv * M0 + i] = m;
+          }
+          int prev = 0;
+          if (lane == 0) prev = atomicAdd(&s_midn, 1);
+          if (__builtin_amdgcn_readfirstlane(prev) == NW - 1) {
+            const uint32_t t = wave_kth_largest(lane < NW * M0 ? s_mid[lane] : 0u, k);
+            wtau = max(wtau, t);
+            if (lane == 0) atomicMax(&s_tau, t);
+          }
+        }
         if (first) {
           // Block-wide start: every wave puts the M largest of its lanes'
           // maxima (distinct elements) into LDS, and the k-th largest of those
