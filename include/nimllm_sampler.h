@@ -139,6 +139,18 @@ int nls_rng_uniforms(int64_t seed, int64_t n, double* out);
 int nls_get_rng_state(nls_sampler* s, int32_t row, uint64_t* a0, uint64_t* a1);
 int nls_set_rng_state(nls_sampler* s, int32_t row, uint64_t a0, uint64_t a1);
 
+/* topTokens (src/nimllm/sampler.nim:123-130): for each of `rows` rows of
+ * d_logits [rows x vocab] (device, row-major), softmaxInPlace over the whole row
+ * (:51-57: maximum, exp(l - max), fp32 sum in index order, division), then the
+ * first m = min(n, vocab) entries of the stable sort by probability, descending
+ * (equal probabilities keep ascending ids).  Row r's ids and probabilities go
+ * to d_ids[r * n + j] and d_probs[r * n + j], j < m.  Asynchronous on `stream`.
+ * m <= 0 or rows == 0 does nothing; m > 2048 is NLS_ERR_INVALID_ARGUMENT.
+ * Rows holding NaN (or +inf with other values) have NaN probabilities, whose
+ * order the reference's comparator leaves undefined: ids 0.. m-1 are returned. */
+int nls_top_tokens(const float* d_logits, int32_t rows, int64_t vocab, int32_t n, int32_t* d_ids,
+                   float* d_probs, void* stream);
+
 /* Correctly rounded exp on fp32 inputs, on the device: d_out[i] = exp(d_in[i]). */
 int nls_expf_device(const float* d_in, float* d_out, int64_t n, void* stream);
 

@@ -30,7 +30,7 @@ EXPORTED = (
     "nls_set_stream", "nls_batch", "nls_vocab", "nls_accept", "nls_accept_row",
     "nls_accept_device", "nls_clear_history", "nls_sample", "nls_sample_host",
     "nls_synchronize", "nls_rng_uniforms", "nls_get_rng_state", "nls_set_rng_state",
-    "nls_expf_device", "nls_profile_next", "nls_status_string", "nls_last_error",
+    "nls_top_tokens", "nls_expf_device", "nls_profile_next", "nls_status_string", "nls_last_error",
 )
 
 
@@ -98,6 +98,7 @@ def lib():
         L.nls_rng_uniforms.argtypes = [ctypes.c_int64, ctypes.c_int64, P(ctypes.c_double)]
         L.nls_get_rng_state.argtypes = [vp, ctypes.c_int32, P(ctypes.c_uint64), P(ctypes.c_uint64)]
         L.nls_set_rng_state.argtypes = [vp, ctypes.c_int32, ctypes.c_uint64, ctypes.c_uint64]
+        L.nls_top_tokens.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, vp, vp, vp]
         L.nls_expf_device.argtypes = [vp, vp, ctypes.c_int64, vp]
         L.nls_profile_next.argtypes = [vp, vp, vp]
         L.nls_status_string.argtypes = [ctypes.c_int]
@@ -323,6 +324,41 @@ def newSampler(p: Optional[SamplerParams] = None, vocab: int = 0) -> Sampler:
     if vocab <= 0:
         raise SamplerError("newSampler needs the vocabulary size")
     return Sampler(p if p is not None else defaultSampling(), vocab)
+
+
+TOP_TOKENS_MAX = 2048  # largest number of entries per row nls_top_tokens returns
+
+
+def top_tokens_device(logits, n: int = 5):
+    """topTokens (sampler.nim:123-130) for a [rows, V] float32 device tensor:
+    returns int32 ids and float32 probabilities, both [rows, min(n, V)], in the
+    reference's order (probability descending, ascending id on ties)."""
+    import torch
+
+    x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    rows, V = x.shape
+    m = max(0, min(n, V))
+    ids = torch.empty((rows, max(n, 1)), dtype=torch.int32, device=x.device)
+    probs = torch.empty((rows, max(n, 1)), dtype=torch.float32, device=x.device)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    check(lib().nls_top_tokens(ctypes.c_void_p(x.data_ptr()), rows, V, n,
+                               ctypes.c_void_p(ids.data_ptr()), ctypes.c_void_p(probs.data_ptr()),
+                               ctypes.c_void_p(stream)), "nls_top_tokens")
+    return ids[:, :m], probs[:, :m]
+
+
+def topTokens(logits, n: int = 5):
+    """topTokens (sampler.nim:123-130): the n most probable ids of one row of
+    logits (any float32 sequence or tensor) with their probabilities, as a list
+    of (id, probability) pairs, computed on the device."""
+    import numpy as np
+    import torch
+
+    x = logits if torch.is_tensor(logits) else torch.from_numpy(np.ascontiguousarray(logits, dtype=np.float32))
+    x = x.reshape(1, -1).to(device="cuda", dtype=torch.float32).contiguous()
+    ids, probs = top_tokens_device(x, n)
+    return [(int(i), float(p)) for i, p in zip(ids[0].tolist(), probs[0].tolist())]
 
 
 def expf_device(x, out=None):

@@ -701,6 +701,17 @@ int nls_set_rng_state(nls_sampler* s, int32_t row, uint64_t a0, uint64_t a1) {
   return NLS_OK;
 }
 
+int nls_top_tokens(const float* d_logits, int32_t rows, int64_t vocab, int32_t n, int32_t* d_ids,
+                   float* d_probs, void* stream) {
+  if (rows < 0 || vocab < 0 || vocab > INT32_MAX) return NLS_ERR_INVALID_ARGUMENT;
+  const int64_t m = std::min<int64_t>(n, vocab);  // topTokens returns min(n, len) entries (:130)
+  if (rows == 0 || m <= 0) return NLS_OK;
+  if (m > nls::kTopMaxN || !d_logits || !d_ids || !d_probs) return NLS_ERR_INVALID_ARGUMENT;
+  NLS_HIP(launch_top_tokens(d_logits, rows, vocab, n, d_ids, d_probs,
+                            reinterpret_cast<hipStream_t>(stream)));
+  return NLS_OK;
+}
+
 int nls_expf_device(const float* d_in, float* d_out, int64_t n, void* stream) {
   if (n < 0 || (n > 0 && (!d_in || !d_out))) return NLS_ERR_INVALID_ARGUMENT;
   NLS_HIP(launch_expf(d_in, d_out, n, reinterpret_cast<hipStream_t>(stream)));

@@ -148,6 +148,12 @@ hipError_t launch_accept_host(const int32_t* d_ids, int B, int count, int32_t* h
 hipError_t launch_accept_device(const int32_t* d_ids, int B, int64_t V, int32_t* hist,
                                 int64_t* hist_len, int hcap, hipStream_t s);
 hipError_t launch_expf(const float* x, float* y, int64_t n, hipStream_t s);
+// topTokens over `rows` rows of V logits: n results per row (stride n), n <= kTopMaxN or V <= kTopMaxN
+constexpr int kTopThreads = 1024;
+constexpr int kTopChunk = 4096;  // exponentials per chunk of the sequential sum
+constexpr int kTopMaxN = 2048;   // largest number of results per row (sorted in LDS)
+hipError_t launch_top_tokens(const float* logits, int rows, int64_t V, int n, int32_t* ids,
+                             float* probs, hipStream_t s);
 hipError_t set_kernel_attributes();
 size_t max_dynamic_lds();
 

@@ -844,17 +844,21 @@ void stream_kernel(const StreamArgs a) {
             const int o = obase + j * GS;
             pbits[j] = bitmap[min(o, len - 1) >> 5] >> (o & 31);
           }
+          // (the maximum is taken on the floats and keyed once: v_max_f32
+          // returns one of its operands, so the lane's maximum is one of its
+          // own unpatched elements whatever NaNs or signed zeros it meets)
+          float fmx = -__builtin_inff();
   #pragma unroll
           for (int j = 0; j < NV4; ++j) {
             const uint32_t pb = has_patch ? pbits[j] : 0u;
   #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int q = 4 * j + e;
-              const uint32_t kq = f2key(sv[q]);
               const bool ok = valid(q) & !((pb >> e) & 1u);
-              lmax = ok ? max(lmax, kq) : lmax;
+              fmx = __builtin_fmaxf(fmx, ok ? sv[q] : -__builtin_inff());
             }
           }
+          lmax = fmx == -__builtin_inff() ? 0u : f2key(fmx);
   #pragma unroll
           for (int i = 0; i < M; ++i) {
             const uint32_t m = wave_max_u32(lmax);
@@ -1850,6 +1854,145 @@ __global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// 3. top_tokens_kernel -- topTokens (sampler.nim:123-130)
+// ---------------------------------------------------------------------------
+// One workgroup per row: softmaxInPlace (:51-57) over the whole row -- the
+// maximum, exp(l - mx), the fp32 sum in index order, the division -- and the
+// first n entries of the stable sort by probability (:127-128).  The
+// probabilities are recomputed from the logits wherever they are needed, so
+// the row is read a few times and only the n results are written.
+//   * The sum runs in index order, one add at a time, in lane 0 of wave 0,
+//     while the other waves compute the next chunk's exponentials into LDS.
+//   * The n-th largest probability T comes from an exact radix select on the
+//     probabilities' keys.  Among the entries equal to T the stable sort keeps
+//     the lowest indices, found by a second select on the index.  (Equal
+//     probabilities can come from different logits: the exp and the division
+//     round, so the order cannot be taken from the logits.)
+//   * The members are sorted by (probability desc, index asc) in LDS.
+// A row holding NaN, or +inf with anything else, has NaN probabilities; the
+// reference's comparator is no order on NaN, so such rows are outside the
+// parity claim (this kernel then returns the first indices).
+template <int NT>
+__global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict__ logits, int64_t V,
+                                                        int n, int32_t* __restrict__ ids,
+                                                        float* __restrict__ probs) {
+  constexpr int NW = NT / kWave;
+  static_assert((size_t)kTopChunk * 2 * sizeof(float) >= (size_t)kTopMaxN * sizeof(uint64_t),
+                "the members reuse the chunk buffers");
+  __shared__ __align__(16) float ebuf[2][kTopChunk];
+  __shared__ uint32_t hist[kSelWords];
+  __shared__ int smem[NW + 4];
+  __shared__ float s_part[NW];
+  __shared__ float s_sum;
+  __shared__ int s_cnt;
+  const int row = (int)blockIdx.x;
+  const int tid = (int)threadIdx.x;
+  const int lane = lane_id();
+  const int wv = tid >> 6;
+  const float* __restrict__ x = logits + (int64_t)row * V;
+  const int m = (int)min((int64_t)n, V);  // 1 <= m <= kTopMaxN (checked by the host)
+  for (int q = tid; q < kSelWords; q += NT) hist[q] = 0u;
+
+  // (1) mx (:53): nim's max(mx, v) takes v when mx <= v, so NaN is never
+  // taken; the float maximum of the rest (its sign of zero changes no l - mx)
+  float mx = -__builtin_inff();
+  for (int64_t i = tid; i < V; i += NT) mx = __builtin_fmaxf(mx, x[i]);
+  for (int o = kWave / 2; o > 0; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) s_part[wv] = mx;
+  __syncthreads();
+  mx = s_part[0];
+  for (int w = 1; w < NW; ++w) mx = __builtin_fmaxf(mx, s_part[w]);
+
+  // (2) s = e_0 + e_1 + ... in index order (:54-56): chunk c is computed by
+  // waves 1.. into ebuf[c & 1] while lane 0 of wave 0 adds chunk c - 1
+  const int64_t nch = (V + kTopChunk - 1) / kTopChunk;
+  float s = 0.0f;
+  for (int64_t c = 0; c <= nch; ++c) {
+    if (wv != 0 && c < nch) {
+      const int64_t c0 = c * kTopChunk;
+      float* eb = ebuf[c & 1];
+      for (int j = tid - kWave; j < kTopChunk; j += NT - kWave) {
+        const int64_t i = c0 + j;
+        eb[j] = i < V ? expf_cr(x[i] - mx) : 0.0f;
+      }
+    }
+    if (wv == 0 && c > 0 && lane == 0) {
+      const int64_t c0 = (c - 1) * kTopChunk;
+      const int cnt = (int)min((int64_t)kTopChunk, V - c0);
+      const float* eb = ebuf[(c - 1) & 1];
+      const f32x4* e4 = reinterpret_cast<const f32x4*>(eb);
+      int j = 0;
+#pragma unroll 2
+      for (; j + 16 <= cnt; j += 16) {
+        const f32x4 a = e4[j / 4], b = e4[j / 4 + 1], cc = e4[j / 4 + 2], d = e4[j / 4 + 3];
+        s = s + a.x; s = s + a.y; s = s + a.z; s = s + a.w;
+        s = s + b.x; s = s + b.y; s = s + b.z; s = s + b.w;
+        s = s + cc.x; s = s + cc.y; s = s + cc.z; s = s + cc.w;
+        s = s + d.x; s = s + d.y; s = s + d.z; s = s + d.w;
+      }
+      for (; j < cnt; ++j) s = s + eb[j];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) s_sum = s;
+  __syncthreads();
+  s = s_sum;
+  // probs[i] /= s (:57)
+  auto pkey = [&](int64_t i) -> uint32_t { return f2key(expf_cr(x[i] - mx) / s); };
+
+  // (3) the m-th largest probability key T
+  const SelectResult sr = block_select<NT>(
+      [&](auto fn) {
+        for (int64_t i0 = 0; i0 < V; i0 += NT) {
+          const int64_t i = i0 + tid;
+          const bool in = i < V;
+          fn(in ? pkey(i) : 0u, in);
+        }
+      },
+      m, -1, hist, smem);
+  const uint32_t T = sr.tau;
+  // (4) ties at T: the stable sort keeps the lowest indices; the (m - gt)-th
+  // lowest index among them is the last one kept
+  uint32_t imax = 0xffffffffu;
+  if (sr.ge > m) {
+    __syncthreads();
+    const SelectResult st = block_select<NT>(
+        [&](auto fn) {
+          for (int64_t i0 = 0; i0 < V; i0 += NT) {
+            const int64_t i = i0 + tid;
+            const bool in = i < V && pkey(i) == T;
+            fn(in ? 0xffffffffu - (uint32_t)i : 0u, in);
+          }
+        },
+        m - sr.gt, -1, hist, smem);
+    imax = 0xffffffffu - st.tau;
+  }
+  // (5) the members, sorted by (key desc, index asc): key << 32 | ~index
+  uint64_t* mem = reinterpret_cast<uint64_t*>(&ebuf[0][0]);
+  if (tid == 0) s_cnt = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < V; i += NT) {
+    const uint32_t k = pkey(i);
+    if (k > T || (k == T && (uint32_t)i <= imax)) {
+      const int slot = atomicAdd(&s_cnt, 1);
+      if (slot < kTopMaxN) mem[slot] = ((uint64_t)k << 32) | (0xffffffffu - (uint32_t)i);
+    }
+  }
+  __syncthreads();
+  const int got = min(s_cnt, kTopMaxN);  // == m
+  const int mp = next_pow2(m);
+  for (int i = got + tid; i < mp; i += NT) mem[i] = 0ull;  // below every real key
+  __syncthreads();
+  bitonic_sort_u64<NT>(mem, mp, true);
+  __syncthreads();
+  for (int j = tid; j < m; j += NT) {
+    const uint64_t e = mem[j];
+    ids[(int64_t)row * n + j] = (int32_t)(0xffffffffu - (uint32_t)e);
+    probs[(int64_t)row * n + j] = key2f((uint32_t)(e >> 32));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // small helpers
 // ---------------------------------------------------------------------------
 __global__ void accept_host_kernel(const int32_t* __restrict__ ids, int B, int count,
@@ -1961,6 +2104,13 @@ hipError_t set_kernel_attributes() {
   if ((e = set_attr_q<256, false>()) != hipSuccess) return e;
   if ((e = set_attr_q<1024, true>()) != hipSuccess) return e;
   return set_attr_q<1024, false>();
+}
+
+hipError_t launch_top_tokens(const float* logits, int rows, int64_t V, int n, int32_t* ids,
+                             float* probs, hipStream_t s) {
+  hipLaunchKernelGGL(top_tokens_kernel<kTopThreads>, dim3(rows), dim3(kTopThreads), 0, s, logits, V, n,
+                     ids, probs);
+  return hipGetLastError();
 }
 
 hipError_t launch_expf(const float* x, float* y, int64_t n, hipStream_t s) {

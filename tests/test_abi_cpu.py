@@ -61,6 +61,13 @@ def test_error_paths_without_device(pkg):
     assert L.nls_sample(None, None, None, None, None) == 1
     assert L.nls_accept(None, None, 0) == 1
     assert L.nls_rng_uniforms(1, -1, None) == 1
+    # topTokens: nothing to return is a no-op; more than 2048 results per row,
+    # negative sizes and missing buffers are rejected before any device work
+    assert L.nls_top_tokens(None, 1, 10, 0, None, None, None) == 0
+    assert L.nls_top_tokens(None, 0, 10, 5, None, None, None) == 0
+    assert L.nls_top_tokens(None, -1, 10, 5, None, None, None) == 1
+    assert L.nls_top_tokens(None, 1, 100000, 3000, None, None, None) == 1
+    assert L.nls_top_tokens(None, 1, 100, 5, None, None, None) == 1
     assert L.nls_status_string(5) == b"no usable device"
     import torch
 

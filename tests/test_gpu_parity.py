@@ -371,3 +371,52 @@ def test_expf_exhaustive_checksum(pkg, torch):
             total += z.sum()
     got = int(total.item()) & M
     assert got == 0xB06E5AA31AE210E1, hex(got)
+
+
+def _oracle_top_tokens(x, n):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = min(n, x.size)
+    ids = np.zeros(max(m, 1), dtype=np.int64)
+    pr = np.zeros(max(m, 1), dtype=np.float32)
+    got = O.lib().nlo_top_tokens(x.ctypes.data_as(O.ctypes.POINTER(O.ctypes.c_float)), x.size, n,
+                                 O.EXPF_CR, ids.ctypes.data_as(O.ctypes.POINTER(O.ctypes.c_int64)),
+                                 pr.ctypes.data_as(O.ctypes.POINTER(O.ctypes.c_float)))
+    return ids[:got], pr[:got]
+
+
+def test_top_tokens_parity(pkg, torch):
+    """topTokens (sampler.nim:123-130) on the device: ids and probabilities
+    bit-identical to the oracle, including probabilities that tie although
+    their logits differ (ordered by id), -inf entries, n beyond V and n at the
+    2048 cap."""
+    rng = np.random.default_rng(11)
+    cases = [("normal 128256", rng.normal(0, 2.5, (4, 128256)).astype(np.float32), (5, 50, 2048)),
+             ("quarter steps", (np.round(rng.normal(0, 2, (3, 32000)) * 4) / 4).astype(np.float32),
+              (1, 100, 700))]
+    col = rng.normal(-6, 1, (2, 4096)).astype(np.float32)
+    col[:, [3, 10, 400, 999]] = np.array([-2.5e-8, -1e-8, 0.0, -2e-8], np.float32)
+    cases.append(("probabilities tied by rounding", col, (4, 9)))
+    neg = rng.normal(0, 1, (2, 5000)).astype(np.float32)
+    neg[:, ::2] = -np.inf
+    cases.append(("every other -inf", neg, (10,)))
+    cases.append(("all equal", np.full((1, 1000), 0.75, np.float32), (7,)))
+    cases.append(("V below n", rng.normal(0, 1, (3, 10)).astype(np.float32), (20, 10, 1)))
+    cases.append(("V = 1", np.array([[1.5]], np.float32), (5,)))
+    for name, x, ns in cases:
+        d = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+        for n in ns:
+            say(f"topTokens {name}: rows={x.shape[0]} V={x.shape[1]} n={n}")
+            ids, pr = pkg.top_tokens_device(d, n)
+            torch.cuda.synchronize()
+            ids, pr = ids.cpu().numpy(), pr.cpu().numpy()
+            assert ids.shape == (x.shape[0], min(n, x.shape[1]))
+            for r in range(x.shape[0]):
+                wi, wp = _oracle_top_tokens(x[r], n)
+                assert np.array_equal(ids[r], wi), (name, n, r, ids[r][:8], wi[:8])
+                assert np.array_equal(pr[r].view(np.uint32), wp.view(np.uint32)), (name, n, r)
+    # the reference's signature: one row in, (id, probability) pairs out
+    x = cases[1][1][0]
+    wi, wp = _oracle_top_tokens(x, 5)
+    assert pkg.topTokens(x, 5) == [(int(i), float(p)) for i, p in zip(wi, wp)]
+    with pytest.raises(pkg.SamplerError):
+        pkg.top_tokens_device(torch.zeros((1, 5000), device="cuda"), 2049)

@@ -279,3 +279,55 @@ def test_top_tokens_and_softmax():
     assert m == 3 and list(ids) == [1, 2, 0]
     e = np.exp(x.astype(np.float64) - 3.0)
     assert np.allclose(pr, (e / e.sum())[[1, 2, 0]], rtol=1e-6)
+
+
+def _oracle_top_tokens(x, n, mode=None):
+    mode = O.EXPF_CR if mode is None else mode
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = min(n, x.size)
+    ids = np.zeros(max(m, 1), dtype=np.int64)
+    pr = np.zeros(max(m, 1), dtype=np.float32)
+    got = O.lib().nlo_top_tokens(x.ctypes.data_as(O.ctypes.POINTER(O.ctypes.c_float)), x.size, n, mode,
+                                 ids.ctypes.data_as(O.ctypes.POINTER(O.ctypes.c_int64)),
+                                 pr.ctypes.data_as(O.ctypes.POINTER(O.ctypes.c_float)))
+    return ids[:got], pr[:got]
+
+
+def _numpy_top_tokens(x, n):
+    """softmaxInPlace (:51-57) and the stable descending sort (:127-128) from
+    numpy parts: exp per element through the oracle's correctly rounded expf,
+    the fp32 sum accumulated strictly in index order (np.add.accumulate), and
+    numpy's stable argsort."""
+    x = np.asarray(x, dtype=np.float32)
+    mx = np.float32(-np.inf)
+    for v in x:
+        if mx <= v:
+            mx = v
+    e = np.array([O.lib().nlo_expf_cr(float(np.float32(v - mx))) for v in x], dtype=np.float32)
+    s = np.add.accumulate(e, dtype=np.float32)[-1]
+    p = (e / s).astype(np.float32)
+    order = np.argsort(-p, kind="stable")[:min(n, x.size)]
+    return order, p[order]
+
+
+def test_top_tokens_oracle_pins():
+    """The oracle's topTokens against a numpy restatement built from library
+    parts, on rows where probabilities tie although the logits differ (the
+    order must follow the probability, then the index, not the logit)."""
+    rng = np.random.default_rng(7)
+    rows = [rng.normal(0, 2.5, 3000).astype(np.float32),
+            (np.round(rng.normal(0, 2, 2000) * 4) / 4).astype(np.float32),
+            np.full(50, 1.25, np.float32)]
+    col = rng.normal(-6, 1, 1000).astype(np.float32)
+    # four logits within 2.9e-8 below the maximum: exp rounds them to 1.0, so
+    # their probabilities equal the maximum's and they follow in index order
+    col[[3, 10, 400, 999]] = np.array([-2.5e-8, -1e-8, 0.0, -2e-8], np.float32)
+    rows.append(col)
+    for x in rows:
+        for n in (1, 5, 37, 4000):
+            ids, pr = _oracle_top_tokens(x, n)
+            want_ids, want_p = _numpy_top_tokens(x, n)
+            assert np.array_equal(ids, want_ids)
+            assert np.array_equal(pr.view(np.uint32), want_p.view(np.uint32))
+    ids, _ = _oracle_top_tokens(col, 4)
+    assert list(ids) == [3, 10, 400, 999]
