@@ -88,6 +88,86 @@ def cpu_baseline(w, budget_s=12.0):
                       f"{glibc[0]} {glibc[1]}"}
 
 
+def bench_top_tokens(args):
+    """topTokens (sampler.nim:123-130) on the headline logits: n = 5 per row.
+    One line of JSON like the sampler's, for this entry point."""
+    import ctypes
+    import numpy as np
+    import torch
+
+    pkg = load_pkg()
+    from nimllm_amd import workloads
+
+    w = workloads.make(args.workload, seed=args.seed)
+    B, V, n = w.B, w.V, args.top_n
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    nbuf = max(2, math.ceil(640e6 / (B * V * 4)))
+    base = torch.from_numpy(w.logits).to(dev)
+    bufs = [base] + [base.clone() for _ in range(nbuf - 1)]
+    ids, pr = pkg.top_tokens_device(bufs[0], n)
+    torch.cuda.synchronize()
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    ok = True
+    for r in (0, B // 2, B - 1):
+        wi = np.zeros(n, dtype=np.int64)
+        wp = np.zeros(n, dtype=np.float32)
+        x = np.ascontiguousarray(w.logits[r])
+        O.lib().nlo_top_tokens(x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), V, n, O.EXPF_CR,
+                               wi.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                               wp.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        ok &= bool(np.array_equal(ids[r].cpu().numpy(), wi)) and bool(
+            np.array_equal(pr[r].cpu().numpy().view(np.uint32), wp.view(np.uint32)))
+    for i in range(args.warmup):
+        pkg.top_tokens_device(bufs[i % nbuf], n)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.steps):
+        pkg.top_tokens_device(bufs[i % nbuf], n)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = float(B * V * 4 + B * n * 8)  # logits once, ids and probabilities out
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    # the reference's sum is V dependent fp32 adds per row; one add issues every
+    # 4 cycles (a wave64 VALU instruction) at the 2.4 GHz peak engine clock
+    chain_us = V * 4 / 2.4e3
+    res = {"metric": f"topTokens rows/sec at B={B} x V={V} fp32, n={n}", "value": B / (ms * 1e-3),
+           "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f32", "data": "synthetic (the sampler workload's logits, rotated over "
+                                   f"{nbuf} buffers)",
+           "config": {"workload": f"{args.workload} logits, topTokens n={n}", "B": B, "V": V},
+           "roofline": {"bound": "latency", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                        "kernel": "top_tokens_kernel", "kernel_avg_us": ms * 1e3,
+                        "algorithmic_bytes_per_launch": nbytes,
+                        "sum_chain_bound_us": chain_us, "frac_of_chain_bound": chain_us / (ms * 1e3)},
+           "parity_spot_check": {"rows": 3, "bit_exact": ok}}
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        done = 0
+        wi = np.zeros(n, dtype=np.int64)
+        wp = np.zeros(n, dtype=np.float32)
+        while time.perf_counter() - t0 < args.cpu_budget:
+            x = np.ascontiguousarray(w.logits[done % B])
+            O.lib().nlo_top_tokens(x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), V, n, O.EXPF_LIBM,
+                                   wi.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                   wp.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+            done += 1
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": done / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+                               "sample": f"{done} rows on one thread for {dt:.1f} s; C restatement of "
+                                         "src/nimllm/sampler.nim:123-130 (softmaxInPlace, stable "
+                                         "merge sort; -O2 -ffp-contract=off, libm expf)"}
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -100,12 +180,17 @@ def main():
     ap.add_argument("--copy-ref", action="store_true",
                     help="also run a plain 256 MiB device copy three times (the reference "
                          "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes)")
+    ap.add_argument("--top-tokens", action="store_true",
+                    help="time topTokens (n = --top-n per row) on the workload's logits instead")
+    ap.add_argument("--top-n", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (rows shard across GPUs with no "
               "collective; see DESIGN.md); --gpus must be 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.top_tokens:
+        return bench_top_tokens(args)
     import numpy as np
     import torch
 

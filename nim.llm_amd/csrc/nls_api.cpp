@@ -703,7 +703,8 @@ int nls_set_rng_state(nls_sampler* s, int32_t row, uint64_t a0, uint64_t a1) {
 
 int nls_top_tokens(const float* d_logits, int32_t rows, int64_t vocab, int32_t n, int32_t* d_ids,
                    float* d_probs, void* stream) {
-  if (rows < 0 || vocab < 0 || vocab > INT32_MAX) return NLS_ERR_INVALID_ARGUMENT;
+  // (the kernel addresses a row in bytes with 32-bit offsets)
+  if (rows < 0 || vocab < 0 || vocab >= (int64_t{1} << 29)) return NLS_ERR_INVALID_ARGUMENT;
   const int64_t m = std::min<int64_t>(n, vocab);  // topTokens returns min(n, len) entries (:130)
   if (rows == 0 || m <= 0) return NLS_OK;
   if (m > nls::kTopMaxN || !d_logits || !d_ids || !d_probs) return NLS_ERR_INVALID_ARGUMENT;

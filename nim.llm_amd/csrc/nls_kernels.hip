@@ -1863,12 +1863,17 @@ __global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
 // the row is read a few times and only the n results are written.
 //   * The sum runs in index order, one add at a time, in lane 0 of wave 0,
 //     while the other waves compute the next chunk's exponentials into LDS.
-//   * The n-th largest probability T comes from an exact radix select on the
-//     probabilities' keys.  Among the entries equal to T the stable sort keeps
-//     the lowest indices, found by a second select on the index.  (Equal
-//     probabilities can come from different logits: the exp and the division
-//     round, so the order cannot be taken from the logits.)
-//   * The members are sorted by (probability desc, index asc) in LDS.
+//   * The n-th largest logit L comes from an exact radix select on the logits'
+//     keys; the entries whose probability reaches p(L) are those with a logit
+//     at or above the lowest float whose probability equals p(L) (a bisection
+//     on the float's bits).  They are few: gathered with their probabilities,
+//     sorted by (probability desc, index asc) in LDS, the first n kept.
+//     (Equal probabilities can come from different logits: the exp and the
+//     division round, so the order cannot be taken from the logits.)
+//   * Rows where that set is large (or s is NaN) select on the probabilities
+//     themselves: an exact radix select of the n-th largest probability T, and
+//     among the entries equal to T the lowest indices (a second select on the
+//     index), as the stable sort keeps them.
 // A row holding NaN, or +inf with anything else, has NaN probabilities; the
 // reference's comparator is no order on NaN, so such rows are outside the
 // parity claim (this kernel then returns the first indices).
@@ -1890,13 +1895,34 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
   const int lane = lane_id();
   const int wv = tid >> 6;
   const float* __restrict__ x = logits + (int64_t)row * V;
+  const __amdgpu_buffer_rsrc_t xr = slice_rsrc(x, (int)V);  // V < 2^29 (checked by the host)
   const int m = (int)min((int64_t)n, V);  // 1 <= m <= kTopMaxN (checked by the host)
   for (int q = tid; q < kSelWords; q += NT) hist[q] = 0u;
+  // fn(i, l, in) over the row, eight requests per thread in flight at a time
+  // (past the row they read 0 with in == false); every lane makes the same
+  // number of calls
+  constexpr int kScanU = 8;
+  auto row_scan = [&](auto fn) __attribute__((always_inline)) {
+    for (int i0 = 0; i0 < (int)V; i0 += NT * kScanU) {
+      float l[kScanU];
+#pragma unroll
+      for (int u = 0; u < kScanU; ++u) {
+        const int i = i0 + u * NT + tid;
+        l[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             xr, i < (int)V ? i * 4 : 0x7ffffff0, 0, 0));
+      }
+#pragma unroll
+      for (int u = 0; u < kScanU; ++u) {
+        const int i = i0 + u * NT + tid;
+        fn(i, l[u], i < (int)V);
+      }
+    }
+  };
 
   // (1) mx (:53): nim's max(mx, v) takes v when mx <= v, so NaN is never
   // taken; the float maximum of the rest (its sign of zero changes no l - mx)
   float mx = -__builtin_inff();
-  for (int64_t i = tid; i < V; i += NT) mx = __builtin_fmaxf(mx, x[i]);
+  row_scan([&](int, float l, bool in) { mx = in ? __builtin_fmaxf(mx, l) : mx; });
   for (int o = kWave / 2; o > 0; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o));
   if (lane == 0) s_part[wv] = mx;
   __syncthreads();
@@ -1909,28 +1935,57 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
   float s = 0.0f;
   for (int64_t c = 0; c <= nch; ++c) {
     if (wv != 0 && c < nch) {
-      const int64_t c0 = c * kTopChunk;
+      // every producer thread's loads go out together (past the row they read 0)
+      constexpr int PP = (kTopChunk + NT - kWave - 1) / (NT - kWave);
+      const int c0 = (int)(c * kTopChunk);
       float* eb = ebuf[c & 1];
-      for (int j = tid - kWave; j < kTopChunk; j += NT - kWave) {
-        const int64_t i = c0 + j;
-        eb[j] = i < V ? expf_cr(x[i] - mx) : 0.0f;
+      float lv[PP];
+#pragma unroll
+      for (int q = 0; q < PP; ++q) {
+        const int j = tid - kWave + q * (NT - kWave);
+        lv[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              xr, j < kTopChunk ? (c0 + j) * 4 : 0x7ffffff0, 0, 0));
+      }
+#pragma unroll
+      for (int q = 0; q < PP; ++q) {
+        const int j = tid - kWave + q * (NT - kWave);
+        if (j < kTopChunk) eb[j] = c0 + j < V ? expf_cr(lv[q] - mx) : 0.0f;
       }
     }
     if (wv == 0 && c > 0 && lane == 0) {
-      const int64_t c0 = (c - 1) * kTopChunk;
-      const int cnt = (int)min((int64_t)kTopChunk, V - c0);
-      const float* eb = ebuf[(c - 1) & 1];
-      const f32x4* e4 = reinterpret_cast<const f32x4*>(eb);
-      int j = 0;
-#pragma unroll 2
-      for (; j + 16 <= cnt; j += 16) {
-        const f32x4 a = e4[j / 4], b = e4[j / 4 + 1], cc = e4[j / 4 + 2], d = e4[j / 4 + 3];
-        s = s + a.x; s = s + a.y; s = s + a.z; s = s + a.w;
-        s = s + b.x; s = s + b.y; s = s + b.z; s = s + b.w;
-        s = s + cc.x; s = s + cc.y; s = s + cc.z; s = s + cc.w;
-        s = s + d.x; s = s + d.y; s = s + d.z; s = s + d.w;
+      // the whole chunk: entries past the row are +0, which leave s unchanged
+      const f32x4* e4 = reinterpret_cast<const f32x4*>(ebuf[(c - 1) & 1]);
+      // blocks of 16; the reads of the block two ahead are issued before the
+      // adds of the current one (the barrier keeps the compiler from sinking
+      // them), so the adds never wait for the LDS
+      constexpr int nb = kTopChunk / 16;
+      constexpr int kLast = nb - 1;
+      f32x4 a[4], b[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        a[q] = e4[q];
+        b[q] = e4[4 + q];
       }
-      for (; j < cnt; ++j) s = s + eb[j];
+#pragma unroll 8
+      for (int blk = 0; blk < nb; ++blk) {
+        const int nx = min(blk + 2, kLast) * 4;
+        f32x4 t[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t[q] = e4[nx + q];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          s = s + a[q].x;
+          s = s + a[q].y;
+          s = s + a[q].z;
+          s = s + a[q].w;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          a[q] = b[q];
+          b[q] = t[q];
+        }
+      }
     }
     __syncthreads();
   }
@@ -1938,18 +1993,68 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
   __syncthreads();
   s = s_sum;
   // probs[i] /= s (:57)
-  auto pkey = [&](int64_t i) -> uint32_t { return f2key(expf_cr(x[i] - mx) / s); };
+  auto pkey = [&](float l) -> uint32_t { return f2key(expf_cr(l - mx) / s); };
 
-  // (3) the m-th largest probability key T
+  uint64_t* mem = reinterpret_cast<uint64_t*>(&ebuf[0][0]);
+  constexpr int kCand = (int)(sizeof(ebuf) / sizeof(uint64_t));
+  auto emit = [&](int cnt) {  // mem[0..cnt): key << 32 | ~index; the first m, sorted, out
+    const int np = next_pow2(cnt);
+    for (int i = cnt + tid; i < np; i += NT) mem[i] = 0ull;  // below every real key
+    __syncthreads();
+    bitonic_sort_u64<NT>(mem, np, true);
+    __syncthreads();
+    for (int j = tid; j < m; j += NT) {
+      const uint64_t e = mem[j];
+      ids[(int64_t)row * n + j] = (int32_t)(0xffffffffu - (uint32_t)e);
+      probs[(int64_t)row * n + j] = key2f((uint32_t)(e >> 32));
+    }
+  };
+  // (3) The probability is non-decreasing in the logit (l - mx, the exp and
+  // the division by s each are), so the m-th largest probability is p(L) of
+  // the m-th largest logit L, and the entries whose probability reaches it are
+  // exactly those whose logit is at least l_lo, the lowest float with
+  // p(l_lo) == p(L).  With s a number (no NaN or +inf in the row) those few
+  // are gathered with their probabilities and sorted.  Rows where they are
+  // many fall through to the selection on the probabilities below.
+  auto prob_of = [&](float l) -> float { return expf_cr(l - mx) / s; };
+  if (s == s) {  // uniform
+    const SelectResult sl = block_select<NT>(
+        [&](auto fn) { row_scan([&](int, float l, bool in) { fn(in ? f2key(l) : 0u, in); }); }, m, -1,
+        hist, smem);
+    if (tid == 0) {
+      // the lowest key in [key(-inf), key(L)] whose probability reaches p(L)
+      const float pm = prob_of(key2f(sl.tau));
+      uint32_t lo = f2key(-__builtin_inff()), hi = sl.tau;
+      while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (prob_of(key2f(mid)) >= pm)
+          hi = mid;
+        else
+          lo = mid + 1;
+      }
+      smem[NW] = (int)hi;
+      s_cnt = 0;
+    }
+    __syncthreads();
+    const uint32_t klo = (uint32_t)smem[NW];
+    row_scan([&](int i, float l, bool in) {
+      if (in && f2key(l) >= klo) {
+        const int slot = atomicAdd(&s_cnt, 1);
+        if (slot < kCand) mem[slot] = ((uint64_t)f2key(prob_of(l)) << 32) | (0xffffffffu - (uint32_t)i);
+      }
+    });
+    __syncthreads();
+    const int nc = s_cnt;
+    if (nc <= kCand) {  // uniform
+      emit(nc);
+      return;
+    }
+    __syncthreads();
+  }
+  // (3') the m-th largest probability key T
   const SelectResult sr = block_select<NT>(
-      [&](auto fn) {
-        for (int64_t i0 = 0; i0 < V; i0 += NT) {
-          const int64_t i = i0 + tid;
-          const bool in = i < V;
-          fn(in ? pkey(i) : 0u, in);
-        }
-      },
-      m, -1, hist, smem);
+      [&](auto fn) { row_scan([&](int, float l, bool in) { fn(in ? pkey(l) : 0u, in); }); }, m, -1,
+      hist, smem);
   const uint32_t T = sr.tau;
   // (4) ties at T: the stable sort keeps the lowest indices; the (m - gt)-th
   // lowest index among them is the last one kept
@@ -1958,38 +2063,26 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
     __syncthreads();
     const SelectResult st = block_select<NT>(
         [&](auto fn) {
-          for (int64_t i0 = 0; i0 < V; i0 += NT) {
-            const int64_t i = i0 + tid;
-            const bool in = i < V && pkey(i) == T;
-            fn(in ? 0xffffffffu - (uint32_t)i : 0u, in);
-          }
+          row_scan([&](int i, float l, bool in) {
+            const bool tie = in && pkey(l) == T;
+            fn(tie ? 0xffffffffu - (uint32_t)i : 0u, tie);
+          });
         },
         m - sr.gt, -1, hist, smem);
     imax = 0xffffffffu - st.tau;
   }
   // (5) the members, sorted by (key desc, index asc): key << 32 | ~index
-  uint64_t* mem = reinterpret_cast<uint64_t*>(&ebuf[0][0]);
   if (tid == 0) s_cnt = 0;
   __syncthreads();
-  for (int64_t i = tid; i < V; i += NT) {
-    const uint32_t k = pkey(i);
-    if (k > T || (k == T && (uint32_t)i <= imax)) {
+  row_scan([&](int i, float l, bool in) {
+    const uint32_t k = pkey(l);
+    if (in && (k > T || (k == T && (uint32_t)i <= imax))) {
       const int slot = atomicAdd(&s_cnt, 1);
       if (slot < kTopMaxN) mem[slot] = ((uint64_t)k << 32) | (0xffffffffu - (uint32_t)i);
     }
-  }
+  });
   __syncthreads();
-  const int got = min(s_cnt, kTopMaxN);  // == m
-  const int mp = next_pow2(m);
-  for (int i = got + tid; i < mp; i += NT) mem[i] = 0ull;  // below every real key
-  __syncthreads();
-  bitonic_sort_u64<NT>(mem, mp, true);
-  __syncthreads();
-  for (int j = tid; j < m; j += NT) {
-    const uint64_t e = mem[j];
-    ids[(int64_t)row * n + j] = (int32_t)(0xffffffffu - (uint32_t)e);
-    probs[(int64_t)row * n + j] = key2f((uint32_t)(e >> 32));
-  }
+  emit(min(s_cnt, kTopMaxN));  // == m
 }
 
 // ---------------------------------------------------------------------------
