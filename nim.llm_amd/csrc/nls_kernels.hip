@@ -98,6 +98,43 @@ struct TailOut {
   float total;
 };
 
+// Wave-level fp32 chain over x[0..cnt) in index order, 64 values per step:
+// acc = acc OP x[b0] OP x[b0 + 1] ... as an unrolled sequence of adds (or
+// subtractions) with the lane index a constant, each lane keeping the running
+// value after its own element.  Past cnt the values read +0, which leave acc
+// unchanged.  stop(lane_value, i) is asked of every lane after each block; the
+// walk ends at the first block where some lane < the block's end says yes and
+// returns that lane's index (cnt if none).  Blocks are fetched 8 ahead so
+// that a walk over global scratch does not wait a round trip per block.
+template <bool SUB, typename XPtr, typename Stop>
+__device__ __forceinline__ int chain_walk(XPtr x, int cnt, float& acc, Stop stop) {
+  constexpr int PF = 8;
+  const int lane = lane_id();
+  for (int base = 0; base < cnt; base += kWave * PF) {
+    float xs[PF];
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int i = base + u * kWave + lane;
+      xs[u] = x[min(i, cnt - 1)];
+      xs[u] = i < cnt ? xs[u] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int b0 = base + u * kWave;
+      if (b0 >= cnt) break;
+      float mine = 0.0f;
+#pragma unroll
+      for (int l = 0; l < kWave; ++l) {
+        acc = SUB ? acc - lane_f(xs[u], l) : acc + lane_f(xs[u], l);
+        if (lane == l) mine = acc;
+      }
+      const uint64_t hit = __ballot(b0 + lane < cnt && stop(mine, b0 + lane));
+      if (hit) return b0 + __ffsll((unsigned long long)hit) - 1;
+    }
+  }
+  return cnt;
+}
+
 template <int NT, typename VPtr, typename IPtr, typename EPtr>
 __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr e, int ncand, const RowParams& P,
                                        double u, int* smem) {
@@ -112,11 +149,7 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
   if (threadIdx.x < kWave) {
     // s = sum of e in order
     float s = 0.0f;
-    for (int base = 0; base < ncand; base += kWave) {
-      const float x = (base + lane < ncand) ? e[base + lane] : 0.0f;
-      const int lim = min(kWave, ncand - base);
-      for (int l = 0; l < lim; ++l) s += lane_f(x, l);
-    }
+    chain_walk<false>(e, ncand, s, [](float, int) { return false; });
     if (lane == 0) s_sum = s;
   }
   __syncthreads();
@@ -126,48 +159,30 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
   if (threadIdx.x < kWave) {
     int n = ncand;
     if (P.topp_active) {
+      // the first i with (double)(e_0 + ... + e_i) >= topP
       float cum = 0.0f;
-      bool done = false;
-      for (int base = 0; base < ncand && !done; base += kWave) {
-        const float x = (base + lane < ncand) ? e[base + lane] : 0.0f;
-        const int lim = min(kWave, ncand - base);
-        for (int l = 0; l < lim; ++l) {
-          cum += lane_f(x, l);
-          if ((double)cum >= P.topP) {
-            n = base + l + 1;
-            done = true;
-            break;
-          }
-        }
-      }
+      const int stop = chain_walk<false>(e, ncand, cum, [&](float c, int) { return (double)c >= P.topP; });
+      if (stop < ncand) n = stop + 1;
     }
     if (P.minp_active) {
+      // m = the first index >= 1 whose probability is below thr (n if none)
       const float thr = e[0] * P.minP32;
-      int m = 1;
-      while (m < n && e[m] >= thr) ++m;
-      n = m;
-    }
-    float total = 0.0f;
-    for (int base = 0; base < n; base += kWave) {
-      const float x = (base + lane < n) ? e[base + lane] : 0.0f;
-      const int lim = min(kWave, n - base);
-      for (int l = 0; l < lim; ++l) total += lane_f(x, l);
-    }
-    float r = (float)u * total;
-    int pos = n - 1;
-    bool found = false;
-    for (int base = 0; base < n && !found; base += kWave) {
-      const float x = (base + lane < n) ? e[base + lane] : 0.0f;
-      const int lim = min(kWave, n - base);
-      for (int l = 0; l < lim; ++l) {
-        r = r - lane_f(x, l);
-        if (r <= 0.0f) {
-          pos = base + l;
-          found = true;
+      int m = n;
+      for (int base = 1; base < n; base += kWave) {
+        const int i = base + lane;
+        const uint64_t fail = __ballot(i < n && !(e[min(i, n - 1)] >= thr));
+        if (fail) {
+          m = base + __ffsll((unsigned long long)fail) - 1;
           break;
         }
       }
+      n = m;
     }
+    float total = 0.0f;
+    chain_walk<false>(e, n, total, [](float, int) { return false; });
+    float r = (float)u * total;
+    const int hit = chain_walk<true>(e, n, r, [](float rr, int) { return rr <= 0.0f; });
+    const int pos = hit < n ? hit : n - 1;
     if (lane == 0) {
       s_n = n;
       s_total = total;
