@@ -425,6 +425,7 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   // Without full-sort rows the whole-row kernel only serves the rare row the
   // streaming kernel hands on: one workgroup keeps that launch cheap.
   s->plan.gen_blocks = any_full ? std::min(B, 256) : 1;
+  s->plan.gen_lds = group_lds_bytes(vocab);
   // ... and then its last workgroup serves that row itself, saving a launch
   s->gen_inline = any_full ? 0 : 1;
 
@@ -642,6 +643,7 @@ int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t
   ga.rng = s->rng;
   ga.out = d_out;
   ga.dbg = dp;
+  ga.grouped = s->plan.gen_lds > 0 ? 1 : 0;
   a.gen_inline = s->gen_inline;
   a.done = s->done;
   a.ga = ga;

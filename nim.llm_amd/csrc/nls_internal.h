@@ -71,6 +71,21 @@ struct DebugPtrs {
   int32_t cap;
 };
 
+// Grouped sort path of the whole-row kernel (full-sort rows replayed over
+// their distinct values): LDS for the row's patch table, a hash table of the
+// distinct values and their sorted list.  Rows that need more take the
+// whole-row sort.
+constexpr int kGrpPatchCap = 2048;   // distinct patched ids (history window + bias)
+constexpr int kGrpHashBits = 12;
+constexpr int kGrpHashCap = 1 << kGrpHashBits;
+constexpr int kGrpHashLimit = 3072;  // distinct values kept (load factor 3/4)
+constexpr int64_t kGrpMaxV = 180224; // vocabularies whose bitmap fits beside the rest
+inline size_t group_lds_bytes(int64_t V) {
+  if (V < 1 || V > kGrpMaxV) return 0;
+  const size_t nw = (size_t)((V + 31) / 32);
+  return nw * 8 + (size_t)kGrpPatchCap * 16 + (size_t)kGrpHashCap * 16;
+}
+
 struct GenericArgs {
   const float* logits;
   int64_t V;
@@ -89,6 +104,7 @@ struct GenericArgs {
   uint64_t* rng;
   int32_t* out;
   DebugPtrs dbg;
+  int grouped;  // 1: the launch carries group_lds_bytes(V) of dynamic LDS
 };
 
 struct StreamArgs {
@@ -139,6 +155,7 @@ struct LaunchPlan {
   bool vec4;     // 16-byte loads (V % 4 == 0 and aligned logits)
   size_t lds;    // dynamic LDS bytes of the streaming kernel
   int gen_blocks;
+  size_t gen_lds;  // dynamic LDS bytes of the whole-row kernel (grouped path), 0 = none
 };
 
 hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const LaunchPlan& lp,

@@ -21,6 +21,7 @@
 #include <stdint.h>
 
 #include "nls_expf.h"
+#include "nls_grouped.h"
 #include "nls_internal.h"
 #include "nls_primitives.h"
 
@@ -411,10 +412,11 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
   }
 }
 
-template <int NT>
+template <int NT, bool GROUPED = false>
 __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int nw, int count, uint32_t* wcnt,
                                              uint32_t* dbase, uint32_t* drun, int* smem, double* s_u_p,
-                                             int* s_i, float* s_rv, int* s_ri);
+                                             int* s_i, float* s_rv, int* s_ri,
+                                             unsigned char* glds = nullptr);
 
 // ---------------------------------------------------------------------------
 // 1. stream_kernel
@@ -1683,13 +1685,389 @@ __device__ __forceinline__ int upper_bound_u32(const uint32_t* a, int n, uint32_
 }
 
 
+// ---------------------------------------------------------------------------
+// Grouped sort path: a full-sort row (sampler.nim:96-121) without the sort.
+// The row's final values (penalties, bias and temperature applied, :64-81)
+// are counted per distinct value in an LDS hash table, for every value whose
+// exp(v - mx) can still move the softmax sum (fl(v - mx) >= kGroupFloor).
+// The distinct values are sorted, and the reference's sequential fp32 chains
+// -- softmax sum, top-p, total, draw -- run over them with each value's
+// multiplicity (nls_grouped.h).  The drawn candidate is the t-th lowest index
+// among the members of its value, as the stable sort orders equal values.
+// Rows that need more (patched ids, distinct values or candidates past the
+// table) report failure and take the whole-row sort.
+// ---------------------------------------------------------------------------
+struct GroupLds {
+  uint32_t* bitmap;  // [nw] patched ids of the row
+  uint32_t* wpre;    // [nw] patched ids before each bitmap word
+  int32_t* pid;      // [kGrpPatchCap] patched ids, in index order
+  uint32_t* pcnt;    //   their window counts
+  int32_t* pbias;    //   their bias entries (-1: none)
+  float* pfin;       //   their final values
+  uint32_t* hkey;    // [kGrpHashCap] f2key of a distinct value (kGrpEmpty: free)
+  uint32_t* hcnt;    //   its multiplicity
+  uint64_t* gsort;   // [kGrpHashCap] (~f2key(value) << 32) | multiplicity, ascending
+};
+constexpr uint32_t kGrpEmpty = 0xffffffffu;  // f2key of a NaN, which never enters
+
+__device__ __forceinline__ GroupLds group_lds(unsigned char* base, int nw) {
+  GroupLds L;
+  L.bitmap = reinterpret_cast<uint32_t*>(base);
+  L.wpre = L.bitmap + nw;
+  L.pid = reinterpret_cast<int32_t*>(L.wpre + nw);
+  L.pcnt = reinterpret_cast<uint32_t*>(L.pid + kGrpPatchCap);
+  L.pbias = reinterpret_cast<int32_t*>(L.pcnt + kGrpPatchCap);
+  L.pfin = reinterpret_cast<float*>(L.pbias + kGrpPatchCap);
+  L.hkey = reinterpret_cast<uint32_t*>(L.pfin + kGrpPatchCap);
+  L.hcnt = L.hkey + kGrpHashCap;
+  L.gsort = reinterpret_cast<uint64_t*>(L.hcnt + kGrpHashCap);  // byte offset 8*nw + 16*caps
+  return L;
+}
+
+// Count one more occurrence of key; false when the table is full.
+__device__ __forceinline__ bool group_insert(const GroupLds& L, uint32_t key, int* distinct) {
+  uint32_t h = (key * 0x9E3779B1u) >> (32 - kGrpHashBits);
+  for (int probe = 0; probe < kGrpHashCap; ++probe) {
+    uint32_t cur = L.hkey[h];
+    if (cur == kGrpEmpty) {
+      cur = atomicCAS(&L.hkey[h], kGrpEmpty, key);
+      if (cur == kGrpEmpty) {
+        cur = key;
+        if (atomicAdd(distinct, 1) >= kGrpHashLimit) return false;
+      }
+    }
+    if (cur == key) {
+      atomicAdd(&L.hcnt[h], 1u);
+      return true;
+    }
+    h = (h + 1) & (kGrpHashCap - 1);
+  }
+  return false;
+}
+
+struct GroupOut {
+  int ok;
+  int id;
+  int n;
+  float total;
+};
+
+template <int NT>
+__device__ GroupOut grouped_row(const GenericArgs& a, int row, const RowParams& P, double u,
+                                const GroupLds& L, int* smem) {
+  constexpr int NW = NT / kWave;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int V = (int)a.V;
+  const int nw = (V + 31) >> 5;
+  const float* __restrict__ src = a.logits + (int64_t)row * a.V;
+  __shared__ int s_fail, s_distinct, s_G, s_id;
+  __shared__ unsigned long long s_held;
+  __shared__ uint32_t s_wmax[NW];
+  __shared__ int s_wnan[NW];
+  __shared__ float s_sum;
+  __shared__ GroupDraw s_draw;
+  __shared__ int s_g;
+  __shared__ int64_t s_t;
+  GroupOut res;
+  res.ok = 0;
+  res.id = 0;
+  res.n = 0;
+  res.total = 0.0f;
+
+  for (int i = tid; i < nw; i += NT) L.bitmap[i] = 0u;
+  for (int i = tid; i < kGrpHashCap; i += NT) {
+    L.hkey[i] = kGrpEmpty;
+    L.hcnt[i] = 0u;
+  }
+  for (int i = tid; i < kGrpPatchCap; i += NT) {
+    L.pcnt[i] = 0u;
+    L.pbias[i] = -1;
+  }
+  if (tid == 0) {
+    s_fail = 0;
+    s_distinct = 0;
+    s_G = 0;
+    s_id = -1;
+    s_held = 0ull;
+  }
+  __syncthreads();
+  // ---- patch table: the window's ids (:64-70) and the bias ids (:75-76) ----
+  const int64_t hlen = a.hist_len[row];
+  int n_hist = 0;
+  if (P.pen_active && hlen > 0)
+    n_hist = (int)((P.repeat_last_n > 0 && P.repeat_last_n < hlen) ? P.repeat_last_n : hlen);
+  const int32_t* __restrict__ hrow = a.hist + (int64_t)row * a.hcap;
+  const int hbase = n_hist > 0 ? (int)((hlen - n_hist) % a.hcap) : 0;
+  auto hist_id = [&](int i) {
+    int slot = hbase + i;
+    if (slot >= a.hcap) slot -= a.hcap;
+    return hrow[slot];
+  };
+  for (int i = tid; i < n_hist; i += NT) {
+    const int id = hist_id(i);
+    if (id >= 0 && id < V) atomicOr(&L.bitmap[id >> 5], 1u << (id & 31));
+  }
+  for (int j = tid; j < P.bias_cnt; j += NT) {
+    const int id = a.bias_ids[P.bias_off + j];
+    if (id >= 0 && id < V) atomicOr(&L.bitmap[id >> 5], 1u << (id & 31));
+  }
+  __syncthreads();
+  const int per = (nw + NT - 1) / NT;
+  const int wlo = tid * per;
+  int pc = 0;
+  for (int q = 0; q < per; ++q)
+    if (wlo + q < nw) pc += __popc(L.bitmap[wlo + q]);
+  int np;
+  int run = block_excl_scan<NT>(pc, smem, np);
+  if (np > kGrpPatchCap) return res;  // np is the same in every thread
+  for (int q = 0; q < per; ++q)
+    if (wlo + q < nw) {
+      L.wpre[wlo + q] = (uint32_t)run;
+      run += __popc(L.bitmap[wlo + q]);
+    }
+  __syncthreads();
+  auto slot_of = [&](int id) {
+    const int ww = id >> 5;
+    return (int)L.wpre[ww] + __popc(L.bitmap[ww] & ((1u << (id & 31)) - 1u));
+  };
+  for (int i = tid; i < n_hist; i += NT) {
+    const int id = hist_id(i);
+    if (id >= 0 && id < V) {
+      const int sl = slot_of(id);
+      atomicAdd(&L.pcnt[sl], 1u);
+      L.pid[sl] = id;
+    }
+  }
+  for (int j = tid; j < P.bias_cnt; j += NT) {
+    const int id = a.bias_ids[P.bias_off + j];
+    if (id >= 0 && id < V) {
+      const int sl = slot_of(id);
+      L.pbias[sl] = j;
+      L.pid[sl] = id;
+    }
+  }
+  __syncthreads();
+  for (int sl = tid; sl < np; sl += NT) {
+    const int id = L.pid[sl];
+    float v = src[id];
+    const uint32_t c = L.pcnt[sl];
+    if (c) {
+      if (P.rp_active) v = (v > 0.0f) ? (v / P.rp32) : (v * P.rp32);
+      v = v - (float)((double)c * P.freq + P.pres);
+    }
+    if (L.pbias[sl] >= 0) v = v + a.bias_vals[P.bias_off + L.pbias[sl]];
+    L.pfin[sl] = v * P.invT;  // (:80-81)
+  }
+  __syncthreads();
+  // ---- the row maximum (:53) over the final values ----
+  const bool vec = (V % 4 == 0) && ((reinterpret_cast<uintptr_t>(src) & 15) == 0);
+  const float4* __restrict__ src4 = reinterpret_cast<const float4*>(src);
+  const float invT = P.invT;
+  // Visit every final value once: unpatched ones from the row, patched ones
+  // from the patch table.  f(v) gets the value; f returns false to stop early.
+  const int V4 = V >> 2;
+  auto for_each_final = [&](auto&& f) {
+    if (vec) {
+      // four 16-byte loads in flight per thread
+      for (int b4 = tid; b4 < V4; b4 += 4 * NT) {
+        float4 x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i4 = b4 + u * NT;
+          x[u] = src4[min(i4, V4 - 1)];
+        }
+        bool go = true;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i4 = b4 + u * NT;
+          if (i4 < V4) {
+            const uint32_t pb = (L.bitmap[i4 >> 3] >> ((i4 & 7) * 4)) & 15u;
+            if (!(pb & 1u)) go &= f(x[u].x * invT);
+            if (!(pb & 2u)) go &= f(x[u].y * invT);
+            if (!(pb & 4u)) go &= f(x[u].z * invT);
+            if (!(pb & 8u)) go &= f(x[u].w * invT);
+          }
+        }
+        if (!go) break;
+      }
+    } else {
+      for (int i = tid; i < V; i += NT) {
+        if ((L.bitmap[i >> 5] >> (i & 31)) & 1u) continue;
+        if (!f(src[i] * invT)) break;
+      }
+    }
+    for (int sl = tid; sl < np; sl += NT)
+      if (!f(L.pfin[sl])) break;
+  };
+  uint32_t kmax = 0u;
+  bool nan = false;
+  for_each_final([&](float v) {
+    nan |= (v != v);
+    kmax = max(kmax, f2key(v));
+    return true;
+  });
+  kmax = wave_max_u32(kmax);
+  const uint64_t nb = __ballot(nan);
+  if (lane == 0) {
+    s_wmax[tid >> 6] = kmax;
+    s_wnan[tid >> 6] = nb != 0ull;
+  }
+  __syncthreads();
+  uint32_t mk = 0u;
+  int anynan = 0;
+  for (int q = 0; q < NW; ++q) {
+    mk = max(mk, s_wmax[q]);
+    anynan |= s_wnan[q];
+  }
+  const float mx = key2f(mk);
+  if (anynan || !(mx > -__builtin_inff() && mx < __builtin_inff())) return res;
+  // ---- count every value that can move the sum ----
+  for_each_final([&](float v) {
+    if (v - mx >= kGroupFloor) {
+      if (!group_insert(L, f2key(v), &s_distinct)) {
+        s_fail = 1;
+        return false;
+      }
+    }
+    return true;
+  });
+  __syncthreads();
+  if (s_fail) return res;
+  for (int h = tid; h < kGrpHashCap; h += NT) {
+    const uint32_t k = L.hkey[h];
+    if (k != kGrpEmpty) {
+      const int at = atomicAdd(&s_G, 1);
+      L.gsort[at] = ((uint64_t)(~k) << 32) | (uint64_t)L.hcnt[h];
+    }
+  }
+  __syncthreads();
+  const int G = s_G;
+  const int Gp = next_pow2(G > 0 ? G : 1);
+  for (int i = G + tid; i < Gp; i += NT) L.gsort[i] = ~0ull;
+  __syncthreads();
+  bitonic_sort_u64<NT>(L.gsort, Gp, false);  // descending value
+  // per group: its exponential (:56) and multiplicity (hash arrays reused)
+  float* ge = reinterpret_cast<float*>(L.hkey);
+  uint32_t* gc = L.hcnt;
+  for (int g = tid; g < G; g += NT) {
+    const uint64_t e = L.gsort[g];
+    const float v = key2f(~(uint32_t)(e >> 32));
+    gc[g] = (uint32_t)e;
+    ge[g] = expf_cr(v - mx);
+    atomicAdd(&s_held, (unsigned long long)(uint32_t)e);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float s = 0.0f;
+    if (!group_sum(ge, gc, G, s)) s_fail = 1;
+    s_sum = s;
+  }
+  __syncthreads();
+  if (s_fail) return res;
+  const float s = s_sum;
+  for (int g = tid; g < G; g += NT) ge[g] = ge[g] / s;  // (:57)
+  __syncthreads();
+  if (tid == 0) {
+    s_draw = group_cut_draw(ge, gc, G, s_held == (unsigned long long)V, a.V, P.topp_active != 0, P.topP,
+                            P.minp_active != 0, P.minP32, u);
+    int64_t pos = s_draw.pos;
+    int g = 0;
+    if (s_draw.status == kGroupOk)
+      while (g < G - 1 && pos >= (int64_t)gc[g]) pos -= gc[g++];
+    s_g = g;
+    s_t = pos;
+  }
+  __syncthreads();
+  if (s_draw.status != kGroupOk) return res;
+  // ---- the drawn candidate: the t-th lowest index holding value vg ----
+  // Blocks of 64 lanes x W values (W = 4 with 16-byte loads): each wave
+  // counts the members of its blocks (counts kept in the patch table's
+  // count/bias arrays, free by now), then wave 0 finds the block holding the
+  // t-th member and the lane and element inside it.
+  const float vg = key2f(~(uint32_t)(L.gsort[s_g] >> 32));
+  const int64_t t = s_t;
+  const int wv = tid >> 6;
+  uint32_t* bcnt = L.pcnt;  // pcnt and pbias are adjacent: 2 * kGrpPatchCap entries
+  auto final_at = [&](int i, float x) -> float {
+    const uint32_t wb = L.bitmap[i >> 5];
+    if ((wb >> (i & 31)) & 1u) return L.pfin[slot_of(i)];
+    return x * invT;
+  };
+  // members among this lane's W values of block bk (bit j: value j)
+  auto lane_members = [&](int bk) -> uint32_t {
+    uint32_t m = 0u;
+    if (vec) {
+      const int i4 = bk * kWave + lane;
+      if (i4 < V4) {
+        const float4 x = src4[i4];
+        const int i = i4 * 4;
+        m |= (final_at(i, x.x) == vg) ? 1u : 0u;
+        m |= (final_at(i + 1, x.y) == vg) ? 2u : 0u;
+        m |= (final_at(i + 2, x.z) == vg) ? 4u : 0u;
+        m |= (final_at(i + 3, x.w) == vg) ? 8u : 0u;
+      }
+    } else {
+      const int i = bk * kWave + lane;
+      if (i < V) m = (final_at(i, src[i]) == vg) ? 1u : 0u;
+    }
+    return m;
+  };
+  const int W = vec ? 4 : 1;
+  const int nblk = (V + kWave * W - 1) / (kWave * W);  // <= 2 * kGrpPatchCap for V <= kGrpMaxV
+  for (int b0 = wv; b0 < nblk; b0 += 4 * NW) {
+    uint32_t m[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) m[u] = (b0 + u * NW < nblk) ? lane_members(b0 + u * NW) : 0u;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = wave_sum_i(__popc(m[u]));
+      if (lane == 0 && b0 + u * NW < nblk) bcnt[b0 + u * NW] = (uint32_t)c;
+    }
+  }
+  __syncthreads();
+  if (wv == 0) {
+    int64_t left = t;
+    for (int base = 0; base < nblk; base += kWave) {
+      const int c = (base + lane < nblk) ? (int)bcnt[base + lane] : 0;
+      const int incl = wave_incl_scan(c);
+      const int sum = __shfl(incl, kWave - 1, kWave);
+      if (left < sum) {
+        // the block: the first lane whose inclusive count passes `left`
+        const uint64_t past = __ballot((int64_t)incl > left);
+        const int bl = __ffsll((unsigned long long)past) - 1;
+        const int bk = base + bl;
+        const int64_t within = left - (__shfl(incl, bl, kWave) - __shfl(c, bl, kWave));
+        const uint32_t m = lane_members(bk);
+        const int mc = __popc(m);
+        const int mi = wave_incl_scan(mc);
+        if ((int64_t)(mi - mc) <= within && within < (int64_t)mi) {
+          uint32_t mm = m;
+          for (int r = (int)(within - (mi - mc)); r > 0; --r) mm &= mm - 1u;
+          s_id = (bk * kWave + lane) * W + (__ffs(mm) - 1);
+        }
+        break;
+      }
+      left -= sum;
+    }
+  }
+  __syncthreads();
+  if (s_id < 0) return res;
+  res.ok = 1;
+  res.id = s_id;
+  res.n = (int)s_draw.n;
+  res.total = s_draw.total;
+  __syncthreads();
+  return res;
+}
+
 // Rows of the list from index w0 on, every nw-th: the whole-row path.  LDS
 // scratch is passed in (wcnt: NW * 256 words, dbase and drun: 256 each), so
 // that the streaming kernel's last workgroup can run it too.
-template <int NT>
+template <int NT, bool GROUPED>
 __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int nw, int count, uint32_t* wcnt,
                                              uint32_t* dbase, uint32_t* drun, int* smem, double* s_u_p,
-                                             int* s_i, float* s_rv, int* s_ri) {
+                                             int* s_i, float* s_rv, int* s_ri, unsigned char* glds) {
   constexpr int NW = NT / kWave;
   const int n = (int)a.V;
   const int tid = threadIdx.x;
@@ -1702,6 +2080,33 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
     const int row = load_agent(&a.generic_list[li]);
     const RowParams P = a.rp[row];
     const float* __restrict__ src = a.logits + (int64_t)row * a.V;
+    bool u_taken = false;
+    GroupOut gout;
+    gout.ok = 0;
+    if constexpr (GROUPED) {
+      if (P.mode == kModeFull && a.grouped) {
+        if (tid == 0) *s_u_p = row_uniform(a.d_u, a.rng, row);
+        __syncthreads();
+        u_taken = true;
+        gout = grouped_row<NT>(a, row, P, *s_u_p, group_lds(glds, (int)((a.V + 31) >> 5)), smem);
+        if (gout.ok) {
+          if (tid == 0) {
+            a.out[row] = gout.id;
+            if (a.dbg.n) a.dbg.n[row] = gout.n;
+            if (a.dbg.ncand) a.dbg.ncand[row] = n;
+            if (a.dbg.total) a.dbg.total[row] = gout.total;
+            if (a.dbg.path) a.dbg.path[row] = 3;
+          }
+          // candidate lists are asked for: the whole-row sort below writes
+          // them (its id, n and total are replaced by these afterwards)
+          if (!a.dbg.cand_ids && !a.dbg.cand_probs) {
+            __syncthreads();
+            continue;
+          }
+        }
+        __syncthreads();
+      }
+    }
     // window counts (kB) and bias slots + 1 (iB) per id (:64-76)
     for (int i = tid; i < n; i += NT) {
       kB[i] = 0u;
@@ -1776,7 +2181,7 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
     radix_sort_pass<NT>(kA, iA, kB, iB, n, 16, wcnt, dbase, drun);
     radix_sort_pass<NT>(kB, iB, kA, iA, n, 24, wcnt, dbase, drun);
     // kA: ~key ascending (value descending, index ascending on ties)
-    if (tid == 0) *s_u_p = row_uniform(a.d_u, a.rng, row);
+    if (tid == 0 && !u_taken) *s_u_p = row_uniform(a.d_u, a.rng, row);
     __syncthreads();
     if (P.mode == kModeFull) {
       // candidates = the whole sorted row (:96-97); values into work, ids stay in iA
@@ -1786,6 +2191,12 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
                                                 smem);
       if (tid == 0) a.out[row] = t.id;
       write_debug<NT>(a.dbg, row, 4, t.n, n, t.total, iA, reinterpret_cast<float*>(kB));
+      if (gout.ok && tid == 0) {
+        a.out[row] = gout.id;
+        if (a.dbg.n) a.dbg.n[row] = gout.n;
+        if (a.dbg.total) a.dbg.total[row] = gout.total;
+        if (a.dbg.path) a.dbg.path[row] = 3;
+      }
       __syncthreads();
       continue;
     }
@@ -1863,9 +2274,11 @@ __global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
   __shared__ int s_i[4];
   __shared__ float s_rv[NW];
   __shared__ int s_ri[NW];
+  extern __shared__ __align__(16) unsigned char glds[];  // group_lds_bytes(V) when a.grouped
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.next_count = 0;
   const int count = *a.generic_count;
-  generic_rows<NT>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri);
+  generic_rows<NT, true>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri,
+                         glds);
 }
 
 // ---------------------------------------------------------------------------
@@ -2170,7 +2583,7 @@ hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const Laun
   if (ev_stop && (e = hipEventRecord(ev_stop, s)) != hipSuccess) return e;
   if (!sa.gen_inline)
     hipLaunchKernelGGL(generic_kernel<kGenericThreads>, dim3(lp.gen_blocks), dim3(kGenericThreads),
-                       0, s, ga);
+                       ga.grouped ? lp.gen_lds : 0, s, ga);
   return hipGetLastError();
 }
 
@@ -2208,6 +2621,10 @@ static hipError_t set_attr_q() {
 
 hipError_t set_kernel_attributes() {
   hipError_t e;
+  if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(&generic_kernel<kGenericThreads>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)group_lds_bytes(kGrpMaxV))) != hipSuccess)
+    return e;
   if ((e = set_attr_q<256, true>()) != hipSuccess) return e;
   if ((e = set_attr_q<256, false>()) != hipSuccess) return e;
   if ((e = set_attr_q<1024, true>()) != hipSuccess) return e;

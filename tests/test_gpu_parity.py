@@ -251,6 +251,11 @@ def test_workload_parity(pkg, torch, name):
     say(f"[workload_parity] {name}: {len(rows)} rows bit-exact; libm-exp exception rows: {libm_exc}")
     paths = dbg["path"]
     say(f"[workload_parity] {name}: paths {np.bincount(paths, minlength=5).tolist()}")
+    # full-sort rows (k = 0) take the grouped sort path: their distinct values,
+    # patched ids and cutoffs all fit its tables on these workloads
+    full = np.array([r.temperature > 0 and not (0 < r.topK < w.V) for r in w.rows])
+    if full.any():
+        assert np.all(paths[full] == 3), (name, np.bincount(paths[full], minlength=5).tolist())
 
 
 def test_device_rng_stream_and_greedy_rows_draw_nothing(pkg, torch):
