@@ -99,16 +99,21 @@ struct TailOut {
   float total;
 };
 
-// Wave-level fp32 chain over x[0..cnt) in index order, 64 values per step:
-// acc = acc OP x[b0] OP x[b0 + 1] ... as an unrolled sequence of adds (or
-// subtractions) with the lane index a constant, each lane keeping the running
-// value after its own element.  Past cnt the values read +0, which leave acc
-// unchanged.  stop(lane_value, i) is asked of every lane after each block; the
-// walk ends at the first block where some lane < the block's end says yes and
-// returns that lane's index (cnt if none).  Blocks are fetched 8 ahead so
-// that a walk over global scratch does not wait a round trip per block.
-template <bool SUB, typename XPtr, typename Stop>
-__device__ __forceinline__ int chain_walk(XPtr x, int cnt, float& acc, Stop stop) {
+// Wave-level fp32 chain over x[0..cnt) in index order: acc = acc OP x[0] OP
+// x[1] ... as a sequence of dependent adds (or subtractions), exactly the
+// reference's sequential accumulation.  Past cnt the values read +0, which
+// leave acc unchanged.  stop(value, i) asks whether the chain ends after
+// element i with the running value `value`; the walk returns the first such
+// i (cnt if none) and, in *at, the running value there.  `stop` must be
+// monotone along the chain (once true it stays true, as for a running sum of
+// non-negative terms against a bound, or a difference of them against 0):
+// it is tested once per block of 64, and only the block where it first holds
+// (or where the value turns NaN) is walked again keeping every lane's value.
+// Lane l holds element b0 + l of a block and readlane broadcasts it, so a
+// step is one readlane and one operation; blocks are fetched 8 ahead so that
+// a walk over global scratch does not wait a round trip per block.
+template <bool SUB, bool HAS_STOP, typename XPtr, typename Stop>
+__device__ __forceinline__ int chain_walk(XPtr x, int cnt, float& acc, Stop stop, float* at = nullptr) {
   constexpr int PF = 8;
   const int lane = lane_id();
   for (int base = 0; base < cnt; base += kWave * PF) {
@@ -123,14 +128,23 @@ __device__ __forceinline__ int chain_walk(XPtr x, int cnt, float& acc, Stop stop
     for (int u = 0; u < PF; ++u) {
       const int b0 = base + u * kWave;
       if (b0 >= cnt) break;
-      float mine = 0.0f;
+      const float a0 = acc;
 #pragma unroll
-      for (int l = 0; l < kWave; ++l) {
-        acc = SUB ? acc - lane_f(xs[u], l) : acc + lane_f(xs[u], l);
-        if (lane == l) mine = acc;
+      for (int l = 0; l < kWave; ++l) acc = SUB ? acc - lane_f(xs[u], l) : acc + lane_f(xs[u], l);
+      if (HAS_STOP && (acc != acc || stop(acc, min(b0 + kWave, cnt) - 1))) {
+        float r = a0, mine = 0.0f;
+#pragma unroll
+        for (int l = 0; l < kWave; ++l) {
+          r = SUB ? r - lane_f(xs[u], l) : r + lane_f(xs[u], l);
+          if (lane == l) mine = r;
+        }
+        const uint64_t hit = __ballot(b0 + lane < cnt && stop(mine, b0 + lane));
+        if (hit) {
+          const int hl = __ffsll((unsigned long long)hit) - 1;
+          if (at) *at = lane_f(mine, hl);
+          return b0 + hl;
+        }
       }
-      const uint64_t hit = __ballot(b0 + lane < cnt && stop(mine, b0 + lane));
-      if (hit) return b0 + __ffsll((unsigned long long)hit) - 1;
     }
   }
   return cnt;
@@ -150,7 +164,7 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
   if (threadIdx.x < kWave) {
     // s = sum of e in order
     float s = 0.0f;
-    chain_walk<false>(e, ncand, s, [](float, int) { return false; });
+    chain_walk<false, false>(e, ncand, s, [](float, int) { return false; });
     if (lane == 0) s_sum = s;
   }
   __syncthreads();
@@ -159,12 +173,18 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
   __syncthreads();
   if (threadIdx.x < kWave) {
     int n = ncand;
+    // the top-p running sum is the same fp32 sequence as the total over its
+    // first n terms: when min-p keeps n, the total is the running sum there
+    float cum_n = 0.0f;
     if (P.topp_active) {
       // the first i with (double)(e_0 + ... + e_i) >= topP
-      float cum = 0.0f;
-      const int stop = chain_walk<false>(e, ncand, cum, [&](float c, int) { return (double)c >= P.topP; });
+      float cum = 0.0f, at = 0.0f;
+      const int stop =
+          chain_walk<false, true>(e, ncand, cum, [&](float c, int) { return (double)c >= P.topP; }, &at);
       if (stop < ncand) n = stop + 1;
+      cum_n = stop < ncand ? at : cum;
     }
+    const int n_topp = n;
     if (P.minp_active) {
       // m = the first index >= 1 whose probability is below thr (n if none)
       const float thr = e[0] * P.minP32;
@@ -180,9 +200,12 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
       n = m;
     }
     float total = 0.0f;
-    chain_walk<false>(e, n, total, [](float, int) { return false; });
+    if (P.topp_active && n == n_topp)
+      total = cum_n;
+    else
+      chain_walk<false, false>(e, n, total, [](float, int) { return false; });
     float r = (float)u * total;
-    const int hit = chain_walk<true>(e, n, r, [](float rr, int) { return rr <= 0.0f; });
+    const int hit = chain_walk<true, true>(e, n, r, [](float rr, int) { return rr <= 0.0f; });
     const int pos = hit < n ? hit : n - 1;
     if (lane == 0) {
       s_n = n;
@@ -749,6 +772,18 @@ void stream_kernel(const StreamArgs a) {
     int bi = 0x7fffffff;
     int buf_n = 0, cur = 0;
     uint32_t tau = 0u;
+    // Block path on a whole row: the first refresh (tile 0) takes the
+    // spec_rank-th largest key of the tile instead of the k-th, a rank that
+    // lets about 2k elements of the row through when the tile is typical of
+    // it, so that the buffer rarely fills again.  Such a threshold need not
+    // bound the k-th largest from below: the candidates are then checked to
+    // number at least k, and the row goes to the whole-row path otherwise.
+    int spec_rank = 0;
+    if (!WAVE && topk && a.S == 1 && len > UE) {
+      const int64_t r = (2LL * k * UE + len - 1) / len;
+      spec_rank = r < k ? (int)r : 0;
+    }
+    bool spec_used = false;
     // wave path (k <= 64): this wave's buffer count, threshold and overflow
     int wn = 0;
     uint32_t wtau = 0u;
@@ -1051,13 +1086,13 @@ void stream_kernel(const StreamArgs a) {
         // is a lower bound of the k-th largest of everything seen.  A coarse
         // digit prefix is enough while it admits few elements; otherwise refine
         // to the exact k-th largest of the tops.
-        auto tops_select = [&](int fit) -> uint32_t {
+        auto tops_select = [&](int rank, int fit) -> uint32_t {
           return block_select<NT>(
                      [&](auto fn) {
   #pragma unroll
                        for (int q = 0; q < Q; ++q) fn(tops[q], q < nv);
                      },
-                     k, fit, shist, smem)
+                     rank, fit, shist, smem)
               .tau;
         };
         auto count_ge = [&](uint32_t th) -> int {
@@ -1069,14 +1104,19 @@ void stream_kernel(const StreamArgs a) {
         };
         uint32_t t1 = tau;
         int cnt = buf_n + ttot;
-        if (tv >= k) {
-          t1 = tops_select(2 * k);
+        if (spec_rank > 0 && tv >= spec_rank) {
+          t1 = tops_select(spec_rank, -1);
+          cnt = count_ge(t1);
+          spec_used = true;
+        } else if (tv >= k) {
+          t1 = tops_select(k, 2 * k);
           cnt = count_ge(t1);
           if (cnt > a.ccap / 2) {
-            t1 = tops_select(-1);
+            t1 = tops_select(k, -1);
             cnt = count_ge(t1);
           }
         }
+        spec_rank = 0;
         if (cnt > a.ccap) {
           // only ties at t1, or values crowded into few threads, get here: the
           // whole-row kernel takes the row
@@ -1520,7 +1560,8 @@ void stream_kernel(const StreamArgs a) {
     }
     // ---- the row's heap-path members, then the reference's tail ----
     uint64_t* mem = reinterpret_cast<uint64_t*>(regA);
-    if (!topk_members<NT>(ent, N, k, mem, a.mcap, shist, smem, &s_cnt)) {
+    // (after a speculative threshold fewer than k elements may reach it)
+    if ((spec_used && N < k) || !topk_members<NT>(ent, N, k, mem, a.mcap, shist, smem, &s_cnt)) {
       if (tid == 0) push_generic(a.generic_list, a.generic_count, row);
       return;
     }

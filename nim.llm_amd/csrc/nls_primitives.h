@@ -339,8 +339,37 @@ __device__ __forceinline__ void topq_insert(uint32_t (&t)[Q], uint32_t key) {
 // In-place bitonic sort of n (power of two) 64-bit keys, ascending.
 template <int NT, typename Ptr>
 __device__ __forceinline__ void bitonic_sort_u64(Ptr a, int n, bool descending) {
-  for (int k = 2; k <= n; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
+  // Bitonic network over a[0..n), n a power of two.  The stages whose
+  // partners lie less than 64 apart stay inside a 64-element block: a wave
+  // loads its blocks into registers (one element per lane) and runs each
+  // such run of stages through lane shuffles, with one barrier after the
+  // run.  Stages of larger distance go through memory, a barrier each.
+  const int lane = (int)(threadIdx.x & (kWave - 1));
+  const int wv = (int)(threadIdx.x / kWave);
+  // stages (k, j) for k = k_lo..k_hi and j = (k == k_lo ? j_lo : k/2) .. 1
+  auto wave_run = [&](int k_lo, int k_hi, int j_lo) __attribute__((always_inline)) {
+    for (int b = wv * kWave; b < n; b += NT) {
+      const int i = b + lane;
+      uint64_t x = i < n ? a[i] : 0ull;
+      for (int k = k_lo; k <= k_hi; k <<= 1) {
+        const bool up = ((i & k) == 0) != descending;
+        for (int j = (k == k_lo ? j_lo : (k >> 1)); j > 0; j >>= 1) {
+          const uint32_t lo = __shfl_xor((uint32_t)x, j, kWave);
+          const uint32_t hi = __shfl_xor((uint32_t)(x >> 32), j, kWave);
+          const uint64_t y = ((uint64_t)hi << 32) | lo;
+          // the lower index of a pair keeps the smaller value when ascending
+          const bool keep_small = ((i & j) == 0) == up;
+          x = keep_small ? (y < x ? y : x) : (y < x ? x : y);
+        }
+      }
+      if (i < n) a[i] = x;
+    }
+  };
+  if (n <= 1) return;
+  wave_run(2, n < kWave ? n : kWave, 1);
+  __syncthreads();
+  for (int k = 2 * kWave; k <= n; k <<= 1) {
+    for (int j = k >> 1; j >= kWave; j >>= 1) {
       for (int i = threadIdx.x; i < n; i += NT) {
         const int ixj = i ^ j;
         if (ixj > i) {
@@ -354,6 +383,8 @@ __device__ __forceinline__ void bitonic_sort_u64(Ptr a, int n, bool descending) 
       }
       __syncthreads();
     }
+    wave_run(k, k, kWave / 2);
+    __syncthreads();
   }
 }
 

@@ -21,9 +21,12 @@
 //   tie, and plain integer arithmetic in between.  Every step that the closed
 //   form does not cover is the hardware's own fp32 operation.
 //
-// All arithmetic on a, d and U is exact in binary64: a < 2^25 is an integer
-// and d carries at most 24 significant bits at or above 2^-25 when it matters
-// (d >= 1/2), so every sum used below fits in 53 bits.
+// The closed forms run in 32-bit integers and exact float operations: a, the
+// integer part of d and the step q are integers below 2^25, d = y * 2^(24-k)
+// is an exact power-of-two scaling of y (it only matters when 1/2 <= d <
+// 2^24), and d's fraction is exact.  The number of steps that stay in the
+// binade comes from the integer inequalities below, so no step is rounded
+// differently from the sequential loop.
 #pragma once
 #include <math.h>
 #include <stdint.h>
@@ -51,14 +54,56 @@ NLS_RD bool run_fast_ok(float x) {
   return x >= 0x1p-125f && x < 0x1p126f;
 }
 
-// Per-step integer change of the closed form, or -1 when the next step must
-// be taken as a real operation (an odd a facing a tie).  d >= 1/2.
-NLS_RD double run_step_q(double a, double d) {
-  const double fl = floor(d);
-  const double fr = d - fl;
-  if (fr != 0.5) return fr > 0.5 ? fl + 1.0 : fl;
-  if (fmod(a, 2.0) != 0.0) return -1.0;
-  return fmod(fl, 2.0) == 0.0 ? fl : fl + 1.0;
+// The integer form of x (positive, normal): x = a * 2^(k-24), a in
+// [2^23, 2^24); returns k.
+NLS_RD int run_split(float x, int32_t& a) {
+  int k;
+  const float m = frexpf(x, &k);  // m in [1/2, 1)
+  a = (int32_t)ldexpf(m, 24);
+  return k;
+}
+
+// One step of a run in units of the spacing: y / 2^(k-24) = fl + fr with fl
+// an integer and fr in [0, 1).  Returns false when y is at least 2^24 units
+// (the step leaves the binade at once).
+NLS_RD bool run_units(float y, int k, int32_t& fl, float& fr) {
+  const float d = ldexpf(y, 24 - k);  // exact, or 0 / subnormal when tiny
+  if (!(d < 0x1p24f)) return false;
+  const float f = floorf(d);
+  fl = (int32_t)f;
+  fr = d - f;  // exact
+  return true;
+}
+
+// Per-step integer change of the closed form: the rounded d (ties to the
+// even result, given an even a), or -1 when the step must be a real
+// operation (an odd a facing a tie).
+NLS_RD int32_t run_step(int32_t a, int32_t fl, float fr) {
+  if (fr != 0.5f) return fr > 0.5f ? fl + 1 : fl;
+  if (a & 1) return -1;
+  return (fl & 1) ? fl + 1 : fl;
+}
+
+// floor(n / q) for 0 <= n < 2^26 and 1 <= q < 2^26.
+NLS_RD int32_t run_div(int32_t n, int32_t q) {
+  int32_t t = (int32_t)((float)n / (float)q);  // within one of the answer
+  while (t > 0 && t * q > n) --t;
+  while ((t + 1) * q <= n) ++t;
+  return t;
+}
+
+// Steps (1-based j) that stay on the binade's grid when adding: a + (j-1)q +
+// fl + fr < 2^24, which for integer (j-1)q is (j-1)q <= 2^24 - a - fl - 1.
+NLS_RD int32_t run_steps_add(int32_t a, int32_t fl, int32_t q) {
+  const int32_t D = (1 << 24) - a - fl;
+  return D >= 1 ? run_div(D - 1, q) + 1 : 0;
+}
+
+// Steps that stay in the binade when subtracting: a - (j-1)q - fl - fr >=
+// 2^23, i.e. (j-1)q <= a - fl - 2^23, less one when fr > 0.
+NLS_RD int32_t run_steps_sub(int32_t a, int32_t fl, float fr, int32_t q) {
+  const int32_t E = a - fl - (1 << 23) - (fr > 0.0f ? 1 : 0);
+  return E >= 0 ? run_div(E, q) + 1 : 0;
 }
 
 // acc <- fl(acc + y), c times (acc >= 0, y >= 0).  Returns false when the
@@ -82,32 +127,28 @@ NLS_RD bool run_add(float& acc, float y, uint32_t c, int& budget) {
       acc = nx;
       return moved;
     }
-    double a, U;
-    const int k = run_binade(acc, a, U);
-    const double d = ldexp((double)y, 24 - k);
-    if (d < 0.5) return false;
-    const double q = run_step_q(a, d);
-    if (q == 0.0) return false;  // ties that keep an even acc
-    double t = 0.0;
-    if (q > 0.0) {
-      // step j (1-based) stays on this binade's grid iff a + (j-1)q + d < 2^24
-      const double lim = 0x1p24 - a - d;
-      if (lim > 0.0) {
-        t = floor(lim / q) + 1.0;
-        while (t > 0.0 && !(a + (t - 1.0) * q + d < 0x1p24)) t -= 1.0;
-        while (a + t * q + d < 0x1p24) t += 1.0;
-        if (t > (double)c) t = (double)c;
+    int32_t a, fl;
+    float fr;
+    const int k = run_split(acc, a);
+    int32_t t = 0;
+    if (run_units(y, k, fl, fr)) {
+      if (fl == 0 && fr < 0.5f) return false;  // d < 1/2
+      const int32_t q = run_step(a, fl, fr);
+      if (q == 0) return false;  // ties that keep an even acc
+      if (q > 0) {
+        t = run_steps_add(a, fl, q);
+        if ((uint32_t)t > c) t = (int32_t)c;
+      }
+      if (t >= 1) {
+        a += t * q;
+        acc = ldexpf((float)a, k - 24);
+        c -= (uint32_t)t;
+        continue;
       }
     }
-    if (t >= 1.0) {
-      a += t * q;
-      acc = (float)(a * U);
-      c -= (uint32_t)t;
-    } else {
-      if (--budget < 0) return true;
-      acc = acc + y;
-      --c;
-    }
+    if (--budget < 0) return true;
+    acc = acc + y;
+    --c;
   }
   return true;
 }
@@ -138,38 +179,34 @@ NLS_RD uint32_t run_add_until(float& acc, float y, uint32_t c, double target, in
       acc = nx;
       return (double)acc >= target ? done + 1 : 0;
     }
-    double a, U;
-    const int k = run_binade(acc, a, U);
-    const double d = ldexp((double)y, 24 - k);
-    const double q = d < 0.5 ? 0.0 : run_step_q(a, d);
-    if (q == 0.0) {
-      *more = false;
-      return (double)acc >= target ? done + 1 : 0;
-    }
-    double t = 0.0;
-    if (q > 0.0) {
-      const double lim = 0x1p24 - a - d;
-      if (lim > 0.0) {
-        t = floor(lim / q) + 1.0;
-        while (t > 0.0 && !(a + (t - 1.0) * q + d < 0x1p24)) t -= 1.0;
-        while (a + t * q + d < 0x1p24) t += 1.0;
-        const double left = (double)(c - done);
-        if (t > left) t = left;
+    int32_t a, fl;
+    float fr;
+    const int k = run_split(acc, a);
+    int32_t t = 0, q = 1;
+    if (run_units(y, k, fl, fr)) {
+      q = (fl == 0 && fr < 0.5f) ? 0 : run_step(a, fl, fr);
+      if (q == 0) {
+        *more = false;
+        return (double)acc >= target ? done + 1 : 0;
+      }
+      if (q > 0) {
+        t = run_steps_add(a, fl, q);
+        if ((uint32_t)t > c - done) t = (int32_t)(c - done);
       }
     }
-    if (t >= 1.0) {
-      // the first j <= t with (a + j q) U >= target, if any
-      if ((a + t * q) * U >= target) {
-        double j = ceil((ldexp(target, 24 - k) - a) / q);
-        if (j < 1.0) j = 1.0;
-        if (j > t) j = t;
-        while (j > 1.0 && (a + (j - 1.0) * q) * U >= target) j -= 1.0;
-        while (!((a + j * q) * U >= target)) j += 1.0;
-        acc = (float)((a + j * q) * U);
+    if (t >= 1) {
+      // (double)acc >= target after step j  <=>  a + j q >= target / U, an
+      // exact scaling; a + j q is an integer, so against its ceiling C
+      const double C = ceil(ldexp(target, 24 - k));
+      if ((double)(a + t * q) >= C) {
+        int32_t j = 1;
+        const int32_t need = (int32_t)C - a;  // C <= a + t q < 2^26 here
+        if (need > q) j = run_div(need - 1, q) + 1;
+        acc = ldexpf((float)(a + j * q), k - 24);
         return done + (uint32_t)j;
       }
       a += t * q;
-      acc = (float)(a * U);
+      acc = ldexpf((float)a, k - 24);
       done += (uint32_t)t;
     } else {
       if (--budget < 0) return 0;
@@ -206,29 +243,25 @@ NLS_RD uint32_t run_sub_until(float& r, float y, uint32_t c, int& budget, bool* 
       r = nx;
       return r <= 0.0f ? done + 1 : 0;
     }
-    double a, U;
-    const int k = run_binade(r, a, U);
-    const double d = ldexp((double)y, 24 - k);
-    const double q = d < 0.5 ? 0.0 : run_step_q(a, d);
-    if (q == 0.0) {
-      *more = false;
-      return 0;
-    }
-    double t = 0.0;
-    if (q > 0.0) {
-      // step j stays in the binade (and so positive) iff a - (j-1)q - d >= 2^23
-      const double lim = a - d - 0x1p23;
-      if (lim >= 0.0) {
-        t = floor(lim / q) + 1.0;
-        while (t > 0.0 && !(a - (t - 1.0) * q - d >= 0x1p23)) t -= 1.0;
-        while (a - t * q - d >= 0x1p23) t += 1.0;
-        const double left = (double)(c - done);
-        if (t > left) t = left;
+    int32_t a, fl;
+    float fr;
+    const int k = run_split(r, a);
+    int32_t t = 0, q = 1;
+    if (run_units(y, k, fl, fr)) {
+      q = (fl == 0 && fr < 0.5f) ? 0 : run_step(a, fl, fr);
+      if (q == 0) {
+        *more = false;
+        return 0;
+      }
+      if (q > 0) {
+        // every step inside the binade leaves r >= 2^(k-1) > 0
+        t = run_steps_sub(a, fl, fr, q);
+        if ((uint32_t)t > c - done) t = (int32_t)(c - done);
       }
     }
-    if (t >= 1.0) {
+    if (t >= 1) {
       a -= t * q;
-      r = (float)(a * U);
+      r = ldexpf((float)a, k - 24);
       done += (uint32_t)t;
     } else {
       if (--budget < 0) return 0;

@@ -191,6 +191,37 @@ def test_patched_ids_that_fall_or_rise(pkg, torch, B, V):
     compare_rows(x, plist, hists, biases, u, ids, dbg, f"B={B} V={V}")
 
 
+@pytest.mark.parametrize("B", [8, 300])
+def test_topk_rows_in_sorted_order(pkg, torch, B):
+    """Top-k rows (64 < k <= 2048) whose first tile is not typical of the row:
+    logits in descending order (the first tile holds the row's largest values,
+    so a threshold taken from it admits fewer than k), ascending order, and
+    shuffled, with ties.  Every id, candidate list and probability must match
+    the oracle."""
+    rng = np.random.default_rng(4242 + B)
+    V = 60000
+    say(f"[topk_sorted] B={B} V={V}")
+    base = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    x = np.empty_like(base)
+    for b in range(B):
+        r = np.sort(base[b])
+        if b % 4 == 0:
+            x[b] = r[::-1]
+        elif b % 4 == 1:
+            x[b] = r
+        elif b % 4 == 2:
+            x[b] = np.round(r[::-1] * 4.0) / 4.0
+        else:
+            x[b] = base[b]
+    ks = [65, 200, 1000, 2048]
+    plist = [dict(temperature=1.0, topK=ks[b % len(ks)], topP=0.95, minP=0.0, repeatPenalty=1.0,
+                  repeatLastN=0, presencePenalty=0.0, frequencyPenalty=0.0, seed=1) for b in range(B)]
+    u = rng.random(B)
+    params = [to_pkg_params(pkg, plist[b], {}) for b in range(B)]
+    ids, dbg = run_gpu(pkg, torch, x, params, None, u, debug_cap=64)
+    compare_rows(x, plist, [[] for _ in range(B)], [{} for _ in range(B)], u, ids, dbg, f"B={B}")
+
+
 def test_golden_fixtures(pkg, torch):
     import json
     import os
