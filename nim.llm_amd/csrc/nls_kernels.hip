@@ -1964,15 +1964,70 @@ __device__ GroupOut grouped_row(const GenericArgs& a, int row, const RowParams& 
   const float mx = key2f(mk);
   if (anynan || !(mx > -__builtin_inff() && mx < __builtin_inff())) return res;
   // ---- count every value that can move the sum ----
-  for_each_final([&](float v) {
-    if (v - mx >= kGroupFloor) {
-      if (!group_insert(L, f2key(v), &s_distinct)) {
-        s_fail = 1;
-        return false;
+  // Sixteen values at a time: their table slots are read together, a value
+  // already in the table at its first slot is counted with one atomic add,
+  // and only the others (first occurrences, collisions) probe.
+  {
+    bool bad = false;
+    auto count16 = [&](const float (&vv)[16], uint32_t want) __attribute__((always_inline)) {
+      uint32_t key[16], hs[16], cur[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        key[q] = f2key(vv[q]);
+        hs[q] = (key[q] * 0x9E3779B1u) >> (32 - kGrpHashBits);
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) cur[q] = L.hkey[hs[q]];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        if (!((want >> q) & 1u)) continue;
+        if (cur[q] == key[q])
+          atomicAdd(&L.hcnt[hs[q]], 1u);
+        else
+          bad |= !group_insert(L, key[q], &s_distinct);
+      }
+    };
+    if (vec) {
+      for (int b4 = tid; b4 < V4 && !bad; b4 += 4 * NT) {
+        float4 x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = src4[min(b4 + u * NT, V4 - 1)];
+        float vv[16];
+        uint32_t want = 0u;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i4 = b4 + u * NT;
+          const uint32_t pb = i4 < V4 ? (L.bitmap[i4 >> 3] >> ((i4 & 7) * 4)) & 15u : 15u;
+          vv[4 * u + 0] = x[u].x * invT;
+          vv[4 * u + 1] = x[u].y * invT;
+          vv[4 * u + 2] = x[u].z * invT;
+          vv[4 * u + 3] = x[u].w * invT;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (!((pb >> c) & 1u) && vv[4 * u + c] - mx >= kGroupFloor) want |= 1u << (4 * u + c);
+        }
+        count16(vv, want);
+      }
+    } else {
+      for (int b = tid; b < V && !bad; b += 16 * NT) {
+        float vv[16];
+        uint32_t want = 0u;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int i = b + q * NT;
+          vv[q] = i < V ? src[i] * invT : 0.0f;
+          if (i < V && !((L.bitmap[i >> 5] >> (i & 31)) & 1u) && vv[q] - mx >= kGroupFloor)
+            want |= 1u << q;
+        }
+        count16(vv, want);
       }
     }
-    return true;
-  });
+    for (int sl = tid; sl < np && !bad; sl += NT) {
+      const float v = L.pfin[sl];
+      if (v - mx >= kGroupFloor) bad |= !group_insert(L, f2key(v), &s_distinct);
+    }
+    if (bad) s_fail = 1;
+  }
   __syncthreads();
   if (s_fail) return res;
   for (int h = tid; h < kGrpHashCap; h += NT) {
@@ -2056,16 +2111,41 @@ __device__ GroupOut grouped_row(const GenericArgs& a, int row, const RowParams& 
   };
   const int W = vec ? 4 : 1;
   const int nblk = (V + kWave * W - 1) / (kWave * W);  // <= 2 * kGrpPatchCap for V <= kGrpMaxV
+  // Counting pass: the unpatched members by value alone (the bitmap is read
+  // only where a value matches), then the patched members from the patch
+  // table; the exact search below walks one block with final_at.
+  auto unpatched_at = [&](int i) -> bool { return !((L.bitmap[i >> 5] >> (i & 31)) & 1u); };
+  auto lane_count = [&](int bk) -> int {
+    int m = 0;
+    if (vec) {
+      const int i4 = bk * kWave + lane;
+      if (i4 < V4) {
+        const float4 x = src4[i4];
+        const int i = i4 * 4;
+        if (x.x * invT == vg && unpatched_at(i)) ++m;
+        if (x.y * invT == vg && unpatched_at(i + 1)) ++m;
+        if (x.z * invT == vg && unpatched_at(i + 2)) ++m;
+        if (x.w * invT == vg && unpatched_at(i + 3)) ++m;
+      }
+    } else {
+      const int i = bk * kWave + lane;
+      if (i < V && src[i] * invT == vg && unpatched_at(i)) m = 1;
+    }
+    return m;
+  };
   for (int b0 = wv; b0 < nblk; b0 += 4 * NW) {
-    uint32_t m[4];
+    int m[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) m[u] = (b0 + u * NW < nblk) ? lane_members(b0 + u * NW) : 0u;
+    for (int u = 0; u < 4; ++u) m[u] = (b0 + u * NW < nblk) ? lane_count(b0 + u * NW) : 0;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int c = wave_sum_i(__popc(m[u]));
+      const int c = wave_sum_i(m[u]);
       if (lane == 0 && b0 + u * NW < nblk) bcnt[b0 + u * NW] = (uint32_t)c;
     }
   }
+  __syncthreads();
+  for (int sl = tid; sl < np; sl += NT)
+    if (L.pfin[sl] == vg) atomicAdd(&bcnt[L.pid[sl] / (kWave * W)], 1u);
   __syncthreads();
   if (wv == 0) {
     int64_t left = t;
