@@ -29,12 +29,133 @@ constexpr int kGroupBudget = 1 << 16;  // real fp32 operations allowed per chain
 
 enum GroupStatus : int32_t { kGroupOk = 0, kGroupNeedAll = 1, kGroupBudgetOut = 2 };
 
+// ---- look-ahead over groups --------------------------------------------
+// Starting at group g with the running value acc, the groups whose whole run
+// stays on acc's binade grid with no tie can be applied together: each adds
+// (or takes away) c_h * q_h spacings, q_h = R(y_h / U), so the running value
+// after them is a prefix sum of integers.  group_skip applies the longest
+// such stretch of groups [g, g + m) and returns m; the group where it stops
+// (a binade crossing, a tie, a term below half a spacing, the target reached,
+// the count cap passed) is left to the run closed forms, one group at a time.
+// The stretch is found 64 groups at a time: on the device every lane of the
+// calling wave takes one group (the wave must be converged and its values
+// uniform), on the host a loop stands in for the lanes.
+//   SUB = false: acc += y (runs of run_add / run_add_until); with has_target,
+//                stops at the group where (double)acc first reaches target.
+//   SUB = true:  acc -= y (runs of run_sub_until); acc stays >= 2^(k-1) > 0.
+// *skipped gets the candidates of the applied groups; their sum may not pass
+// `cap`.
+constexpr int kSkipLanes = 64;
+
+// One group against binade k: its step q (in spacings), integer part fl and
+// fraction fr of y / U; false when the group needs the closed forms (y not
+// positive, y / U below 1/2 or at least 2^24, or a tie).
+NLS_RD bool skip_setup(float y, int k, int32_t& q, int32_t& fl, float& fr) {
+  if (!(y > 0.0f)) return false;
+  if (!run_units(y, k, fl, fr)) return false;
+  if (fl == 0 && fr < 0.5f) return false;
+  if (fr == 0.5f) return false;
+  q = fr > 0.5f ? fl + 1 : fl;
+  return true;
+}
+
+// Whether group h, whose run ends at integer position E = A + P (adds) or
+// A - P (subtractions) after P spacings in all, stays on the grid.
+template <bool SUB>
+NLS_RD bool skip_stays(double A, double P, int32_t q, int32_t fl, float fr, bool has_target,
+                       double target, double U) {
+  if (!SUB) {
+    // last step: a_h + (c - 1) q + fl + fr < 2^24 with a_h + c q = A + P
+    if (!(A + P - q + fl < 0x1p24)) return false;
+    return !(has_target && (A + P) * U >= target);
+  }
+  // last step: a_h - (c - 1) q - fl - fr >= 2^23
+  return A - P + q - fl - (fr > 0.0f ? 1 : 0) >= 0x1p23;
+}
+
+#if defined(__HIP_DEVICE_COMPILE__)
+__device__ __forceinline__ double skip_scan(double v) {
+  const int lane = (int)(threadIdx.x & (kSkipLanes - 1));
+#pragma unroll
+  for (int o = 1; o < kSkipLanes; o <<= 1) {
+    const double t = __shfl_up(v, o, kSkipLanes);
+    if (lane >= o) v += t;  // integers below 2^53: exact
+  }
+  return v;
+}
+#endif
+
+template <bool SUB>
+NLS_RD int group_skip(float& acc, const float* y, const uint32_t* c, int g, int gend, bool has_target,
+                      double target, int64_t cap, int64_t* skipped) {
+  *skipped = 0;
+  if (g >= gend || !run_fast_ok(acc)) return 0;
+  int32_t a0;
+  const int k = run_split(acc, a0);
+  const double U = ldexp(1.0, k - 24);
+  double A = (double)a0, S = 0.0;
+  int done = 0;
+  for (int base = g; base < gend; base += kSkipLanes) {
+    const int nv = gend - base < kSkipLanes ? gend - base : kSkipLanes;
+    int m = nv;
+    double Pm = 0.0, Sm = 0.0;
+#if defined(__HIP_DEVICE_COMPILE__)
+    {
+      const int lane = (int)(threadIdx.x & (kSkipLanes - 1));
+      const bool valid = lane < nv;
+      const float yh = valid ? y[base + lane] : 0.0f;
+      const uint32_t ch = valid ? c[base + lane] : 0u;
+      int32_t q = 0, fl = 0;
+      float fr = 0.0f;
+      bool ok = valid && skip_setup(yh, k, q, fl, fr);
+      const double P = skip_scan(ok ? (double)ch * (double)q : 0.0);
+      const double Sc = skip_scan((double)ch);
+      if (ok) ok = skip_stays<SUB>(A, P, q, fl, fr, has_target, target, U) && S + Sc <= (double)cap;
+      const uint64_t bad = __ballot(valid && !ok);
+      if (bad) m = __ffsll((unsigned long long)bad) - 1;
+      if (m > 0) {
+        Pm = __shfl(P, m - 1, kSkipLanes);
+        Sm = __shfl(Sc, m - 1, kSkipLanes);
+      }
+    }
+#else
+    {
+      double P = 0.0, Sc = 0.0;
+      for (int l = 0; l < nv; ++l) {
+        int32_t q = 0, fl = 0;
+        float fr = 0.0f;
+        bool ok = skip_setup(y[base + l], k, q, fl, fr);
+        P += ok ? (double)c[base + l] * (double)q : 0.0;
+        Sc += (double)c[base + l];
+        if (ok) ok = skip_stays<SUB>(A, P, q, fl, fr, has_target, target, U) && S + Sc <= (double)cap;
+        if (!ok) {
+          m = l;
+          break;
+        }
+        Pm = P;
+        Sm = Sc;
+      }
+    }
+#endif
+    A = SUB ? A - Pm : A + Pm;
+    S += Sm;
+    done += m;
+    if (m < nv) break;
+  }
+  if (done > 0) acc = ldexpf((float)A, k - 24);
+  *skipped = (int64_t)S;
+  return done;
+}
+
 // s = the softmax sum (:55-56) over the groups' exponentials ge[] (group g
 // repeated gc[g] times), in order.  Returns false when the budget ran out.
 NLS_RD bool group_sum(const float* ge, const uint32_t* gc, int G, float& s) {
   float acc = 0.0f;
   int budget = kGroupBudget;
+  int64_t sk;
   for (int g = 0; g < G; ++g) {
+    g += group_skip<false>(acc, ge, gc, g, G, false, 0.0, INT64_MAX, &sk);
+    if (g >= G) break;
     const bool more = run_add(acc, ge[g], gc[g], budget);
     if (budget < 0) return false;
     if (!more) break;
@@ -68,6 +189,10 @@ NLS_RD GroupDraw group_cut_draw(const float* pg, const uint32_t* gc, int G, bool
     int64_t pos = 0;
     bool found = false, more = true;
     for (int g = 0; g < G; ++g) {
+      int64_t sk;
+      g += group_skip<false>(cum, pg, gc, g, G, true, topP, INT64_MAX, &sk);
+      pos += sk;
+      if (g >= G) break;
       const uint32_t j = run_add_until(cum, pg[g], gc[g], topP, budget, &more);
       if (budget < 0) {
         out.status = kGroupBudgetOut;
@@ -112,6 +237,10 @@ NLS_RD GroupDraw group_cut_draw(const float* pg, const uint32_t* gc, int G, bool
     int64_t pos = 0;
     bool more = true;
     for (int g = 0; g < G && pos < n; ++g) {
+      int64_t sk;
+      g += group_skip<false>(total, pg, gc, g, G, false, 0.0, n - pos, &sk);
+      pos += sk;
+      if (g >= G || pos >= n) break;
       const int64_t left = n - pos;
       const uint32_t c = (int64_t)gc[g] < left ? gc[g] : (uint32_t)left;
       more = run_add(total, pg[g], c, budget);
@@ -133,6 +262,12 @@ NLS_RD GroupDraw group_cut_draw(const float* pg, const uint32_t* gc, int G, bool
   {
     int64_t pos = 0;
     for (int g = 0; g < G && pos < n; ++g) {
+      int64_t sk;
+      if (r > 0.0f) {
+        g += group_skip<true>(r, pg, gc, g, G, false, 0.0, n - pos, &sk);
+        pos += sk;
+      }
+      if (g >= G || pos >= n) break;
       const int64_t left = n - pos;
       const uint32_t c = (int64_t)gc[g] < left ? gc[g] : (uint32_t)left;
       bool more = true;

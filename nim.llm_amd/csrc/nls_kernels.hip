@@ -2054,25 +2054,32 @@ __device__ GroupOut grouped_row(const GenericArgs& a, int row, const RowParams& 
     atomicAdd(&s_held, (unsigned long long)(uint32_t)e);
   }
   __syncthreads();
-  if (tid == 0) {
+  // wave 0 walks the groups (its lanes look ahead 64 groups at a time)
+  if (tid < kWave) {
     float s = 0.0f;
-    if (!group_sum(ge, gc, G, s)) s_fail = 1;
-    s_sum = s;
+    const bool ok = group_sum(ge, gc, G, s);
+    if (tid == 0) {
+      if (!ok) s_fail = 1;
+      s_sum = s;
+    }
   }
   __syncthreads();
   if (s_fail) return res;
   const float s = s_sum;
   for (int g = tid; g < G; g += NT) ge[g] = ge[g] / s;  // (:57)
   __syncthreads();
-  if (tid == 0) {
-    s_draw = group_cut_draw(ge, gc, G, s_held == (unsigned long long)V, a.V, P.topp_active != 0, P.topP,
-                            P.minp_active != 0, P.minP32, u);
-    int64_t pos = s_draw.pos;
-    int g = 0;
-    if (s_draw.status == kGroupOk)
-      while (g < G - 1 && pos >= (int64_t)gc[g]) pos -= gc[g++];
-    s_g = g;
-    s_t = pos;
+  if (tid < kWave) {
+    const GroupDraw dr = group_cut_draw(ge, gc, G, s_held == (unsigned long long)V, a.V,
+                                        P.topp_active != 0, P.topP, P.minp_active != 0, P.minP32, u);
+    if (tid == 0) {
+      s_draw = dr;
+      int64_t pos = dr.pos;
+      int g = 0;
+      if (dr.status == kGroupOk)
+        while (g < G - 1 && pos >= (int64_t)gc[g]) pos -= gc[g++];
+      s_g = g;
+      s_t = pos;
+    }
   }
   __syncthreads();
   if (s_draw.status != kGroupOk) return res;
