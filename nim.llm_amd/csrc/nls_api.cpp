@@ -216,8 +216,33 @@ struct Geometry {
   size_t lds;
 };
 
-Geometry plan_geometry(int B, int64_t V, int kmax, int ncu) {
+Geometry plan_geometry(int B, int64_t V, int kmax, int ncu, int max_patch) {
   Geometry g{};
+  // Top-k rows past the wave path (k > 64) on a batch of at least two rows
+  // per CU: 512-thread workgroups whose LDS leaves room for two per CU, so
+  // that one row's selection and tail run while the other row streams.
+  if (kmax > kWaveTopK && B >= 2 * ncu && max_patch >= 0 && env_int("NLS_STREAM_NT", 512) == 512) {
+    Geometry d{};
+    d.nt = 512;
+    d.S = 1;
+    d.L = (int)((V + 3) / 4 * 4);
+    d.pc = 0;
+    d.wave = false;
+    d.ccap = next_pow2_i(std::max<int64_t>(1024, 2LL * kmax));
+    d.nwords = (int)((V + 31) / 32);
+    d.mcap = next_pow2_i(std::max(2 * kmax, 2));
+    d.kcap = kmax;
+    d.q = 1;
+    while (d.q < 8 && (int64_t)d.q * d.nt < 2LL * kmax) d.q <<= 1;
+    const size_t cand = (size_t)2 * d.ccap * 8;
+    const size_t head = (size_t)d.nwords * 4 + (((size_t)d.nwords * 2 + 3) & ~(size_t)3);
+    const size_t tail = (size_t)d.mcap * 8 + (size_t)d.kcap * 12;
+    const size_t target = kDualStreamLds;
+    d.offA = (int)cand;
+    if (cand + head < target) d.pcap = (int)std::min<size_t>(65535, (target - cand - head) / 16);
+    d.lds = cand + std::max(head + (size_t)d.pcap * 16, tail);
+    if (d.lds <= target && d.pcap >= std::max(max_patch, 1)) return d;
+  }
   // 256-thread workgroups, >= 4 per CU: rows are split into S slices until the
   // grid holds about 4 workgroups per CU, keeping >= 2 tiles per slice.
   // a whole row per 1024-thread workgroup once the batch fills the chip;
@@ -339,6 +364,7 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   std::vector<NimRand> rng_h(B);
   std::random_device rd;
   int kmax = 0;
+  int max_patch = 0;  // patched ids a row can need (window + bias); -1: unbounded window
   for (int b = 0; b < B; ++b) {
     const nls_params& p = per_row[b];
     if (p.logit_bias_count < 0 || (p.logit_bias_count > 0 &&
@@ -380,6 +406,13 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
       if (r.mode == kModeTopK && k <= kMaxTopKFast) kmax = std::max(kmax, (int)k);
     }
     if (r.pen_active) s->need_window[b] = p.repeat_last_n > 0 ? (int)std::min<int64_t>(p.repeat_last_n, 1 << 24) : -1;
+    if (max_patch >= 0) {
+      if (r.pen_active && p.repeat_last_n <= 0)
+        max_patch = -1;
+      else
+        max_patch = std::max(max_patch, (r.pen_active ? (int)std::min<int64_t>(p.repeat_last_n, 1 << 24) : 0) +
+                                            (int)r.bias_cnt);
+    }
     int64_t seed = p.seed;
     if (seed < 0) {
       const uint64_t t = (uint64_t)std::chrono::high_resolution_clock::now().time_since_epoch().count();
@@ -393,10 +426,10 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 1)
     ncu = 256;
   int kfast = kmax;
-  Geometry g = plan_geometry(B, vocab, kfast, ncu);
-  while (kfast > 0 && (g.lds > max_dynamic_lds() || g.pcap < 256)) {
+  Geometry g = plan_geometry(B, vocab, kfast, ncu, max_patch);
+  while (kfast > 0 && (g.lds > max_dynamic_lds() || (g.nt != 512 && g.pcap < 256))) {
     kfast = kfast * 7 / 8;
-    g = plan_geometry(B, vocab, kfast, ncu);
+    g = plan_geometry(B, vocab, kfast, ncu, max_patch);
   }
   // (false only for vocabularies far beyond 2^19; the slice's byte size must
   // also fit the 32-bit range of the kernel's buffer loads)

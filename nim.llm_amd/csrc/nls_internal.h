@@ -50,6 +50,7 @@ constexpr int kGenericThreads = 1024;
 constexpr int kMaxSlices = 64;
 constexpr int kWaveCap = 256;        // per-wave candidate buffer of the k <= 64 path
 constexpr int kWaveTopK = 64;        // largest k of the wave path
+constexpr size_t kDualStreamLds = 68 * 1024;  // dynamic LDS of a 512-thread workgroup, two per CU
 
 // Slice-exchange record of one (row, slice) when a row is split over S
 // workgroups.
@@ -149,7 +150,7 @@ struct StreamArgs {
 
 
 struct LaunchPlan {
-  int nt;        // streaming workgroup size: 256 or 1024
+  int nt;        // streaming workgroup size: 256, 512 (k > 64, two per CU) or 1024
   bool wave;     // every top-k row has k <= kWaveTopK: per-wave candidate buffers
   int q;         // per-thread top-Q of the threshold refresh: 1, 2, 4 or 8
   bool vec4;     // 16-byte loads (V % 4 == 0 and aligned logits)

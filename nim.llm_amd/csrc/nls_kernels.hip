@@ -458,7 +458,7 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
 // the argmax does it test the bitmap -- and they rejoin the candidates (or
 // the argmax) after the stream.
 template <int NT, bool VEC, int Q, bool WAVE>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT <= 256 ? 4 : 2)))
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT <= 512 ? 4 : 2)))
 void stream_kernel(const StreamArgs a) {
   constexpr int NW = NT / kWave;
   constexpr int NV4 = kStreamVec4;
@@ -780,7 +780,8 @@ void stream_kernel(const StreamArgs a) {
     // number at least k, and the row goes to the whole-row path otherwise.
     int spec_rank = 0;
     if (!WAVE && topk && a.S == 1 && len > UE) {
-      const int64_t r = (2LL * k * UE + len - 1) / len;
+      const int64_t want = min(2LL * k, (int64_t)a.ccap * 7 / 8);  // passing elements aimed at
+      const int64_t r = (want * UE + len - 1) / len;
       spec_rank = r < k ? (int)r : 0;
     }
     bool spec_used = false;
@@ -2697,7 +2698,19 @@ static hipError_t launch_stream_q(const StreamArgs& a, const LaunchPlan& p, hipS
   }
 }
 
+// 512-thread workgroups serve only the block path (k > 64)
+template <bool VEC>
+static hipError_t launch_stream_dual(const StreamArgs& a, const LaunchPlan& p, hipStream_t s) {
+  switch (p.q) {
+    case 1: return launch_stream_t<512, VEC, 1, false>(a, p.lds, s);
+    case 2: return launch_stream_t<512, VEC, 2, false>(a, p.lds, s);
+    case 4: return launch_stream_t<512, VEC, 4, false>(a, p.lds, s);
+    default: return launch_stream_t<512, VEC, 8, false>(a, p.lds, s);
+  }
+}
+
 static hipError_t launch_stream(const StreamArgs& a, const LaunchPlan& p, hipStream_t s) {
+  if (p.nt == 512) return p.vec4 ? launch_stream_dual<true>(a, p, s) : launch_stream_dual<false>(a, p, s);
   if (p.nt == 1024)
     return p.vec4 ? launch_stream_q<1024, true>(a, p, s) : launch_stream_q<1024, false>(a, p, s);
   return p.vec4 ? launch_stream_q<256, true>(a, p, s) : launch_stream_q<256, false>(a, p, s);
@@ -2747,8 +2760,19 @@ static hipError_t set_attr_q() {
   return set_attr_one<NT, VEC, 8, false>();
 }
 
+template <bool VEC>
+static hipError_t set_attr_dual() {
+  hipError_t e;
+  if ((e = set_attr_one<512, VEC, 1, false>()) != hipSuccess) return e;
+  if ((e = set_attr_one<512, VEC, 2, false>()) != hipSuccess) return e;
+  if ((e = set_attr_one<512, VEC, 4, false>()) != hipSuccess) return e;
+  return set_attr_one<512, VEC, 8, false>();
+}
+
 hipError_t set_kernel_attributes() {
   hipError_t e;
+  if ((e = set_attr_dual<true>()) != hipSuccess) return e;
+  if ((e = set_attr_dual<false>()) != hipSuccess) return e;
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(&generic_kernel<kGenericThreads>),
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)group_lds_bytes(kGrpMaxV))) != hipSuccess)

@@ -191,7 +191,7 @@ def test_patched_ids_that_fall_or_rise(pkg, torch, B, V):
     compare_rows(x, plist, hists, biases, u, ids, dbg, f"B={B} V={V}")
 
 
-@pytest.mark.parametrize("B", [8, 300])
+@pytest.mark.parametrize("B", [8, 300, 600])
 def test_topk_rows_in_sorted_order(pkg, torch, B):
     """Top-k rows (64 < k <= 2048) whose first tile is not typical of the row:
     logits in descending order (the first tile holds the row's largest values,
@@ -220,6 +220,36 @@ def test_topk_rows_in_sorted_order(pkg, torch, B):
     params = [to_pkg_params(pkg, plist[b], {}) for b in range(B)]
     ids, dbg = run_gpu(pkg, torch, x, params, None, u, debug_cap=64)
     compare_rows(x, plist, [[] for _ in range(B)], [{} for _ in range(B)], u, ids, dbg, f"B={B}")
+
+
+def test_topk_rows_with_window_and_bias_two_per_cu(pkg, torch):
+    """A batch of top-k rows (64 < k <= 2048) large enough for two streaming
+    workgroups per CU, with repetition/frequency/presence penalties over a
+    bounded window and logit bias, so the patch table is in use on that
+    path; ids, candidates and probabilities against the oracle."""
+    rng = np.random.default_rng(777)
+    B, V, H = 560, 24000, 48
+    say(f"[topk_two_per_cu] B={B} V={V}")
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    x[::7] = np.round(x[::7] * 4.0) / 4.0  # ties on some rows
+    hist = rng.integers(0, V, size=(B, H)).astype(np.int64)
+    hist[:, H // 2:] = hist[:, :H // 2]  # repeated ids: counts above one
+    ks = [65, 130, 700, 2048]
+    plist, biases = [], []
+    for b in range(B):
+        plist.append(dict(temperature=float(rng.choice([0.7, 1.0])), topK=ks[b % len(ks)],
+                          topP=float(rng.choice([0.9, 1.0])), minP=float(rng.choice([0.0, 0.05])),
+                          repeatPenalty=1.1, repeatLastN=32, presencePenalty=0.3,
+                          frequencyPenalty=0.5, seed=1))
+        ids = rng.choice(V, 6, replace=False)
+        bias = {int(i): float(rng.uniform(-5, 5)) for i in ids}
+        bias[int(ids[0])] = -math.inf
+        bias[int(ids[1])] = 6.0  # a raising bias
+        biases.append(bias)
+    u = rng.random(B)
+    params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
+    ids_, dbg = run_gpu(pkg, torch, x, params, hist, u, debug_cap=64)
+    compare_rows(x, plist, [list(hist[b]) for b in range(B)], biases, u, ids_, dbg, "two_per_cu")
 
 
 def test_golden_fixtures(pkg, torch):
