@@ -147,6 +147,24 @@ NLS_RD int group_skip(float& acc, const float* y, const uint32_t* c, int g, int 
   return done;
 }
 
+// The candidates the groups hold, sum of gc[0..G) (on the device the calling
+// wave adds 64 groups per step).
+NLS_RD int64_t group_count_sum(const uint32_t* gc, int G) {
+  int64_t held = 0;
+#if defined(__HIP_DEVICE_COMPILE__)
+  const int lane = (int)(threadIdx.x & (kSkipLanes - 1));
+  for (int base = 0; base < G; base += kSkipLanes) {
+    double c = base + lane < G ? (double)gc[base + lane] : 0.0;
+#pragma unroll
+    for (int o = kSkipLanes / 2; o > 0; o >>= 1) c += __shfl_xor(c, o, kSkipLanes);
+    held += (int64_t)c;
+  }
+#else
+  for (int g = 0; g < G; ++g) held += gc[g];
+#endif
+  return held;
+}
+
 // s = the softmax sum (:55-56) over the groups' exponentials ge[] (group g
 // repeated gc[g] times), in order.  Returns false when the budget ran out.
 NLS_RD bool group_sum(const float* ge, const uint32_t* gc, int G, float& s) {
@@ -286,8 +304,7 @@ NLS_RD GroupDraw group_cut_draw(const float* pg, const uint32_t* gc, int G, bool
   }
   if (hit < 0) hit = n - 1;  // (:121)
   // the drawn candidate must lie inside the groups
-  int64_t held = 0;
-  for (int g = 0; g < G; ++g) held += gc[g];
+  const int64_t held = complete ? V : group_count_sum(gc, G);
   if (hit >= held) {
     out.status = kGroupNeedAll;
     return out;

@@ -1965,28 +1965,31 @@ __device__ GroupOut grouped_row(const GenericArgs& a, int row, const RowParams& 
   const float mx = key2f(mk);
   if (anynan || !(mx > -__builtin_inff() && mx < __builtin_inff())) return res;
   // ---- count every value that can move the sum ----
-  // Sixteen values at a time: their table slots are read together, a value
-  // already in the table at its first slot is counted with one atomic add,
-  // and only the others (first occurrences, collisions) probe.
+  // Eight values at a time (the kernel runs at its register limit): their
+  // table slots are read together, a value already in the table at its first
+  // slot is counted with one atomic add, and only the others (first
+  // occurrences, collisions) probe.
   {
     bool bad = false;
-    auto count16 = [&](const float (&vv)[16], uint32_t want) __attribute__((always_inline)) {
-      uint32_t key[16], hs[16], cur[16];
+    auto count8 = [&](const float* vv, uint32_t want) __attribute__((always_inline)) {
+      uint32_t hs[8], cur[8];
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        key[q] = f2key(vv[q]);
-        hs[q] = (key[q] * 0x9E3779B1u) >> (32 - kGrpHashBits);
-      }
+      for (int q = 0; q < 8; ++q) hs[q] = (f2key(vv[q]) * 0x9E3779B1u) >> (32 - kGrpHashBits);
 #pragma unroll
-      for (int q = 0; q < 16; ++q) cur[q] = L.hkey[hs[q]];
+      for (int q = 0; q < 8; ++q) cur[q] = L.hkey[hs[q]];
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
+      for (int q = 0; q < 8; ++q) {
         if (!((want >> q) & 1u)) continue;
-        if (cur[q] == key[q])
+        const uint32_t key = f2key(vv[q]);
+        if (cur[q] == key)
           atomicAdd(&L.hcnt[hs[q]], 1u);
         else
-          bad |= !group_insert(L, key[q], &s_distinct);
+          bad |= !group_insert(L, key, &s_distinct);
       }
+    };
+    auto count16 = [&](const float (&vv)[16], uint32_t want) __attribute__((always_inline)) {
+      count8(vv, want & 0xffu);
+      count8(vv + 8, want >> 8);
     };
     if (vec) {
       for (int b4 = tid; b4 < V4 && !bad; b4 += 4 * NT) {
@@ -2072,12 +2075,27 @@ __device__ GroupOut grouped_row(const GenericArgs& a, int row, const RowParams& 
   if (tid < kWave) {
     const GroupDraw dr = group_cut_draw(ge, gc, G, s_held == (unsigned long long)V, a.V,
                                         P.topp_active != 0, P.topP, P.minp_active != 0, P.minP32, u);
+    // the drawn group: the first g with gc[0] + ... + gc[g] > pos, 64 groups
+    // per step
+    int g = 0;
+    int64_t pos = dr.pos;
+    if (dr.status == kGroupOk) {
+      for (int base = 0; base < G; base += kWave) {
+        const int c = base + lane < G ? (int)gc[base + lane] : 0;
+        const int incl = wave_incl_scan(c);
+        const int tot = __shfl(incl, kWave - 1, kWave);
+        if (pos < (int64_t)tot || base + kWave >= G) {
+          const uint64_t past = __ballot((int64_t)incl > pos);
+          const int hl = past ? __ffsll((unsigned long long)past) - 1 : min(G - base, kWave) - 1;
+          g = base + hl;
+          pos -= (int64_t)(__shfl(incl, hl, kWave) - __shfl(c, hl, kWave));
+          break;
+        }
+        pos -= tot;
+      }
+    }
     if (tid == 0) {
       s_draw = dr;
-      int64_t pos = dr.pos;
-      int g = 0;
-      if (dr.status == kGroupOk)
-        while (g < G - 1 && pos >= (int64_t)gc[g]) pos -= gc[g++];
       s_g = g;
       s_t = pos;
     }
