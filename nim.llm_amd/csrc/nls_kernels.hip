@@ -1795,7 +1795,7 @@ struct GroupOut {
 };
 
 template <int NT>
-__device__ GroupOut grouped_row(const GenericArgs& a, int row, const RowParams& P, double u,
+__device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, const RowParams& P, double u,
                                 const GroupLds& L, int* smem) {
   constexpr int NW = NT / kWave;
   const int tid = threadIdx.x;
