@@ -245,9 +245,12 @@ Geometry plan_geometry(int B, int64_t V, int kmax, int ncu, int max_patch) {
   }
   // 256-thread workgroups, >= 4 per CU: rows are split into S slices until the
   // grid holds about 4 workgroups per CU, keeping >= 2 tiles per slice.
-  // a whole row per 1024-thread workgroup once the batch fills the chip;
-  // smaller batches split rows over 256-thread workgroups
-  g.nt = env_int("NLS_STREAM_NT", B >= ncu ? 1024 : 256) == 1024 ? 1024 : 256;
+  // a whole row per 1024-thread workgroup once the batch fills the chip, or
+  // when a row is small enough that one workgroup streams it faster than the
+  // slices of a split row exchange their candidates (V = 32000, B = 1: 18.9
+  // against 23.9 us per call); otherwise rows are split over 256-thread
+  // workgroups
+  g.nt = env_int("NLS_STREAM_NT", (B >= ncu || V <= kSmallRowV) ? 1024 : 256) == 1024 ? 1024 : 256;
   const int64_t te = (int64_t)g.nt * kStreamVec4 * 4;
   const int want = g.nt == 1024 ? 1 : std::max(1, (4 * ncu + B - 1) / B);
   g.S = std::max(1, env_int("NLS_STREAM_S", want));

@@ -51,6 +51,7 @@ constexpr int kMaxSlices = 64;
 constexpr int kWaveCap = 256;        // per-wave candidate buffer of the k <= 64 path
 constexpr int kWaveTopK = 64;        // largest k of the wave path
 constexpr size_t kDualStreamLds = 68 * 1024;  // dynamic LDS of a 512-thread workgroup, two per CU
+constexpr int64_t kSmallRowV = 49152;  // rows up to this size stream in one workgroup
 
 // Slice-exchange record of one (row, slice) when a row is split over S
 // workgroups.
