@@ -1803,7 +1803,8 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   const int V = (int)a.V;
   const int nw = (V + 31) >> 5;
   const float* __restrict__ src = a.logits + (int64_t)row * a.V;
-  __shared__ int s_fail, s_distinct, s_G, s_id;
+  __shared__ int s_fail, s_distinct, s_G, s_id, s_found;
+  __shared__ int64_t s_left;
   __shared__ unsigned long long s_held;
   __shared__ uint32_t s_wmax[NW];
   __shared__ int s_wnan[NW];
@@ -2159,46 +2160,64 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     }
     return m;
   };
-  for (int b0 = wv; b0 < nblk; b0 += 4 * NW) {
-    int m[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) m[u] = (b0 + u * NW < nblk) ? lane_count(b0 + u * NW) : 0;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = wave_sum_i(m[u]);
-      if (lane == 0 && b0 + u * NW < nblk) bcnt[b0 + u * NW] = (uint32_t)c;
-    }
-  }
+  // The row is counted in rounds of 4 * NW blocks, in index order, and the
+  // walk stops at the round holding the t-th member (on average half the row
+  // is read).  The patched members go in first.
+  for (int i = tid; i < nblk; i += NT) bcnt[i] = 0u;
   __syncthreads();
   for (int sl = tid; sl < np; sl += NT)
     if (L.pfin[sl] == vg) atomicAdd(&bcnt[L.pid[sl] / (kWave * W)], 1u);
-  __syncthreads();
-  if (wv == 0) {
-    int64_t left = t;
-    for (int base = 0; base < nblk; base += kWave) {
-      const int c = (base + lane < nblk) ? (int)bcnt[base + lane] : 0;
-      const int incl = wave_incl_scan(c);
-      const int sum = __shfl(incl, kWave - 1, kWave);
-      if (left < sum) {
-        // the block: the first lane whose inclusive count passes `left`
-        const uint64_t past = __ballot((int64_t)incl > left);
-        const int bl = __ffsll((unsigned long long)past) - 1;
-        const int bk = base + bl;
-        const int64_t within = left - (__shfl(incl, bl, kWave) - __shfl(c, bl, kWave));
-        const uint32_t m = lane_members(bk);
-        const int mc = __popc(m);
-        const int mi = wave_incl_scan(mc);
-        if ((int64_t)(mi - mc) <= within && within < (int64_t)mi) {
-          uint32_t mm = m;
-          for (int r = (int)(within - (mi - mc)); r > 0; --r) mm &= mm - 1u;
-          s_id = (bk * kWave + lane) * W + (__ffs(mm) - 1);
-        }
-        break;
-      }
-      left -= sum;
-    }
+  if (tid == 0) {
+    s_left = t;
+    s_found = 0;
   }
   __syncthreads();
+  constexpr int RB = 4 * NW;
+  for (int r0 = 0; r0 < nblk; r0 += RB) {
+    int m[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int bk = r0 + wv + u * NW;
+      m[u] = bk < nblk ? lane_count(bk) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int bk = r0 + wv + u * NW;
+      const int c = wave_sum_i(m[u]);
+      if (lane == 0 && bk < nblk) bcnt[bk] += (uint32_t)c;
+    }
+    __syncthreads();
+    if (wv == 0) {
+      int64_t left = s_left;
+      const int rend = min(r0 + RB, nblk);
+      for (int base = r0; base < rend; base += kWave) {
+        const int c = (base + lane < rend) ? (int)bcnt[base + lane] : 0;
+        const int incl = wave_incl_scan(c);
+        const int sum = __shfl(incl, kWave - 1, kWave);
+        if (left < sum) {
+          // the block: the first lane whose inclusive count passes `left`
+          const uint64_t past = __ballot((int64_t)incl > left);
+          const int bl = __ffsll((unsigned long long)past) - 1;
+          const int bk = base + bl;
+          const int64_t within = left - (__shfl(incl, bl, kWave) - __shfl(c, bl, kWave));
+          const uint32_t mb = lane_members(bk);
+          const int mc = __popc(mb);
+          const int mi = wave_incl_scan(mc);
+          if ((int64_t)(mi - mc) <= within && within < (int64_t)mi) {
+            uint32_t mm = mb;
+            for (int r = (int)(within - (mi - mc)); r > 0; --r) mm &= mm - 1u;
+            s_id = (bk * kWave + lane) * W + (__ffs(mm) - 1);
+          }
+          if (lane == 0) s_found = 1;
+          break;
+        }
+        left -= sum;
+      }
+      if (lane == 0) s_left = left;
+    }
+    __syncthreads();
+    if (s_found) break;
+  }
   if (s_id < 0) return res;
   res.ok = 1;
   res.id = s_id;
