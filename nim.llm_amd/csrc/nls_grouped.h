@@ -21,6 +21,9 @@
 #include <stdint.h>
 
 #include "nls_runs.h"
+#if defined(__HIP_DEVICE_COMPILE__)
+#include "nls_primitives.h"  // wave_incl_scan
+#endif
 
 namespace nls {
 
@@ -73,17 +76,12 @@ NLS_RD bool skip_stays(double A, double P, int32_t q, int32_t fl, float fr, bool
   return A - P + q - fl - (fr > 0.0f ? 1 : 0) >= 0x1p23;
 }
 
-#if defined(__HIP_DEVICE_COMPILE__)
-__device__ __forceinline__ double skip_scan(double v) {
-  const int lane = (int)(threadIdx.x & (kSkipLanes - 1));
-#pragma unroll
-  for (int o = 1; o < kSkipLanes; o <<= 1) {
-    const double t = __shfl_up(v, o, kSkipLanes);
-    if (lane >= o) v += t;  // integers below 2^53: exact
-  }
-  return v;
-}
-#endif
+// On the device the window's step totals are 32-bit integers: a group's c * q
+// is clamped to 2^25 - 1, so the 64 lanes' sum stays below 2^31.  A group
+// whose c * q reaches the clamp fails its stay test whatever the value (its
+// run alone spans at least 2^24 spacings), so only groups after the stopping
+// one ever see a clamped total.
+constexpr int32_t kSkipClamp = (1 << 25) - 1;
 
 template <bool SUB>
 NLS_RD int group_skip(float& acc, const float* y, const uint32_t* c, int g, int gend, bool has_target,
@@ -108,14 +106,15 @@ NLS_RD int group_skip(float& acc, const float* y, const uint32_t* c, int g, int 
       int32_t q = 0, fl = 0;
       float fr = 0.0f;
       bool ok = valid && skip_setup(yh, k, q, fl, fr);
-      const double P = skip_scan(ok ? (double)ch * (double)q : 0.0);
-      const double Sc = skip_scan((double)ch);
-      if (ok) ok = skip_stays<SUB>(A, P, q, fl, fr, has_target, target, U) && S + Sc <= (double)cap;
+      const int64_t cq = ok ? (int64_t)ch * q : 0;
+      const int32_t P = wave_incl_scan((int32_t)(cq < kSkipClamp ? cq : kSkipClamp));
+      const int32_t Sc = wave_incl_scan((int32_t)ch);  // a row's counts: below 2^31
+      if (ok) ok = skip_stays<SUB>(A, (double)P, q, fl, fr, has_target, target, U) && S + Sc <= (double)cap;
       const uint64_t bad = __ballot(valid && !ok);
       if (bad) m = __ffsll((unsigned long long)bad) - 1;
       if (m > 0) {
-        Pm = __shfl(P, m - 1, kSkipLanes);
-        Sm = __shfl(Sc, m - 1, kSkipLanes);
+        Pm = (double)__shfl(P, m - 1, kSkipLanes);
+        Sm = (double)__shfl(Sc, m - 1, kSkipLanes);
       }
     }
 #else
