@@ -11,9 +11,15 @@
 //      completes a row (the only one when S == 1) selects the heap-path
 //      members in reference order (:85-95), then runs softmax (:98-100),
 //      top-p (:103-108), min-p (:110-114) and the draw (:115-121).
-//   2. generic_kernel  whole-row stable radix sort for full-sort rows
-//      (:96-97) and for rows the streaming kernel hands on (candidate or
-//      patch overflow).
+//      Workgroups: one 1024-thread workgroup per row when the batch fills
+//      the chip or the row is small; two 512-thread workgroups per CU for
+//      large batches of top-k rows with k > 64; otherwise rows split over
+//      256-thread slices.
+//   2. generic_kernel  full-sort rows (:96-97) and rows the streaming kernel
+//      hands on (candidate or patch overflow, a speculative threshold that
+//      admitted fewer than k): the row's distinct values with their
+//      multiplicities and the exact run closed forms of the sequential fp32
+//      chains (grouped_row), or else a whole-row stable radix sort.
 //
 // All fp32/fp64 arithmetic follows the reference's order; this file is built
 // with -ffp-contract=off so no multiply-add is fused.
