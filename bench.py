@@ -168,6 +168,70 @@ def bench_top_tokens(args):
     print(json.dumps(res), flush=True)
 
 
+def bench_row_nll(args):
+    """perplexity's per-position term (model.nim:578-583) on the workload's
+    logits, one random target id per row.  One line of JSON like the
+    sampler's, for this entry point."""
+    import numpy as np
+    import torch
+
+    pkg = load_pkg()
+    from nimllm_amd import workloads
+
+    w = workloads.make(args.workload, seed=args.seed)
+    B, V = w.B, w.V
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    nbuf = max(2, math.ceil(640e6 / (B * V * 4)))
+    base = torch.from_numpy(w.logits).to(dev)
+    bufs = [base] + [base.clone() for _ in range(nbuf - 1)]
+    rng = np.random.default_rng(args.seed)
+    tgt = torch.from_numpy(rng.integers(0, V, size=B).astype(np.int32)).to(dev)
+    out = pkg.row_nll_device(bufs[0], tgt).cpu().numpy()
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    ok = True
+    for r in (0, B // 2, B - 1):
+        ref = O.row_nll(w.logits[r], int(tgt[r]))
+        ok &= bool(abs(out[r] - ref) <= 1e-12 * max(1.0, abs(ref)))
+    for i in range(args.warmup):
+        pkg.row_nll_device(bufs[i % nbuf], tgt)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.steps):
+        pkg.row_nll_device(bufs[i % nbuf], tgt)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = float(B * V * 4 + B * 12)  # logits once, the target and the float64 result
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    res = {"metric": f"perplexity terms (rows/sec) at B={B} x V={V} fp32", "value": B / (ms * 1e-3),
+           "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f32 logits, f64 sum", "data": "synthetic (the sampler workload's logits, rotated over "
+                                                   f"{nbuf} buffers; random targets)",
+           "config": {"workload": f"{args.workload} logits, row_nll", "B": B, "V": V},
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "row_nll_kernel",
+                        "kernel_avg_us": ms * 1e3, "algorithmic_bytes_per_launch": nbytes},
+           "parity_spot_check": {"rows": 3, "within_1e-12": ok}}
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        done = 0
+        while time.perf_counter() - t0 < args.cpu_budget:
+            O.row_nll(w.logits[done % B], int(tgt[done % B]))
+            done += 1
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": done / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+                               "sample": f"{done} rows on one thread for {dt:.1f} s; C restatement of "
+                                         "src/nimllm/model.nim:578-583 (-O2 -ffp-contract=off, libm exp/log)"}
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -183,6 +247,8 @@ def main():
     ap.add_argument("--top-tokens", action="store_true",
                     help="time topTokens (n = --top-n per row) on the workload's logits instead")
     ap.add_argument("--top-n", type=int, default=5)
+    ap.add_argument("--row-nll", action="store_true",
+                    help="time perplexity's per-position term (one target per row) on the workload's logits")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (rows shard across GPUs with no "
@@ -191,6 +257,8 @@ def main():
 
     if args.top_tokens:
         return bench_top_tokens(args)
+    if args.row_nll:
+        return bench_row_nll(args)
     import numpy as np
     import torch
 

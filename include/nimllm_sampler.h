@@ -151,6 +151,17 @@ int nls_set_rng_state(nls_sampler* s, int32_t row, uint64_t a0, uint64_t a1);
 int nls_top_tokens(const float* d_logits, int32_t rows, int64_t vocab, int32_t n, int32_t* d_ids,
                    float* d_probs, void* stream);
 
+/* perplexity's per-position term (src/nimllm/model.nim:578-583): for each of
+ * `rows` rows of d_logits [rows x vocab] (device, row-major) and its target id
+ * d_targets[r] in [0, vocab), d_out[r] = -(float64(l[t] - mx) - ln(s)), with mx
+ * the float32 maximum of the row (NaN entries skipped, as Nim's max keeps mx)
+ * and s the float64 sum of exp(float64(l - mx)), the subtraction in float32.
+ * The sum runs in a fixed tree order on the device, not the reference's index
+ * order, so d_out matches the reference within rounding (relative 1e-12), not
+ * bit for bit.  Asynchronous on `stream`; targets outside [0, vocab) give NaN. */
+int nls_row_nll(const float* d_logits, int32_t rows, int64_t vocab, const int32_t* d_targets,
+                double* d_out, void* stream);
+
 /* Correctly rounded exp on fp32 inputs, on the device: d_out[i] = exp(d_in[i]). */
 int nls_expf_device(const float* d_in, float* d_out, int64_t n, void* stream);
 

@@ -30,7 +30,8 @@ EXPORTED = (
     "nls_set_stream", "nls_batch", "nls_vocab", "nls_accept", "nls_accept_row",
     "nls_accept_device", "nls_clear_history", "nls_sample", "nls_sample_host",
     "nls_synchronize", "nls_rng_uniforms", "nls_get_rng_state", "nls_set_rng_state",
-    "nls_top_tokens", "nls_expf_device", "nls_profile_next", "nls_status_string", "nls_last_error",
+    "nls_top_tokens", "nls_row_nll", "nls_expf_device", "nls_profile_next", "nls_status_string",
+    "nls_last_error",
 )
 
 
@@ -99,6 +100,7 @@ def lib():
         L.nls_get_rng_state.argtypes = [vp, ctypes.c_int32, P(ctypes.c_uint64), P(ctypes.c_uint64)]
         L.nls_set_rng_state.argtypes = [vp, ctypes.c_int32, ctypes.c_uint64, ctypes.c_uint64]
         L.nls_top_tokens.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, vp, vp, vp]
+        L.nls_row_nll.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, vp, vp, vp]
         L.nls_expf_device.argtypes = [vp, vp, ctypes.c_int64, vp]
         L.nls_profile_next.argtypes = [vp, vp, vp]
         L.nls_status_string.argtypes = [ctypes.c_int]
@@ -359,6 +361,33 @@ def topTokens(logits, n: int = 5):
     x = x.reshape(1, -1).to(device="cuda", dtype=torch.float32).contiguous()
     ids, probs = top_tokens_device(x, n)
     return [(int(i), float(p)) for i, p in zip(ids[0].tolist(), probs[0].tolist())]
+
+
+def row_nll_device(logits, targets):
+    """perplexity's per-position term (src/nimllm/model.nim:578-583) for a
+    [rows, V] float32 device tensor and int32 target ids [rows]: float64
+    -(l[t] - max) + ln(sum of exp(l - max)) per row."""
+    import torch
+
+    x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    t = targets.to(device=x.device, dtype=torch.int32).contiguous()
+    rows, V = x.shape
+    assert t.numel() == rows
+    out = torch.empty(rows, dtype=torch.float64, device=x.device)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    check(lib().nls_row_nll(ctypes.c_void_p(x.data_ptr()), rows, V, ctypes.c_void_p(t.data_ptr()),
+                            ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream)), "nls_row_nll")
+    return out
+
+
+def perplexity(logits, targets):
+    """exp of the mean per-position term over the rows (model.nim:570-589,
+    for logits already evaluated), computed on the device."""
+    import math
+
+    nll = row_nll_device(logits, targets)
+    return math.exp(float(nll.sum().item()) / max(1, nll.numel()))
 
 
 def expf_device(x, out=None):

@@ -171,6 +171,8 @@ hipError_t launch_expf(const float* x, float* y, int64_t n, hipStream_t s);
 constexpr int kTopThreads = 1024;
 constexpr int kTopChunk = 4096;  // exponentials per chunk of the sequential sum
 constexpr int kTopMaxN = 2048;   // largest number of results per row (sorted in LDS)
+hipError_t launch_row_nll(const float* logits, int rows, int64_t V, const int32_t* targets, double* out,
+                          hipStream_t s);
 hipError_t launch_top_tokens(const float* logits, int rows, int64_t V, int n, int32_t* ids,
                              float* probs, hipStream_t s);
 hipError_t set_kernel_attributes();

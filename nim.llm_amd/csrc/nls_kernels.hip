@@ -2688,6 +2688,63 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // small helpers
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// 4. row_nll_kernel -- perplexity's per-position term (model.nim:578-583)
+// ---------------------------------------------------------------------------
+// One workgroup per row: the float32 maximum (Nim's max(mx, v) keeps mx for a
+// NaN v, as fmaxf does), then s = sum of exp(float64(l - mx)) in float64 --
+// each thread over its own elements in index order, then a fixed tree over
+// the threads -- and -(float64(l[t] - mx) - ln(s)).  The reference adds in
+// index order; the tree differs from it only by float64 rounding.
+template <int NT>
+__global__ __launch_bounds__(NT) void row_nll_kernel(const float* __restrict__ logits, int64_t V,
+                                                     const int32_t* __restrict__ targets,
+                                                     double* __restrict__ out) {
+  constexpr int NW = NT / kWave;
+  constexpr int U = 8;  // loads in flight per thread
+  __shared__ float s_mx[NW];
+  __shared__ double s_ps[NW];
+  const int row = (int)blockIdx.x;
+  const int tid = (int)threadIdx.x;
+  const int lane = lane_id();
+  const int wv = tid >> 6;
+  const float* __restrict__ x = logits + (int64_t)row * V;
+  const __amdgpu_buffer_rsrc_t xr = slice_rsrc(x, (int)V);  // V < 2^29 (checked by the host)
+  auto scan = [&](auto fn) __attribute__((always_inline)) {
+    for (int i0 = 0; i0 < (int)V; i0 += NT * U) {
+      float l[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * NT + tid;
+        l[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             xr, i < (int)V ? i * 4 : 0x7ffffff0, 0, 0));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) fn(l[u], i0 + u * NT + tid < (int)V);
+    }
+  };
+  float mx = -__builtin_inff();
+  scan([&](float l, bool in) { mx = in ? __builtin_fmaxf(mx, l) : mx; });
+  for (int o = kWave / 2; o > 0; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) s_mx[wv] = mx;
+  __syncthreads();
+  mx = s_mx[0];
+  for (int w = 1; w < NW; ++w) mx = __builtin_fmaxf(mx, s_mx[w]);
+  double ps = 0.0;
+  scan([&](float l, bool in) {
+    if (in) ps += exp((double)(l - mx));
+  });
+  for (int o = kWave / 2; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
+  if (lane == 0) s_ps[wv] = ps;
+  __syncthreads();
+  if (tid == 0) {
+    double s = s_ps[0];
+    for (int w = 1; w < NW; ++w) s += s_ps[w];
+    const int t = targets[row];
+    out[row] = (t >= 0 && (int64_t)t < V) ? -((double)(x[t] - mx) - log(s)) : __builtin_nan("");
+  }
+}
+
 __global__ void accept_host_kernel(const int32_t* __restrict__ ids, int B, int count,
                                    int32_t* __restrict__ hist, int64_t* __restrict__ hist_len,
                                    int hcap, int row_only) {
@@ -2830,6 +2887,12 @@ hipError_t launch_top_tokens(const float* logits, int rows, int64_t V, int n, in
                              float* probs, hipStream_t s) {
   hipLaunchKernelGGL(top_tokens_kernel<kTopThreads>, dim3(rows), dim3(kTopThreads), 0, s, logits, V, n,
                      ids, probs);
+  return hipGetLastError();
+}
+
+hipError_t launch_row_nll(const float* logits, int rows, int64_t V, const int32_t* targets, double* out,
+                          hipStream_t s) {
+  hipLaunchKernelGGL(row_nll_kernel<1024>, dim3(rows), dim3(1024), 0, s, logits, V, targets, out);
   return hipGetLastError();
 }
 

@@ -186,6 +186,19 @@ int64_t nlo_top_tokens(const float* logits, int64_t V, int64_t n, int expf_mode,
   return m;
 }
 
+/* perplexity's per-position term (src/nimllm/model.nim:578-583): the float32
+ * maximum of the row (Nim's max(mx, v) keeps mx when v is NaN), the float64
+ * sum in index order of exp(float64(l - mx)) (the subtraction in float32),
+ * and -(float64(l[target] - mx) - ln(s)). */
+double nlo_row_nll(const float* logits, int64_t V, int64_t target) {
+  float mx = -INFINITY;
+  for (int64_t k = 0; k < V; ++k)
+    if (mx <= logits[k]) mx = logits[k];
+  double s = 0.0;
+  for (int64_t k = 0; k < V; ++k) s += exp((double)(logits[k] - mx));
+  return -((double)(logits[target] - mx) - log(s));
+}
+
 /* ------------------------------------------------------------------------ */
 /* HeapQueue[(float32, int)] (sampler.nim:88-95): binary min-heap ordered by */
 /* Nim's lexicographic tuple `<`, which compares fields with `cmp`.          */

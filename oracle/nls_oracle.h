@@ -106,6 +106,8 @@ void nlo_softmax_inplace(float* x, int64_t n, int expf_mode);
 /* topTokens (sampler.nim:123-130); returns min(n, V) entries. */
 int64_t nlo_top_tokens(const float* logits, int64_t V, int64_t n, int expf_mode,
                        int64_t* ids, float* probs);
+/* perplexity's per-position negative log-likelihood (model.nim:578-583). */
+double nlo_row_nll(const float* logits, int64_t V, int64_t target);
 
 #ifdef __cplusplus
 }

@@ -102,6 +102,8 @@ def lib():
         L.nlo_top_tokens.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64,
                                      ctypes.c_int, P(ctypes.c_int64), P(ctypes.c_float)]
         L.nlo_top_tokens.restype = ctypes.c_int64
+        L.nlo_row_nll.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64]
+        L.nlo_row_nll.restype = ctypes.c_double
         _lib = L
     return _lib
 
@@ -174,3 +176,10 @@ def sample_batch(params_list, logits, hist=None, hlen=None, bias_ids=None, bias_
                        _ptr(nb64, ctypes.c_int64), _ptr(uu, ctypes.c_double), expf_mode,
                        _ptr(out, ctypes.c_int64), nthreads)
     return out
+
+
+def row_nll(x, target):
+    """perplexity's per-position term (src/nimllm/model.nim:578-583)."""
+    import numpy as np
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return lib().nlo_row_nll(x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(x), int(target))

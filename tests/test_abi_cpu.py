@@ -68,6 +68,10 @@ def test_error_paths_without_device(pkg):
     assert L.nls_top_tokens(None, -1, 10, 5, None, None, None) == 1
     assert L.nls_top_tokens(None, 1, 100000, 3000, None, None, None) == 1
     assert L.nls_top_tokens(None, 1, 100, 5, None, None, None) == 1
+    assert L.nls_row_nll(None, 0, 100, None, None, None) == 0      # no rows
+    assert L.nls_row_nll(None, -1, 100, None, None, None) == 1
+    assert L.nls_row_nll(None, 1, 0, None, None, None) == 2        # empty vocab
+    assert L.nls_row_nll(None, 1, 100, None, None, None) == 1      # null buffers
     assert L.nls_status_string(5) == b"no usable device"
     import torch
 

@@ -486,3 +486,35 @@ def test_top_tokens_parity(pkg, torch):
     assert pkg.topTokens(x, 5) == [(int(i), float(p)) for i, p in zip(wi, wp)]
     with pytest.raises(pkg.SamplerError):
         pkg.top_tokens_device(torch.zeros((1, 5000), device="cuda"), 2049)
+
+
+def test_row_nll_parity(pkg, torch):
+    """perplexity's per-position term (src/nimllm/model.nim:578-583) on the
+    device against the oracle's index-order float64 sum.  The device sums in a
+    fixed tree order, so the bar is float64 rounding: relative 1e-12."""
+    import math
+
+    rng = np.random.default_rng(99)
+    say("[row_nll] rows of 128256 and 32000")
+    for B, V, scale in ((64, 128256, 2.5), (8, 32000, 3.0), (5, 7, 1.0)):
+        x = (rng.standard_normal((B, V)) * scale).astype(np.float32)
+        x[0] = np.round(x[0] * 4.0) / 4.0                 # ties
+        if B > 2:
+            x[1, rng.choice(V, min(V, 5), replace=False)] = -np.inf  # banned ids
+            x[2, :] = 1.0                                  # flat row: ln(V)
+        t = rng.integers(0, V, size=B).astype(np.int32)
+        got = pkg.row_nll_device(torch.from_numpy(x).cuda(), torch.from_numpy(t)).cpu().numpy()
+        for b in range(B):
+            ref = O.row_nll(x[b], int(t[b]))
+            if not math.isfinite(ref):  # a banned target: +inf on both sides
+                assert got[b] == ref, (B, V, b, got[b], ref)
+                continue
+            assert abs(got[b] - ref) <= 1e-12 * max(1.0, abs(ref)), (B, V, b, got[b], ref)
+        if B > 2:
+            assert got[2] == math.log(V) or abs(got[2] - math.log(V)) <= 1e-15 * math.log(V)
+    # a NaN logit makes the term NaN (the sum takes exp(NaN)); a bad target too
+    x = rng.standard_normal((2, 1000)).astype(np.float32)
+    x[0, 10] = np.nan
+    t = np.array([3, 5000], np.int32)
+    got = pkg.row_nll_device(torch.from_numpy(x).cuda(), torch.from_numpy(t)).cpu().numpy()
+    assert math.isnan(got[0]) and math.isnan(got[1])

@@ -331,3 +331,35 @@ def test_top_tokens_oracle_pins():
             assert np.array_equal(pr.view(np.uint32), want_p.view(np.uint32))
     ids, _ = _oracle_top_tokens(col, 4)
     assert list(ids) == [3, 10, 400, 999]
+
+
+def test_row_nll_oracle_pins():
+    """perplexity's per-position term (src/nimllm/model.nim:578-583) in the
+    oracle, pinned by closed forms and a float64 library evaluation."""
+    import math
+
+    # all logits equal: s = V exactly, nll = ln(V)
+    for V in (1, 7, 1000, 32000):
+        assert O.row_nll(np.full(V, 2.5, np.float32), V // 2) == math.log(V)
+    # two values a > b with counts: nll of a = ln(ca + cb e^(b - a))
+    x = np.array([1.0, -2.0, 1.0, -2.0, -2.0], np.float32)
+    want = math.log(2.0 + 3.0 * math.exp(-3.0))
+    assert abs(O.row_nll(x, 0) - want) <= 1e-15 * want
+    assert abs(O.row_nll(x, 1) - (want + 3.0)) <= 1e-15 * (want + 3.0)
+    # random rows against a float64 evaluation of the same terms (numpy's
+    # exp and pairwise sum): equal to rounding
+    rng = np.random.default_rng(11)
+    for V in (10, 5000, 128256):
+        x = (rng.standard_normal(V) * 2.5).astype(np.float32)
+        t = int(rng.integers(0, V))
+        mx = np.float32(np.max(x))
+        d = (x - mx).astype(np.float32).astype(np.float64)
+        ref = -(float(d[t]) - math.log(float(np.sum(np.exp(d)))))
+        got = O.row_nll(x, t)
+        assert abs(got - ref) <= 1e-12 * max(1.0, abs(ref)), (V, got, ref)
+    # NaN: max skips it (Nim's max keeps mx), the sum does not: NaN
+    x = np.array([0.5, np.nan, 1.5], np.float32)
+    assert math.isnan(O.row_nll(x, 0))
+    # -inf entries add exp(-inf) = 0
+    x = np.array([0.0, -np.inf, 0.0], np.float32)
+    assert O.row_nll(x, 2) == math.log(2.0)
