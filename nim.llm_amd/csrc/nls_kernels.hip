@@ -26,6 +26,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "nls_exp64.h"
 #include "nls_expf.h"
 #include "nls_grouped.h"
 #include "nls_internal.h"
@@ -2691,11 +2692,13 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // 4. row_nll_kernel -- perplexity's per-position term (model.nim:578-583)
 // ---------------------------------------------------------------------------
-// One workgroup per row: the float32 maximum (Nim's max(mx, v) keeps mx for a
+// One workgroup per row, two passes over it (16-byte loads, 64 KB in flight
+// per workgroup): the float32 maximum (Nim's max(mx, v) keeps mx for a
 // NaN v, as fmaxf does), then s = sum of exp(float64(l - mx)) in float64 --
 // each thread over its own elements in index order, then a fixed tree over
 // the threads -- and -(float64(l[t] - mx) - ln(s)).  The reference adds in
-// index order; the tree differs from it only by float64 rounding.
+// index order; the tree differs from it only by float64 rounding.  The exp is
+// the table-driven one of nls_exp64.h (within a few ulps of the library's).
 template <int NT>
 __global__ __launch_bounds__(NT) void row_nll_kernel(const float* __restrict__ logits, int64_t V,
                                                      const int32_t* __restrict__ targets,
@@ -2704,13 +2707,39 @@ __global__ __launch_bounds__(NT) void row_nll_kernel(const float* __restrict__ l
   constexpr int U = 8;  // loads in flight per thread
   __shared__ float s_mx[NW];
   __shared__ double s_ps[NW];
+  __shared__ double s_t[kExp64Table];
   const int row = (int)blockIdx.x;
   const int tid = (int)threadIdx.x;
   const int lane = lane_id();
   const int wv = tid >> 6;
   const float* __restrict__ x = logits + (int64_t)row * V;
   const __amdgpu_buffer_rsrc_t xr = slice_rsrc(x, (int)V);  // V < 2^29 (checked by the host)
+  // fn(l, in) over the row: with 16-byte loads (V % 4 == 0, aligned rows),
+  // four per thread in flight (64 KB per workgroup); otherwise 4-byte loads,
+  // eight per thread.  Past the row the loads read 0 with in == false.
+  const bool vec = (V % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
   auto scan = [&](auto fn) __attribute__((always_inline)) {
+    if (vec) {
+      const int V4 = (int)(V >> 2);
+      for (int b = tid; b < V4; b += NT * 4) {
+        f32x4 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i4 = b + u * NT;
+          q[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               xr, i4 < V4 ? i4 * 16 : 0x7ffffff0, 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const bool in = b + u * NT < V4;
+          fn(q[u].x, in);
+          fn(q[u].y, in);
+          fn(q[u].z, in);
+          fn(q[u].w, in);
+        }
+      }
+      return;
+    }
     for (int i0 = 0; i0 < (int)V; i0 += NT * U) {
       float l[U];
 #pragma unroll
@@ -2723,6 +2752,7 @@ __global__ __launch_bounds__(NT) void row_nll_kernel(const float* __restrict__ l
       for (int u = 0; u < U; ++u) fn(l[u], i0 + u * NT + tid < (int)V);
     }
   };
+  if (tid < kExp64Table) s_t[tid] = exp64_table_entry(tid);
   float mx = -__builtin_inff();
   scan([&](float l, bool in) { mx = in ? __builtin_fmaxf(mx, l) : mx; });
   for (int o = kWave / 2; o > 0; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o));
@@ -2732,7 +2762,7 @@ __global__ __launch_bounds__(NT) void row_nll_kernel(const float* __restrict__ l
   for (int w = 1; w < NW; ++w) mx = __builtin_fmaxf(mx, s_mx[w]);
   double ps = 0.0;
   scan([&](float l, bool in) {
-    if (in) ps += exp((double)(l - mx));
+    if (in) ps += exp64((double)(l - mx), s_t);  // table-driven (nls_exp64.h)
   });
   for (int o = kWave / 2; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
   if (lane == 0) s_ps[wv] = ps;

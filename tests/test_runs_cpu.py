@@ -4,6 +4,8 @@ nls_grouped.h, which the gfx950 kernel compiles as device code).
 * tests/runs_check.cpp: the closed forms of a run of equal terms against the
   plain sequential fp32 loops, on random and constructed runs (ties to even,
   binade crossings, runs of millions of terms, targets on exact partial sums).
+* tests/exp64_check.cpp: the float64 exp of the row log-sum-exp
+  (nls_exp64.h) against the C library's exp on float32 arguments.
 * tests/grouped_check.cpp: the whole group walk -- softmax sum, top-p, min-p,
   total, draw, and the drawn member -- against the oracle's sort path
   (src/nimllm/sampler.nim:96-121) on rows with ties, wide and narrow ranges,
@@ -31,6 +33,14 @@ def built(tmp_path_factory):
     subprocess.run(["g++", *FLAGS, "-shared", "-fPIC", "-o", so,
                     os.path.join(HERE, "grouped_check.cpp")], check=True)
     return exe, so
+
+
+def test_exp64_matches_libm(tmp_path):
+    exe = str(tmp_path / "exp64_check")
+    subprocess.run(["g++", *FLAGS, "-o", exe, os.path.join(HERE, "exp64_check.cpp"), "-lm"], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "0 failures" in r.stdout
 
 
 def test_run_closed_forms_match_sequential_loops(built):
