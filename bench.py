@@ -7,11 +7,21 @@ exceed the 256 MB Infinity Cache, so every step reads its logits from HBM.
 
     python bench.py [--steps K] [--warmup W] [--workload headline] [--no-cpu-baseline]
 
-Prints one JSON line.  `roofline` is for the streaming kernel (stream_kernel,
-the single read of the logits, which runs the whole pipeline of greedy and
-top-k rows), timed with HIP events on the sampler's stream (around K back-to-back calls
-when a call is that one launch); `cpu_baseline` times the CPU restatement of the
-reference sampler (oracle/) on the host on a bounded sample of the same rows.
+Prints one JSON line.  `roofline` is for the dominant kernel of a call: the
+streaming kernel (stream_kernel: the single read of the logits, running the
+whole pipeline of greedy and top-k rows) or, when full-sort rows take longer,
+the whole-row kernel (generic_kernel).  Each kernel is charged with the
+algorithmic bytes of the rows it serves (`kernels` lists both) and timed with
+HIP events on the sampler's stream: around K back-to-back calls when a call is
+one launch, else around each kernel.  `traffic` comes from the committed
+rocprofv3 counter summary (profiles/traffic_<workload>.md) only when that
+summary was measured on these sources (a hash of nim.llm_amd/csrc and
+include/).  `cpu_baseline` times the CPU restatement of the reference sampler
+(oracle/) on one host core, `cpu_baseline_all_cores` on every core this process
+may use (at most 16), each on a bounded sample of the same rows.
+
+    python bench.py --traffic-summary --workload W --fetch-dir D1 --write-dir D2 --out F
+writes such a summary from two rocprofv3 --pmc runs (no GPU needed).
 """
 import argparse
 import importlib.util
@@ -39,19 +49,126 @@ def load_pkg():
     return mod
 
 
+SOURCE_GLOBS = ("nim.llm_amd/csrc/*.hip", "nim.llm_amd/csrc/*.h", "nim.llm_amd/csrc/*.cpp",
+                "nim.llm_amd/csrc/Makefile", "include/*.h")
+
+
+def source_hash():
+    """sha256 over the sources of the HIP library: a traffic profile is valid
+    only for the code it was measured on."""
+    import glob
+    import hashlib
+
+    h = hashlib.sha256()
+    for pat in SOURCE_GLOBS:
+        for f in sorted(glob.glob(os.path.join(ROOT, pat))):
+            h.update(os.path.relpath(f, ROOT).encode())
+            with open(f, "rb") as fh:
+                h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def traffic_path(workload):
+    return os.path.join(ROOT, "profiles", f"traffic_{workload}.md")
+
+
 def read_traffic(workload):
-    """HBM bytes per launch of the streaming kernel, from the committed
-    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)."""
-    path = os.path.join(ROOT, "profiles", f"stream_kernel_{workload}_traffic.md")
+    """{kernel: HBM bytes per launch} from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled), or ({}, reason) when the
+    summary is missing or was measured on other sources."""
+    path = traffic_path(workload)
     if not os.path.exists(path):
-        return None
+        return {}, "no traffic profile for this workload"
+    stamp, out = None, {}
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1])
-    return None
+        if line.startswith("source_hash:"):
+            stamp = line.split(":", 1)[1].strip()
+        elif line.startswith("traffic_bytes_per_launch "):
+            k, v = line[len("traffic_bytes_per_launch "):].split(":", 1)
+            out[k.strip()] = float(v)
+    if stamp != source_hash():
+        return {}, f"traffic profile measured on sources {stamp}, not these ({source_hash()})"
+    return out, None
 
 
-def cpu_baseline(w, budget_s=12.0):
+def _pmc_rows(d):
+    """(kernel name, counter name, value) of every dispatch in a rocprofv3
+    --pmc csv output directory."""
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            yield r.get("Kernel_Name", ""), r.get("Counter_Name", ""), float(r.get("Counter_Value", 0)), \
+                r.get("Dispatch_Id", "")
+
+
+def traffic_summary(args):
+    """Writes the per-kernel HBM traffic summary of a workload from two
+    rocprofv3 --pmc runs of this script (FETCH_SIZE, then WRITE_SIZE, both with
+    --copy-ref), scaled by the 256 MiB copy of known size in the same runs."""
+    from collections import defaultdict
+
+    per = {}
+    for counter, d in (("FETCH_SIZE", args.fetch_dir), ("WRITE_SIZE", args.write_dir)):
+        acc = defaultdict(dict)
+        for kern, cname, val, disp in _pmc_rows(d):
+            if cname != counter:
+                continue
+            acc[kern][disp] = acc[kern].get(disp, 0.0) + val
+        per[counter] = {k: (sum(v.values()) / len(v), len(v), max(v.values())) for k, v in acc.items()}
+    copy_bytes = 64 * 1024 * 1024 * 4
+    copy = [k for k in per["FETCH_SIZE"] if "copyBuffer" in k]
+    if not copy:
+        raise SystemExit("no copy kernel in the FETCH_SIZE run: run bench.py with --copy-ref")
+    ck = copy[0]
+    f_fac = copy_bytes / (per["FETCH_SIZE"][ck][2] * 1024)
+    w_fac = copy_bytes / (per["WRITE_SIZE"][ck][2] * 1024)
+    lines = [f"# HBM traffic per launch, workload {args.workload}", "",
+             "Two counter passes, each its own run (from the repository root on an MI355X):", "", "```",
+             f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE -f csv -d <fetch> "
+             f"-o pmc -- python3 <repo>/bench.py --workload {args.workload} --steps 10 --warmup 2 "
+             f"--no-cpu-baseline --copy-ref",
+             f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE -f csv -d <write> "
+             f"-o pmc -- python3 <repo>/bench.py --workload {args.workload} --steps 10 --warmup 2 "
+             f"--no-cpu-baseline --copy-ref",
+             f"python3 <repo>/bench.py --traffic-summary --workload {args.workload} --fetch-dir <fetch> "
+             f"--write-dir <write> --out <this file>", "```", "",
+             f"Scale factors from the largest `{ck}` dispatch (256 MiB read, 256 MiB written): "
+             f"FETCH_SIZE x {f_fac:.4f}, WRITE_SIZE x {w_fac:.4f}.", "",
+             "| Kernel | dispatches | FETCH_SIZE KiB/dispatch | WRITE_SIZE KiB/dispatch | HBM bytes/launch |",
+             "|---|---|---|---|---|"]
+    totals = {}
+    for k, (fv, n, _) in sorted(per["FETCH_SIZE"].items()):
+        if "copyBuffer" in k or "fillBuffer" in k:
+            continue
+        wv = per["WRITE_SIZE"].get(k, (0.0, 0, 0.0))[0]
+        b = fv * 1024 * f_fac + wv * 1024 * w_fac
+        short = k.split("(")[0].replace("void ", "").replace("nls::", "")
+        base = short.split("<")[0]
+        totals[base] = max(totals.get(base, 0.0), b)
+        lines.append(f"| `{short}` | {n} | {fv:.2f} | {wv:.2f} | {b:.0f} |")
+    lines += ["", f"source_hash: {source_hash()}", f"commit: {args.commit or 'unknown'}"]
+    for base, b in sorted(totals.items()):
+        lines.append(f"traffic_bytes_per_launch {base}: {b:.0f}")
+    with open(args.out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def host_cores():
+    """Cores this process may use, capped at the 16 a one-GPU box grants."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_baseline(w, budget_s=12.0, nthreads=1):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle as O
@@ -62,13 +179,15 @@ def cpu_baseline(w, budget_s=12.0):
     hist = w.hist if w.hist.shape[1] else None
     rows_done = 0
     t0 = time.perf_counter()
-    chunk = max(1, min(w.B, 64))
+    # rows split in contiguous blocks over the threads: a chunk gives each
+    # thread several rows
+    chunk = max(1, min(w.B, 64)) if nthreads == 1 else max(nthreads, min(w.B, 8 * nthreads))
     start = 0
     while time.perf_counter() - t0 < budget_s:
         rows = np.arange(start, start + chunk) % w.B
         O.sample_batch([params[r] for r in rows], w.logits[rows],
                        None if hist is None else hist[rows], hl[rows], bid[rows], bval[rows],
-                       bcnt[rows], w.u[rows], O.EXPF_LIBM, nthreads=1)
+                       bcnt[rows], w.u[rows], O.EXPF_LIBM, nthreads=nthreads)
         rows_done += chunk
         start = (start + chunk) % w.B
     dt = time.perf_counter() - t0
@@ -81,9 +200,11 @@ def cpu_baseline(w, budget_s=12.0):
                 break
     except OSError:
         pass
-    return {"value": rows_done / dt, "unit": "rows/s", "cores": 1, "kind": "port",
-            "sample": f"{rows_done} rows of the same workload ({w.name}), rows run serially on "
-                      f"one thread for {dt:.1f} s; C restatement of src/nimllm/sampler.nim:59-121 "
+    how = ("rows run serially on one thread" if nthreads == 1 else
+           f"rows split over {nthreads} threads (POSIX threads, contiguous blocks of {chunk // nthreads}+ rows)")
+    return {"value": rows_done / dt, "unit": "rows/s", "cores": nthreads, "kind": "port",
+            "sample": f"{rows_done} rows of the same workload ({w.name}), {how} for {dt:.1f} s; "
+                      f"C restatement of src/nimllm/sampler.nim:59-121 "
                       f"(-O2 -ffp-contract=off, libm expf); CPU: {cpu}; "
                       f"{glibc[0]} {glibc[1]}"}
 
@@ -249,7 +370,16 @@ def main():
     ap.add_argument("--top-n", type=int, default=5)
     ap.add_argument("--row-nll", action="store_true",
                     help="time perplexity's per-position term (one target per row) on the workload's logits")
+    ap.add_argument("--traffic-summary", action="store_true",
+                    help="write the per-kernel traffic summary from two rocprofv3 --pmc runs "
+                         "(--fetch-dir, --write-dir) to --out; no GPU needed")
+    ap.add_argument("--fetch-dir")
+    ap.add_argument("--write-dir")
+    ap.add_argument("--out")
+    ap.add_argument("--commit", default="")
     args = ap.parse_args()
+    if args.traffic_summary:
+        return traffic_summary(args)
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (rows shard across GPUs with no "
               "collective; see DESIGN.md); --gpus must be 1", file=sys.stderr)
@@ -272,6 +402,7 @@ def main():
     s = pkg.BatchSampler(workloads.sampler_params(w, pkg), V, stream=stream)
     if w.hist.shape[1]:
         s.accept(w.hist)
+    plan, streamed = s.plan()
     row_bytes = B * V * 4
     nbuf = max(2, math.ceil(640e6 / row_bytes))
     base = torch.from_numpy(w.logits).to(dev)
@@ -307,32 +438,60 @@ def main():
     torch.cuda.synchronize()
     total_ms = t_all0.elapsed_time(t_all1)
     ms = total_ms / args.steps
-    # (2) HIP events recorded around the streaming kernel alone on the
-    # sampler's stream, one pair per call (each pair adds its own overhead)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
-    for a, b in ev:  # materialise the underlying hipEvents
-        a.record(stream)
-        b.record(stream)
+    # (2) HIP events recorded around each kernel of a call on the sampler's
+    # stream, one pair per kernel and call (each pair adds its own overhead)
+    def events():
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+        for a, b in ev:  # materialise the underlying hipEvents
+            a.record(stream)
+            b.record(stream)
+        return ev
+    ev_s = events()
+    ev_g = events() if plan.generic_launch else None
     torch.cuda.synchronize()
     for i in range(args.steps):
-        s.profile_next(ev[i][0], ev[i][1])
+        s.profile_next(ev_s[i][0], ev_s[i][1])
+        if ev_g:
+            s.profile_next_generic(ev_g[i][0], ev_g[i][1])
         s.sample(bufs[i % nbuf], du, out)
     torch.cuda.synchronize()
-    kern_ms = sorted(a.elapsed_time(b) for a, b in ev)
-    kern_avg_ms = sum(kern_ms) / len(kern_ms)
-    kern_med_ms = kern_ms[len(kern_ms) // 2]
-    pipe_bytes = w.algorithmic_bytes()
-    kern_bytes = float(pipe_bytes)  # the streaming kernel runs the whole pipeline of top-k/greedy rows
-    # When every row is greedy or top-k with k <= 2048, a call is one launch of
-    # the streaming kernel (rows it hands on are served by its last
-    # workgroup), so the kernel's average launch duration is the time of the
-    # K back-to-back calls of (1) over K; otherwise the event pairs of (2).
-    single = all(r.temperature <= 0 or 0 < r.topK < min(V, 2049) for r in w.rows)
-    launch_ms = ms if single else kern_avg_ms
-    achieved = kern_bytes / (launch_ms * 1e-3) / 1e9
+
+    def stats(ev):
+        t = sorted(a.elapsed_time(b) for a, b in ev)
+        return sum(t) / len(t), t[len(t) // 2]
+
+    # Algorithmic bytes per kernel: the streaming kernel reads the rows it
+    # runs to the end, plus the first unit a workgroup of every other row
+    # requests before it leaves; the whole-row kernel reads those other rows.
+    per_row = w.row_bytes()
+    stream_bytes = float(sum(per_row[b] if streamed[b] else min(plan.first_unit_bytes, 4 * V)
+                             for b in range(B)))
+    generic_bytes = float(sum(per_row[b] for b in range(B) if not streamed[b]))
+    pipe_bytes = float(sum(per_row))
+    s_avg, s_med = stats(ev_s)
+    kernels = {"stream_kernel": {"rows": int(sum(streamed)), "algorithmic_bytes_per_launch": stream_bytes,
+                                 "event_pair_avg_us": s_avg * 1e3, "event_pair_median_us": s_med * 1e3}}
+    if ev_g:
+        g_avg, g_med = stats(ev_g)
+        kernels["generic_kernel"] = {"rows": int(B - sum(streamed)), "algorithmic_bytes_per_launch": generic_bytes,
+                                     "event_pair_avg_us": g_avg * 1e3, "event_pair_median_us": g_med * 1e3}
+    # When a call is one launch (no full-sort rows: rows the streaming kernel
+    # hands on are served by its last workgroup) the kernel's average launch
+    # duration is the time of the K back-to-back calls of (1) over K; otherwise
+    # the event pairs of (2).
+    single = not plan.generic_launch
+    for name, k in kernels.items():
+        k["avg_us"] = ms * 1e3 if single else k["event_pair_avg_us"]
+        k["avg_from"] = "back-to-back calls" if single else "event pairs"
+        k["achieved_GBs"] = k["algorithmic_bytes_per_launch"] / (k["avg_us"] * 1e-6) / 1e9
+        k["frac"] = k["achieved_GBs"] / HBM_PEAK_GBS
+    dom = max(kernels, key=lambda n: kernels[n]["avg_us"])
+    traffic, stale = read_traffic(args.workload)
+    for name, k in kernels.items():
+        k["traffic"] = traffic.get(name)
     rows_per_s = B / (ms * 1e-3)
-    traffic = read_traffic(args.workload)
+    dk = kernels[dom]
     res = {
         "metric": "sampled rows/sec at B=256 x V=128256 fp32; % of MI355X peak HBM GB/s",
         "value": rows_per_s,
@@ -352,17 +511,18 @@ def main():
                                "50 bias ids per row (5 at -inf); top-k 50, top-p 0.95, T 1.0"
                    if args.workload == "headline" else args.workload,
                    "B": B, "V": V, "seed": args.seed},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "stream_kernel", "kernel_avg_us": launch_ms * 1e3,
-                     "kernel_avg_from": "back-to-back calls" if single else "event pairs",
-                     "event_pair_avg_us": kern_avg_ms * 1e3, "event_pair_median_us": kern_med_ms * 1e3,
-                     "algorithmic_bytes_per_launch": kern_bytes},
+        "roofline": {"bound": "hbm", "achieved": dk["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dk["frac"], "traffic": dk["traffic"],
+                     "kernel": dom, "kernel_avg_us": dk["avg_us"], "kernel_avg_from": dk["avg_from"],
+                     "algorithmic_bytes_per_launch": dk["algorithmic_bytes_per_launch"]},
+        "kernels": kernels,
         "pipeline": {"algorithmic_bytes": pipe_bytes,
                      "achieved_GBs": pipe_bytes / (ms * 1e-3) / 1e9,
                      "frac": pipe_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
         "parity_spot_check": {"rows": int(len(chk)), "bit_exact": parity_ok},
     }
+    if stale:
+        res["roofline"]["traffic_note"] = stale
     s.close()
     if args.copy_ref:
         n = 64 * 1024 * 1024  # 64 Mi floats = 256 MiB read and 256 MiB written per copy
@@ -376,6 +536,7 @@ def main():
         del a, b
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, args.cpu_budget)
+        res["cpu_baseline_all_cores"] = cpu_baseline(w, args.cpu_budget, nthreads=host_cores())
     else:
         res["cpu_baseline"] = None
     print(json.dumps(res), flush=True)

@@ -100,16 +100,22 @@ int32_t nls_batch(const nls_sampler* s);
 int64_t nls_vocab(const nls_sampler* s);
 
 /*
- * accept (sampler.nim:41-43), batched.  Appends `count` ids to every row's
- * history: ids is host memory [batch x count], row-major.  Any int64 is
+ * accept (sampler.nim:41-43), batched.  Appends up to `count` ids to every
+ * row's history: ids is host memory [batch x count], row-major.  Any int64 is
  * accepted; ids outside [0, vocab) occupy a history slot and are skipped by
- * the penalties, as in the reference (:70).
+ * the penalties, as in the reference (:70).  The one exception is
+ * NLS_ACCEPT_SKIP, which appends nothing: a batched generation loop passes it
+ * for rows that accept nothing this step (the reference loop never accepts an
+ * end-of-generation id, src/nimllm/chat.nim:206-208).
  */
+#define NLS_ACCEPT_SKIP INT64_MIN
+#define NLS_ACCEPT_SKIP32 INT32_MIN /* the same for nls_accept_device's int32 ids */
 int nls_accept(nls_sampler* s, const int64_t* ids, int32_t count);
-/* accept for one row only. */
+/* accept for one row only (NLS_ACCEPT_SKIP entries append nothing). */
 int nls_accept_row(nls_sampler* s, int32_t row, const int64_t* ids, int32_t count);
 /* Appends one id per row straight from device memory (e.g. the previous
- * nls_sample output), without a host round trip.  d_ids: device [batch]. */
+ * nls_sample output), without a host round trip.  d_ids: device [batch];
+ * a row whose entry is NLS_ACCEPT_SKIP32 appends nothing. */
 int nls_accept_device(nls_sampler* s, const int32_t* d_ids);
 /* Drops every row's history (a fresh newSampler keeps none). */
 int nls_clear_history(nls_sampler* s);
@@ -170,6 +176,21 @@ int nls_expf_device(const float* d_in, float* d_out, int64_t n, void* stream);
  * immediately after its streaming kernel (the one full read of the logits), on
  * the handle's stream, then clears the hook.  Pass NULLs to clear it. */
 int nls_profile_next(nls_sampler* s, void* start_event, void* stop_event);
+/* The same around the next call's whole-row kernel (full-sort rows), when the
+ * call launches one. */
+int nls_profile_next_generic(nls_sampler* s, void* start_event, void* stop_event);
+
+/* Introspection (no counterpart in the reference): how nls_sample runs this
+ * handle's batch, for byte accounting in measurements. */
+typedef struct nls_plan {
+  int32_t stream_threads;  /* workgroup size of the streaming kernel             */
+  int32_t slices;          /* streaming workgroups per row                       */
+  int32_t generic_launch;  /* 1: a second kernel serves the full-sort rows       */
+  int32_t streamed_rows;   /* rows the streaming kernel runs to the end          */
+  int64_t first_unit_bytes;/* logits a non-streamed row's workgroup requests before it leaves */
+} nls_plan;
+/* row_streamed: NULL or host [batch], 1 where the streaming kernel runs the row. */
+int nls_get_plan(const nls_sampler* s, nls_plan* out, int32_t* row_streamed);
 
 const char* nls_status_string(int status);
 /* Last HIP error text seen by this thread ("" if none). */

@@ -24,14 +24,18 @@ LIB_PATH = os.path.join(HERE, "libnimllm_sampler.so")
 
 NLS_OK = 0
 PATH_GREEDY, PATH_TOPK, PATH_FULL, PATH_GENERIC = 1, 2, 3, 4
+# accept entries that append nothing (a row that ended this step):
+# NLS_ACCEPT_SKIP for host int64 ids, NLS_ACCEPT_SKIP32 for device int32 ids
+ACCEPT_SKIP = -(1 << 63)
+ACCEPT_SKIP32 = -(1 << 31)
 
 EXPORTED = (
     "nls_default_sampling", "nls_greedy_sampling", "nls_create", "nls_destroy",
     "nls_set_stream", "nls_batch", "nls_vocab", "nls_accept", "nls_accept_row",
     "nls_accept_device", "nls_clear_history", "nls_sample", "nls_sample_host",
     "nls_synchronize", "nls_rng_uniforms", "nls_get_rng_state", "nls_set_rng_state",
-    "nls_top_tokens", "nls_row_nll", "nls_expf_device", "nls_profile_next", "nls_status_string",
-    "nls_last_error",
+    "nls_top_tokens", "nls_row_nll", "nls_expf_device", "nls_profile_next",
+    "nls_profile_next_generic", "nls_get_plan", "nls_status_string", "nls_last_error",
 )
 
 
@@ -61,6 +65,16 @@ class NlsDebug(ctypes.Structure):
         ("total", ctypes.c_void_p),
         ("path", ctypes.c_void_p),
         ("cap", ctypes.c_int32),
+    ]
+
+
+class NlsPlan(ctypes.Structure):
+    _fields_ = [
+        ("stream_threads", ctypes.c_int32),
+        ("slices", ctypes.c_int32),
+        ("generic_launch", ctypes.c_int32),
+        ("streamed_rows", ctypes.c_int32),
+        ("first_unit_bytes", ctypes.c_int64),
     ]
 
 
@@ -103,6 +117,8 @@ def lib():
         L.nls_row_nll.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, vp, vp, vp]
         L.nls_expf_device.argtypes = [vp, vp, ctypes.c_int64, vp]
         L.nls_profile_next.argtypes = [vp, vp, vp]
+        L.nls_profile_next_generic.argtypes = [vp, vp, vp]
+        L.nls_get_plan.argtypes = [vp, P(NlsPlan), P(ctypes.c_int32)]
         L.nls_status_string.argtypes = [ctypes.c_int]
         L.nls_status_string.restype = ctypes.c_char_p
         L.nls_last_error.restype = ctypes.c_char_p
@@ -217,7 +233,7 @@ class BatchSampler:
 
     def accept(self, ids, row: Optional[int] = None):
         """accept (sampler.nim:41-43): one id per row ([B]) or [B, n] ids; or
-        ids for a single `row`."""
+        ids for a single `row`.  ACCEPT_SKIP entries append nothing."""
         import numpy as np
 
         a = np.ascontiguousarray(np.asarray(ids, dtype=np.int64))
@@ -232,6 +248,7 @@ class BatchSampler:
               "nls_accept")
 
     def accept_device(self, d_ids):
+        """One id per row from device int32 [B]; ACCEPT_SKIP32 appends nothing."""
         assert d_ids.dtype == self._torch.int32 and d_ids.is_cuda and d_ids.numel() == self.B
         check(lib().nls_accept_device(self._h, ctypes.c_void_p(d_ids.data_ptr())), "nls_accept_device")
 
@@ -285,6 +302,18 @@ class BatchSampler:
         (recorded on this sampler's stream)."""
         check(lib().nls_profile_next(self._h, ctypes.c_void_p(start_event.cuda_event),
                                      ctypes.c_void_p(stop_event.cuda_event)), "nls_profile_next")
+
+    def profile_next_generic(self, start_event, stop_event):
+        """Time the next sample()'s whole-row kernel (when it launches one)."""
+        check(lib().nls_profile_next_generic(self._h, ctypes.c_void_p(start_event.cuda_event),
+                                             ctypes.c_void_p(stop_event.cuda_event)), "nls_profile_next_generic")
+
+    def plan(self):
+        """(NlsPlan, per-row list: 1 where the streaming kernel runs the row)."""
+        p = NlsPlan()
+        rows = (ctypes.c_int32 * self.B)()
+        check(lib().nls_get_plan(self._h, ctypes.byref(p), rows), "nls_get_plan")
+        return p, list(rows)
 
     def synchronize(self):
         check(lib().nls_synchronize(self._h), "nls_synchronize")

@@ -101,7 +101,8 @@ struct nls_sampler {
   int bstride = 0;  // > 0: bias lists at a fixed stride (row b at b * bstride)
 
   std::vector<RowParams> h_rp;
-  std::vector<int64_t> h_len;     // accepted ids per row
+  std::vector<int64_t> h_len;     // accepted ids per row (an upper bound while !len_exact)
+  bool len_exact = true;          // false after nls_accept_device, whose rows may skip
   std::vector<int> need_window;   // repeat_last_n (>0) or -1 (whole history), 0 if unused
   int hcap = 0;
 
@@ -126,13 +127,15 @@ struct nls_sampler {
   int gen_inline = 0;
   uint32_t* gen_scratch = nullptr;
   int64_t gen_vpad = 0;
-  int32_t* stage_ids = nullptr;
+  int32_t* stage_ids = nullptr;  // staged ids, then one append count per staged row
   size_t stage_cap = 0;
   std::vector<int32_t> h_stage;
   float* tmp_logits = nullptr;
   int32_t* tmp_out = nullptr;
   hipEvent_t prof_start = nullptr;
   hipEvent_t prof_stop = nullptr;
+  hipEvent_t prof_gstart = nullptr;
+  hipEvent_t prof_gstop = nullptr;
 
   ~nls_sampler() {
     dfree(rp);
@@ -165,6 +168,13 @@ struct nls_sampler {
       need = std::max(need, w);
     }
     if (need <= hcap && hist) return NLS_OK;
+    if (hist && !len_exact) {
+      // rows that skipped a device accept: the device lengths are the true ones
+      NLS_HIP(hipMemcpyAsync(h_len.data(), hist_len, sizeof(int64_t) * B, hipMemcpyDeviceToHost, stream));
+      NLS_HIP(hipStreamSynchronize(stream));
+      len_exact = true;
+      return ensure_history(row, extra);
+    }
     int64_t ncap = std::max<int64_t>(hcap, 16);
     while (ncap < need) ncap *= 2;
     if (ncap > (1 << 24)) {
@@ -560,28 +570,41 @@ static int accept_impl(nls_sampler* s, int row, const int64_t* ids, int32_t coun
   if (row >= s->B) return NLS_ERR_INVALID_ARGUMENT;
   if (count == 0) return NLS_OK;
   const int rows = row >= 0 ? 1 : s->B;
-  int rc = s->ensure_history(row, count);
-  if (rc) return rc;
+  // Stage each row's appended ids (NLS_ACCEPT_SKIP entries dropped) at
+  // [r * count, ...), then the per-row counts after all rows.
   const size_t n = (size_t)rows * count;
-  s->h_stage.resize(n);
-  for (size_t i = 0; i < n; ++i) {
-    const int64_t id = ids[i];
-    s->h_stage[i] = (id >= 0 && id < s->V) ? (int32_t)id : -1;  // out of range: skipped later
+  s->h_stage.assign(n + rows, -1);
+  std::vector<int64_t> add(rows, 0);
+  for (int r = 0; r < rows; ++r) {
+    int c = 0;
+    for (int j = 0; j < count; ++j) {
+      const int64_t id = ids[(size_t)r * count + j];
+      if (id == NLS_ACCEPT_SKIP) continue;
+      s->h_stage[(size_t)r * count + c++] = (id >= 0 && id < s->V) ? (int32_t)id : -1;  // out of range: skipped later
+    }
+    s->h_stage[n + r] = c;
+    add[r] = c;
   }
-  if (n > s->stage_cap) {
+  int64_t most = 0;
+  for (int r = 0; r < rows; ++r) most = std::max(most, add[r]);
+  if (most == 0) return NLS_OK;
+  int rc = s->ensure_history(row, most);
+  if (rc) return rc;
+  if (n + rows > s->stage_cap) {
     dfree(s->stage_ids);
-    rc = dalloc(&s->stage_ids, n);
+    rc = dalloc(&s->stage_ids, n + rows);
     if (rc) return rc;
-    s->stage_cap = n;
+    s->stage_cap = n + rows;
   }
-  NLS_HIP(hipMemcpyAsync(s->stage_ids, s->h_stage.data(), n * 4, hipMemcpyHostToDevice, s->stream));
-  NLS_HIP(launch_accept_host(s->stage_ids, s->B, count, s->hist, s->hist_len, s->hcap, row,
-                             s->stream));
+  NLS_HIP(hipMemcpyAsync(s->stage_ids, s->h_stage.data(), (n + rows) * 4, hipMemcpyHostToDevice,
+                         s->stream));
+  NLS_HIP(launch_accept_host(s->stage_ids, s->stage_ids + n, s->B, count, s->hist, s->hist_len,
+                             s->hcap, row, s->stream));
   NLS_HIP(hipStreamSynchronize(s->stream));
   if (row >= 0)
-    s->h_len[row] += count;
+    s->h_len[row] += add[0];
   else
-    for (int b = 0; b < s->B; ++b) s->h_len[b] += count;
+    for (int b = 0; b < s->B; ++b) s->h_len[b] += add[b];
   return NLS_OK;
 }
 
@@ -599,13 +622,16 @@ int nls_accept_device(nls_sampler* s, const int32_t* d_ids) {
   int rc = s->ensure_history(-1, 1);
   if (rc) return rc;
   NLS_HIP(launch_accept_device(d_ids, s->B, s->V, s->hist, s->hist_len, s->hcap, s->stream));
+  // a row may skip (NLS_ACCEPT_SKIP32): the host lengths become upper bounds
   for (int b = 0; b < s->B; ++b) s->h_len[b] += 1;
+  s->len_exact = false;
   return NLS_OK;
 }
 
 int nls_clear_history(nls_sampler* s) {
   if (!s) return NLS_ERR_INVALID_ARGUMENT;
   std::fill(s->h_len.begin(), s->h_len.end(), 0);
+  s->len_exact = true;
   NLS_HIP(hipMemcpyAsync(s->hist_len, s->h_len.data(), sizeof(int64_t) * s->B,
                          hipMemcpyHostToDevice, s->stream));
   NLS_HIP(hipStreamSynchronize(s->stream));
@@ -685,9 +711,9 @@ int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t
   a.ga = ga;
   LaunchPlan lp = s->plan;
   lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
-  hipEvent_t e0 = s->prof_start, e1 = s->prof_stop;
-  s->prof_start = s->prof_stop = nullptr;
-  NLS_HIP(launch_sample(a, ga, lp, s->stream, e0, e1));
+  hipEvent_t e0 = s->prof_start, e1 = s->prof_stop, g0 = s->prof_gstart, g1 = s->prof_gstop;
+  s->prof_start = s->prof_stop = s->prof_gstart = s->prof_gstop = nullptr;
+  NLS_HIP(launch_sample(a, ga, lp, s->stream, e0, e1, g0, g1));
   s->parity ^= 1;
   return NLS_OK;
 }
@@ -696,6 +722,31 @@ int nls_profile_next(nls_sampler* s, void* start_event, void* stop_event) {
   if (!s || (!start_event) != (!stop_event)) return NLS_ERR_INVALID_ARGUMENT;
   s->prof_start = reinterpret_cast<hipEvent_t>(start_event);
   s->prof_stop = reinterpret_cast<hipEvent_t>(stop_event);
+  return NLS_OK;
+}
+
+int nls_profile_next_generic(nls_sampler* s, void* start_event, void* stop_event) {
+  if (!s || (!start_event) != (!stop_event)) return NLS_ERR_INVALID_ARGUMENT;
+  s->prof_gstart = reinterpret_cast<hipEvent_t>(start_event);
+  s->prof_gstop = reinterpret_cast<hipEvent_t>(stop_event);
+  return NLS_OK;
+}
+
+int nls_get_plan(const nls_sampler* s, nls_plan* out, int32_t* row_streamed) {
+  if (!s || !out) return NLS_ERR_INVALID_ARGUMENT;
+  std::memset(out, 0, sizeof *out);
+  out->stream_threads = s->plan.lds > 0 ? s->plan.nt : 0;
+  out->slices = s->S;
+  out->generic_launch = s->gen_inline ? 0 : 1;
+  // a workgroup requests its first unit (kStreamVec4 float4 per thread)
+  // before it reads the row's constants
+  out->first_unit_bytes =
+      s->plan.lds > 0 ? std::min<int64_t>((int64_t)s->S * s->plan.nt * kStreamVec4 * 16, s->V * 4) : 0;
+  for (int b = 0; b < s->B; ++b) {
+    const int f = s->h_rp[b].fast ? 1 : 0;
+    out->streamed_rows += f;
+    if (row_streamed) row_streamed[b] = f;
+  }
   return NLS_OK;
 }
 

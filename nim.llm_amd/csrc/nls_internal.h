@@ -161,9 +161,10 @@ struct LaunchPlan {
 };
 
 hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const LaunchPlan& lp,
-                         hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop);
-hipError_t launch_accept_host(const int32_t* d_ids, int B, int count, int32_t* hist,
-                              int64_t* hist_len, int hcap, int row_only, hipStream_t s);
+                         hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, hipEvent_t gev_start,
+                         hipEvent_t gev_stop);
+hipError_t launch_accept_host(const int32_t* d_ids, const int32_t* d_cnt, int B, int count,
+                              int32_t* hist, int64_t* hist_len, int hcap, int row_only, hipStream_t s);
 hipError_t launch_accept_device(const int32_t* d_ids, int B, int64_t V, int32_t* hist,
                                 int64_t* hist_len, int hcap, hipStream_t s);
 hipError_t launch_expf(const float* x, float* y, int64_t n, hipStream_t s);

@@ -90,18 +90,22 @@ class Workload:
                 ids[b, j], vals[b, j] = k, v
         return ids, vals, cnt
 
-    def algorithmic_bytes(self) -> int:
-        """Bytes a perfect implementation must move: logits read once, int32
-        history window, (int32 id + fp32 value) per bias entry, the float64
-        uniform and the int32 output id, per row."""
-        total = 0
+    def row_bytes(self) -> list:
+        """Bytes a perfect implementation must move for each row: logits read
+        once, int32 history window, (int32 id + fp32 value) per bias entry, the
+        float64 uniform and the int32 output id."""
+        out = []
         for b, r in enumerate(self.rows):
             h = self.hist.shape[1] if (r.repeatPenalty != 1.0 or r.presencePenalty != 0 or
                                        r.frequencyPenalty != 0) else 0
             if r.repeatLastN > 0:
                 h = min(h, r.repeatLastN)
-            total += 4 * self.V + 4 * h + 8 * len(r.logitBias or {}) + 8 + 4
-        return total
+            out.append(4 * self.V + 4 * h + 8 * len(r.logitBias or {}) + 8 + 4)
+        return out
+
+    def algorithmic_bytes(self) -> int:
+        """Bytes a perfect implementation must move, summed over the rows."""
+        return sum(self.row_bytes())
 
 
 def nim_uniforms(seed: int, n: int) -> np.ndarray:

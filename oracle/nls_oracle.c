@@ -460,6 +460,7 @@ typedef struct {
   const double* u;
   int expf_mode;
   int64_t* out;
+  nlo_result* res;
   int64_t r0, r1;
 } batch_job;
 
@@ -470,8 +471,8 @@ static void* batch_worker(void* arg) {
                            j->hist ? j->hist + r * j->H : NULL, j->hlen ? j->hlen[r] : 0,
                            j->bias_ids ? j->bias_ids + r * j->NB : NULL,
                            j->bias_vals ? j->bias_vals + r * j->NB : NULL,
-                           j->nb ? j->nb[r] : 0, j->u[r], j->expf_mode, NULL, NULL,
-                           NULL, NULL);
+                           j->nb ? j->nb[r] : 0, j->u[r], j->expf_mode,
+                           j->res ? &j->res[r] : NULL, NULL, NULL, NULL);
   }
   return NULL;
 }
@@ -481,6 +482,15 @@ void nlo_sample_batch(const nlo_params* p, const float* logits, int64_t B, int64
                       const int64_t* bias_ids, const double* bias_vals, int64_t NB,
                       const int64_t* nb, const double* u, int expf_mode,
                       int64_t* out_ids, int nthreads) {
+  nlo_sample_batch_res(p, logits, B, V, hist, H, hlen, bias_ids, bias_vals, NB, nb, u, expf_mode,
+                       out_ids, NULL, nthreads);
+}
+
+void nlo_sample_batch_res(const nlo_params* p, const float* logits, int64_t B, int64_t V,
+                          const int64_t* hist, int64_t H, const int64_t* hlen,
+                          const int64_t* bias_ids, const double* bias_vals, int64_t NB,
+                          const int64_t* nb, const double* u, int expf_mode,
+                          int64_t* out_ids, nlo_result* res, int nthreads) {
   if (nthreads < 1) nthreads = 1;
   if (nthreads > B) nthreads = (int)(B > 0 ? B : 1);
   batch_job* jobs = (batch_job*)calloc((size_t)nthreads, sizeof(batch_job));
@@ -500,6 +510,7 @@ void nlo_sample_batch(const nlo_params* p, const float* logits, int64_t B, int64
     j->u = u;
     j->expf_mode = expf_mode;
     j->out = out_ids;
+    j->res = res;
     j->r0 = B * t / nthreads;
     j->r1 = B * (t + 1) / nthreads;
   }

@@ -99,6 +99,15 @@ void nlo_sample_batch(const nlo_params* p, const float* logits, int64_t B, int64
                       const int64_t* nb, const double* u, int expf_mode,
                       int64_t* out_ids, int nthreads);
 
+/* nlo_sample_batch that also fills res[B] (NULL: skip) with every row's
+ * nlo_result: n, total and the distances of the draw, the top-p cutoff and
+ * the min-p cutoff from their boundaries (the exception classes). */
+void nlo_sample_batch_res(const nlo_params* p, const float* logits, int64_t B, int64_t V,
+                          const int64_t* hist, int64_t H, const int64_t* hlen,
+                          const int64_t* bias_ids, const double* bias_vals, int64_t NB,
+                          const int64_t* nb, const double* u, int expf_mode,
+                          int64_t* out_ids, nlo_result* res, int nthreads);
+
 /* argmax (sampler.nim:45-49): first index of the greatest value. */
 int64_t nlo_argmax(const float* x, int64_t n);
 /* softmaxInPlace (sampler.nim:51-57). */

@@ -96,6 +96,7 @@ def lib():
             P(ctypes.c_int64), P(ctypes.c_double), ctypes.c_int64, P(ctypes.c_int64),
             P(ctypes.c_double), ctypes.c_int, P(ctypes.c_int64), ctypes.c_int,
         ]
+        L.nlo_sample_batch_res.argtypes = L.nlo_sample_batch.argtypes[:-1] + [P(Result), ctypes.c_int]
         L.nlo_argmax.argtypes = [P(ctypes.c_float), ctypes.c_int64]
         L.nlo_argmax.restype = ctypes.c_int64
         L.nlo_softmax_inplace.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int]
@@ -155,8 +156,9 @@ def sample(params: Params, logits, history=(), bias=None, u=0.5,
 
 
 def sample_batch(params_list, logits, hist=None, hlen=None, bias_ids=None, bias_vals=None,
-                 nb=None, u=None, expf_mode=EXPF_LIBM, nthreads=1) -> np.ndarray:
-    """Rows [B, V] through the restated sampler on `nthreads` threads."""
+                 nb=None, u=None, expf_mode=EXPF_LIBM, nthreads=1, want_res=False):
+    """Rows [B, V] through the restated sampler on `nthreads` threads.  Returns
+    the ids, or (ids, list of Result) with want_res."""
     L = lib()
     x = np.ascontiguousarray(logits, dtype=np.float32)
     B, V = x.shape
@@ -170,12 +172,17 @@ def sample_batch(params_list, logits, hist=None, hlen=None, bias_ids=None, bias_
     nb64 = None if nb is None else np.ascontiguousarray(nb, dtype=np.int64)
     uu = np.ascontiguousarray(u, dtype=np.float64)
     out = np.zeros(B, dtype=np.int64)
-    L.nlo_sample_batch(parr, _ptr(x, ctypes.c_float), B, V,
-                       _ptr(hist64, ctypes.c_int64), H, _ptr(hlen64, ctypes.c_int64),
-                       _ptr(bid, ctypes.c_int64), _ptr(bv, ctypes.c_double), NB,
-                       _ptr(nb64, ctypes.c_int64), _ptr(uu, ctypes.c_double), expf_mode,
-                       _ptr(out, ctypes.c_int64), nthreads)
-    return out
+    args = (parr, _ptr(x, ctypes.c_float), B, V,
+            _ptr(hist64, ctypes.c_int64), H, _ptr(hlen64, ctypes.c_int64),
+            _ptr(bid, ctypes.c_int64), _ptr(bv, ctypes.c_double), NB,
+            _ptr(nb64, ctypes.c_int64), _ptr(uu, ctypes.c_double), expf_mode,
+            _ptr(out, ctypes.c_int64))
+    if not want_res:
+        L.nlo_sample_batch(*args, nthreads)
+        return out
+    res = (Result * max(B, 1))()
+    L.nlo_sample_batch_res(*args, res, nthreads)
+    return out, [res[i] for i in range(B)]
 
 
 def row_nll(x, target):

@@ -274,49 +274,97 @@ def test_golden_fixtures(pkg, torch):
             assert [int(v) for v in dbg["cand_probs"][0][:n].view(np.uint32)] == e["probs_bits"]
 
 
-WORKLOAD_ROWS = {
-    "single_32k": 1,
-    "zipf_minp_128k": 64,
-    "headline": 48,
-    "penalties_152k": 32,
-    "flat_topk1000": 32,
-    "mixed_ties_152k": 48,
-}
+WORKLOAD_NAMES = ["single_32k", "zipf_minp_128k", "headline", "penalties_152k", "flat_topk1000",
+                  "mixed_ties_152k"]
+# The north star's window: a row may differ from the reference (the oracle
+# with the C library's expf) only when one of its draws or cutoffs lies within
+# 1e-6 of a boundary: the draw (margin_draw, in units of the CDF), the top-p
+# running sum (margin_topp, absolute) or the min-p threshold (margin_minp,
+# relative to the threshold).
+EXC_WINDOW = 1e-6
 
 
-@pytest.mark.parametrize("name", list(WORKLOAD_ROWS))
+def exception_classes(res):
+    """SURVEY-style exception classes a row falls in, from an oracle Result."""
+    out = []
+    if res.greedy:
+        return out
+    if res.margin_draw < EXC_WINDOW:
+        out.append("E1_draw")
+    if res.margin_topp < EXC_WINDOW:
+        out.append("E2_topp")
+    if res.margin_minp < EXC_WINDOW:
+        out.append("E3_minp")
+    return out
+
+
+def write_report(name, record):
+    """Appends one JSON line per workload to $NLS_PARITY_REPORT when set."""
+    import json
+    import os
+
+    path = os.environ.get("NLS_PARITY_REPORT")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(dict(workload=name, **record)) + "\n")
+
+
+@pytest.mark.parametrize("name", WORKLOAD_NAMES)
 def test_workload_parity(pkg, torch, name):
+    """Every row of the workload at full size against the oracle, in both exp
+    modes.  Against the correctly rounded exp (the device's) ids, n and the
+    total are bit-exact on every row.  Against the C library's expf (what the
+    reference's exp(float32) calls) a row may differ only inside the north
+    star's 1e-6 window, which the libm oracle's own margins must show."""
     from nimllm_amd import workloads
 
     w = workloads.make(name, seed=7)
     say(f"[workload_parity] {name} B={w.B} V={w.V}")
     params = workloads.sampler_params(w, pkg)
     ids, dbg = run_gpu(pkg, torch, w.logits, params, w.hist, w.u, debug_cap=64)
-    # every id is a valid token
     assert ids.min() >= 0 and ids.max() < w.V
-    rows = np.linspace(0, w.B - 1, WORKLOAD_ROWS[name]).astype(int)
-    rows = sorted(set(int(r) for r in rows))
     bid, bval, bcnt = w.bias_arrays()
-    plist = [w.rows[r].as_kwargs() for r in rows]
-    sub_hist = w.hist[rows] if w.hist.shape[1] else np.zeros((len(rows), 0), dtype=np.int64)
-    oc = O.sample_batch([O.make_params(**p) for p in plist], w.logits[rows], sub_hist,
-                        np.full(len(rows), w.hist.shape[1]), bid[rows], bval[rows], bcnt[rows],
-                        w.u[rows], O.EXPF_CR, nthreads=8)
-    ol = O.sample_batch([O.make_params(**p) for p in plist], w.logits[rows], sub_hist,
-                        np.full(len(rows), w.hist.shape[1]), bid[rows], bval[rows], bcnt[rows],
-                        w.u[rows], O.EXPF_LIBM, nthreads=8)
-    got = ids[rows]
-    assert np.array_equal(got, oc), (name, np.nonzero(got != oc)[0][:10])
-    libm_exc = int(np.sum(oc != ol))
-    assert np.all((got == ol) | (oc != ol))
-    say(f"[workload_parity] {name}: {len(rows)} rows bit-exact; libm-exp exception rows: {libm_exc}")
-    paths = dbg["path"]
-    say(f"[workload_parity] {name}: paths {np.bincount(paths, minlength=5).tolist()}")
+    plist = [O.make_params(**r.as_kwargs()) for r in w.rows]
+    H = w.hist.shape[1]
+    hist = w.hist if H else None
+    hl = np.full(w.B, H)
+    oc, rc = O.sample_batch(plist, w.logits, hist, hl, bid, bval, bcnt, w.u, O.EXPF_CR,
+                            nthreads=8, want_res=True)
+    ol, rl = O.sample_batch(plist, w.logits, hist, hl, bid, bval, bcnt, w.u, O.EXPF_LIBM,
+                            nthreads=8, want_res=True)
+    say(f"[workload_parity] {name}: oracle done for {w.B} rows in both exp modes")
+    # (1) correctly rounded exp: every row bit-exact (id, n, total)
+    bad = np.nonzero(ids != oc)[0]
+    assert bad.size == 0, (name, bad[:10].tolist())
+    for b in range(w.B):
+        r = rc[b]
+        if r.greedy:
+            continue
+        assert int(dbg["n"][b]) == r.n, (name, b, int(dbg["n"][b]), r.n)
+        assert dbg["total"][b].view(np.uint32) == np.float32(r.total).view(np.uint32), (name, b)
+    # (2) the C library's expf: differing rows lie in the 1e-6 window
+    counts = {"E1_draw": 0, "E2_topp": 0, "E3_minp": 0}
+    for b in range(w.B):
+        for c in exception_classes(rl[b]):
+            counts[c] += 1
+    differ = np.nonzero(ids != ol)[0]
+    for b in differ:
+        cls = exception_classes(rl[b])
+        assert cls, (name, int(b), "differs from the libm-exp oracle outside the 1e-6 window",
+                     rl[b].margin_draw, rl[b].margin_topp, rl[b].margin_minp)
+    oracle_flips = int(np.sum(oc != ol))
+    paths = np.bincount(dbg["path"], minlength=5).tolist()
+    record = {"rows": int(w.B), "rows_bit_exact_cr_exp": int(w.B - bad.size),
+              "rows_differing_from_libm_exp": int(differ.size),
+              "rows_where_oracle_cr_and_libm_differ_E4": oracle_flips,
+              "rows_in_window": counts, "paths_greedy_topk_full_generic": paths[1:]}
+    write_report(name, record)
+    say(f"[workload_parity] {name}: {record}")
     # full-sort rows (k = 0) take the grouped sort path: their distinct values,
     # patched ids and cutoffs all fit its tables on these workloads
     full = np.array([r.temperature > 0 and not (0 < r.topK < w.V) for r in w.rows])
     if full.any():
-        assert np.all(paths[full] == 3), (name, np.bincount(paths[full], minlength=5).tolist())
+        assert np.all(dbg["path"][full] == 3), (name, np.bincount(dbg["path"][full], minlength=5).tolist())
 
 
 def test_device_rng_stream_and_greedy_rows_draw_nothing(pkg, torch):
@@ -379,6 +427,88 @@ def test_accept_loop_with_windows_and_growth(pkg, torch):
                 s.accept(out.astype(np.int64))
     finally:
         s.close()
+
+
+def test_batched_generate_loop_skips_end_of_generation(pkg, torch):
+    """A batched generation loop over B chats (src/nimllm/chat.nim:204-208):
+    every step each row samples with its own RNG stream; a row that draws an
+    end-of-generation id ends its turn and accepts nothing (ACCEPT_SKIP /
+    ACCEPT_SKIP32), and its next turn continues with the same history and RNG
+    (Chat.sampler persists across turns, chat.nim:266,401).  Checked step by
+    step against one oracle per row; histories outgrow the ring while the
+    device-side skips leave the host's lengths inexact."""
+    rng = np.random.default_rng(21)
+    V, B, steps = 3000, 6, 48
+    eog = (0, 1, 2)
+    say(f"[batched_generate] V={V} B={B} steps={steps} eog={eog}")
+    plist = [dict(temperature=0.8, topK=40, topP=0.95, minP=0.05, repeatPenalty=1.2,
+                  repeatLastN=[0, 8, 0, 24, 0, 0][b], presencePenalty=0.3, frequencyPenalty=0.5,
+                  seed=100 + b) for b in range(B)]
+    plist[2]["temperature"] = 0.0          # greedy: draws nothing
+    plist[4].update(topK=0, topP=0.9)      # full-sort path
+    plist[5].update(topK=500)              # block top-k path
+    s = pkg.BatchSampler([to_pkg_params(pkg, p, {}) for p in plist], V)
+    streams = [list(O.uniforms(plist[b]["seed"], steps)) for b in range(B)]
+    used = [0] * B
+    hist = [[] for _ in range(B)]
+    skipped = 0
+    try:
+        for t in range(steps):
+            x = rng.standard_normal((B, V)).astype(np.float32) * 2
+            # some rows are pushed towards an end-of-generation id this step
+            for b in range(B):
+                if rng.random() < 0.3:
+                    x[b, eog[int(rng.integers(0, len(eog)))]] += 12.0
+            d_out = s.sample(torch.from_numpy(x).cuda())
+            out = d_out.cpu().numpy()
+            for b in range(B):
+                greedy = plist[b]["temperature"] <= 0
+                u = 0.0 if greedy else streams[b][used[b]]
+                res, _, _, _ = oracle_row(x[b], plist[b], hist[b], {}, u, O.EXPF_CR)
+                assert out[b] == res.id, (t, b, int(out[b]), res.id)
+                if not greedy:
+                    used[b] += 1
+            ended = np.isin(out, eog)
+            skipped += int(ended.sum())
+            if t % 2 == 0:
+                d_acc = d_out.clone()
+                d_acc[torch.from_numpy(ended).cuda()] = pkg.ACCEPT_SKIP32
+                s.accept_device(d_acc)
+            else:
+                a = out.astype(np.int64)
+                a[ended] = pkg.ACCEPT_SKIP
+                s.accept(a)
+            for b in range(B):
+                if not ended[b]:
+                    hist[b].append(int(out[b]))
+        # RNG states advanced exactly once per non-greedy call
+        for b in range(B):
+            r = O.Rand()
+            O.lib().nlo_init_rand(O.ctypes.byref(r), plist[b]["seed"])
+            for _ in range(used[b]):
+                O.lib().nlo_rand_float(O.ctypes.byref(r), 1.0)
+            assert s.rng_state(b) == (r.a0, r.a1), b
+    finally:
+        s.close()
+    say(f"[batched_generate] {skipped} row-steps ended a turn and accepted nothing")
+    assert skipped > 0
+
+
+def test_nim_binding_call_sequence(pkg, torch):
+    """tests/nim_binding_check.c makes exactly the calls of the Nim binding in
+    INTEGRATION.md (create, set the RNG state from the Nim Rand, replay the
+    history, then sample_host / accept per step, skipping accept on an
+    end-of-generation id) and checks every id against the oracle."""
+    import os
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(__file__), "nim_binding_check.bin")
+    assert os.path.exists(exe), "build it first: python -c 'import __graft_entry__ as g; g.build()'"
+    say("[nim_binding] running tests/nim_binding_check.bin")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    say(r.stdout[-2000:])
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "nim binding sequence ok" in r.stdout
 
 
 def test_sample_host_and_single_row_sampler(pkg, torch):
