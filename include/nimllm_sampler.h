@@ -137,6 +137,17 @@ int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t
  * RNGs and returns the ids in h_out [batch]. */
 int nls_sample_host(nls_sampler* s, const float* h_logits, int64_t* h_out);
 
+/* No counterpart in the reference: nls_sample_host for callers that cannot
+ * allocate (a serving loop or harness that forbids hipMalloc after set-up).
+ * It allocates nothing, on the device or the host: the logits and ids are
+ * staged in a 16 MiB device array of the library (one per GPU, set up by
+ * nls_create on the device current there, held until the process ends), so
+ * batch x vocab x 4 bytes (+ 4 bytes per row) must fit 16 MiB, else
+ * NLS_ERR_UNSUPPORTED.  Same results as nls_sample_host.  Every call on one
+ * GPU shares that array: calls that overlap on one GPU (other threads, other
+ * handles' streams) race and must be serialised by the caller. */
+int nls_sample_host_noalloc(nls_sampler* s, const float* h_logits, int64_t* h_out);
+
 int nls_synchronize(nls_sampler* s);
 
 /* The first n values of rand(1.0) after initRand(seed) (Nim std/random). */

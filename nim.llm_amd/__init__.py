@@ -33,6 +33,7 @@ EXPORTED = (
     "nls_default_sampling", "nls_greedy_sampling", "nls_create", "nls_destroy",
     "nls_set_stream", "nls_batch", "nls_vocab", "nls_accept", "nls_accept_row",
     "nls_accept_device", "nls_clear_history", "nls_sample", "nls_sample_host",
+    "nls_sample_host_noalloc",
     "nls_synchronize", "nls_rng_uniforms", "nls_get_rng_state", "nls_set_rng_state",
     "nls_top_tokens", "nls_row_nll", "nls_expf_device", "nls_profile_next",
     "nls_profile_next_generic", "nls_get_plan", "nls_status_string", "nls_last_error",
@@ -109,6 +110,7 @@ def lib():
         L.nls_clear_history.argtypes = [vp]
         L.nls_sample.argtypes = [vp, vp, vp, vp, P(NlsDebug)]
         L.nls_sample_host.argtypes = [vp, P(ctypes.c_float), P(ctypes.c_int64)]
+        L.nls_sample_host_noalloc.argtypes = [vp, P(ctypes.c_float), P(ctypes.c_int64)]
         L.nls_synchronize.argtypes = [vp]
         L.nls_rng_uniforms.argtypes = [ctypes.c_int64, ctypes.c_int64, P(ctypes.c_double)]
         L.nls_get_rng_state.argtypes = [vp, ctypes.c_int32, P(ctypes.c_uint64), P(ctypes.c_uint64)]

@@ -12,6 +12,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <new>
 #include <random>
 #include <string>
@@ -78,6 +79,40 @@ double nim_rand_unit(NimRand& r) {
   return f - 1.0;
 }
 
+// Staging of nls_sample_host_noalloc: the logits, then the ids, of one call.
+// A file-scope device array, so that the entry point allocates nothing; every
+// GPU the library runs on holds its own copy (16 MiB) until the process ends.
+// In host code `scratch` names a host-side stand-in, never the device memory:
+// its device address is taken once per device (scratch_device) and only that
+// address is used.
+constexpr size_t kNoAllocBytes = size_t{16} << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on device `dev` (which must be current).
+int scratch_device(int dev, void** out) {
+  *out = nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    g_last_error = "device ordinal beyond the scratch table";
+    return NLS_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) {
+      g_last_error = "hipGetSymbolAddress(scratch) returned no address";
+      return NLS_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NLS_OK;
+}
+
 template <typename T>
 int dalloc(T** p, size_t n) {
   *p = nullptr;
@@ -96,6 +131,8 @@ void dfree(T*& p) {
 struct nls_sampler {
   int B = 0;
   int64_t V = 0;
+  int device = 0;        // the device current at nls_create
+  void* scratch = nullptr;  // that device's address of `scratch`
   hipStream_t stream = nullptr;
   int max_bias = 0;
   int bstride = 0;  // > 0: bias lists at a fixed stride (row b at b * bstride)
@@ -436,6 +473,15 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   // streaming geometry: the largest k whose buffers fit in LDS
   int dev = 0, ncu = 0;
   (void)hipGetDevice(&dev);
+  s->device = dev;
+  {
+    // the no-allocation entry point's staging on this device, set up here
+    const int rc0 = scratch_device(dev, &s->scratch);
+    if (rc0) {
+      delete s;
+      return rc0;
+    }
+  }
   if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 1)
     ncu = 256;
   int kfast = kmax;
@@ -763,6 +809,37 @@ int nls_sample_host(nls_sampler* s, const float* h_logits, int64_t* h_out) {
   NLS_HIP(hipMemcpyAsync(o.data(), s->tmp_out, (size_t)s->B * 4, hipMemcpyDeviceToHost, s->stream));
   NLS_HIP(hipStreamSynchronize(s->stream));
   for (int b = 0; b < s->B; ++b) h_out[b] = o[b];
+  return NLS_OK;
+}
+
+int nls_sample_host_noalloc(nls_sampler* s, const float* h_logits, int64_t* h_out) {
+  if (!s || !h_logits || !h_out) return NLS_ERR_INVALID_ARGUMENT;
+  const size_t n = (size_t)s->B * (size_t)s->V;
+  const size_t ids_off = (n * 4 + 255) & ~(size_t)255;
+  if (ids_off + (size_t)s->B * 4 > kNoAllocBytes) {
+    g_last_error = "nls_sample_host_noalloc: batch x vocab x 4 bytes (+ the ids) exceeds its " +
+                   std::to_string(kNoAllocBytes >> 20) + " MiB staging; use nls_sample_host";
+    return NLS_ERR_UNSUPPORTED;
+  }
+  if (!s->scratch) {
+    g_last_error = "nls_sample_host_noalloc: no staging address for the handle's device";
+    return NLS_ERR_HIP;
+  }
+  unsigned char* base = static_cast<unsigned char*>(s->scratch);
+  float* d_logits = reinterpret_cast<float*>(base);
+  int32_t* d_out = reinterpret_cast<int32_t*>(base + ids_off);
+  NLS_HIP(hipMemcpyAsync(d_logits, h_logits, n * 4, hipMemcpyHostToDevice, s->stream));
+  const int rc = nls_sample(s, d_logits, nullptr, d_out, nullptr);
+  if (rc) return rc;
+  // the int32 ids land in the first half of h_out and are widened in place,
+  // from the last one down (no host buffer either)
+  int32_t* narrow = reinterpret_cast<int32_t*>(h_out);
+  NLS_HIP(hipMemcpyAsync(narrow, d_out, (size_t)s->B * 4, hipMemcpyDeviceToHost, s->stream));
+  NLS_HIP(hipStreamSynchronize(s->stream));
+  for (int b = s->B - 1; b >= 0; --b) {
+    const int32_t v = narrow[b];
+    h_out[b] = v;
+  }
   return NLS_OK;
 }
 
