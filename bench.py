@@ -353,6 +353,104 @@ def bench_row_nll(args):
     print(json.dumps(res), flush=True)
 
 
+def phase_stamps(args):
+    """Per-phase wall-clock of the k64 kernel on the workload, from the
+    `phases` build of the library (make -C nim.llm_amd/csrc phases):
+    medians over the rows' workgroups of the time each phase took, for the
+    last of a run of back-to-back calls."""
+    import ctypes
+    import numpy as np
+    import torch
+
+    pkg = load_pkg()
+    path = os.path.join(PKG_DIR, "libnimllm_sampler_phases.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"{path} is missing: make -C nim.llm_amd/csrc phases")
+    pkg.LIB_PATH = path
+    L = pkg.lib()
+    from nimllm_amd import workloads
+
+    w = workloads.make(args.workload, seed=args.seed)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    s = pkg.BatchSampler(workloads.sampler_params(w, pkg), w.V, stream=stream)
+    if w.hist.shape[1]:
+        s.accept(w.hist)
+    nbuf = max(2, math.ceil(640e6 / (w.B * w.V * 4)))
+    base = torch.from_numpy(w.logits).to(dev)
+    bufs = [base] + [base.clone() for _ in range(nbuf - 1)]
+    du = torch.from_numpy(w.u).to(dev)
+    out = torch.empty(w.B, dtype=torch.int32, device=dev)
+    for i in range(args.steps):
+        s.sample(bufs[i % nbuf], du, out)
+    torch.cuda.synchronize()
+    buf = np.zeros(4096 * 16, dtype=np.uint64)
+    st = {}
+    for which in (0, 1, 2):
+        if L.nls_phase_stamps(which, buf.ctypes.data_as(ctypes.c_void_p)) != 0:
+            raise SystemExit("nls_phase_stamps failed")
+        st[which] = buf.reshape(4096, 16)[:w.B].astype(np.int64).copy()
+    s.close()
+    P, W, D = st[0], st[1], st[2]
+    us = lambda d: d / 100.0  # 100 MHz counter
+    t0 = P[:, 0].min()
+    wend = W.max(axis=1)
+    wfirst = W.min(axis=1)
+    rows = {
+        "workgroup start after the first": us(P[:, 0] - t0),
+        "row constants in": us(P[:, 1] - P[:, 0]),
+        "zero tables, barrier": us(P[:, 2] - P[:, 1]),
+        "patch bitmap + hash, barrier": us(P[:, 3] - P[:, 2]),
+        "bootstrap bound (2 barriers)": us(P[:, 4] - P[:, 3]),
+        "stream: to the first wave's end": us(wfirst - P[:, 4]),
+        "stream: to the last wave's end": us(wend - P[:, 4]),
+        "last wave: hand-in": us(P[:, 5] - wend),
+        "patched values, bound, gather": us(P[:, 6] - P[:, 5]),
+        "members in order": us(P[:, 7] - P[:, 6]),
+        "tail: exp, sum chain, division": us(P[:, 9] - P[:, 8]),
+        "tail: top-p chain, cut points": us(P[:, 10] - P[:, 9]),
+        "tail: draw chain, output": us(P[:, 11] - P[:, 10]),
+        "workgroup total": us(P[:, 11] - P[:, 0]),
+    }
+    ok = (P[:, 11] > 0) & (P[:, 7] > 0)
+    print(f"# k64_kernel phases, workload {args.workload} (B={w.B} V={w.V}), last of {args.steps} calls; "
+          f"{int(ok.sum())} rows with every stamp")
+    print("| Phase | median us | p10 | p90 |")
+    print("|---|---|---|---|")
+    for name, v in rows.items():
+        v = v[ok]
+        print(f"| {name} | {np.median(v):.2f} | {np.percentile(v, 10):.2f} | {np.percentile(v, 90):.2f} |")
+    print(f"candidates above the shared bound per row (median / p90 / max): {np.median(P[ok, 12]):.0f} / "
+          f"{np.percentile(P[ok, 12], 90):.0f} / {P[ok, 12].max()}; above the offers' bound: "
+          f"{np.median(P[ok, 13]):.0f} / {np.percentile(P[ok, 13], 90):.0f} / {P[ok, 13].max()}")
+    def key2f(k):
+        k = np.uint32(k)
+        b = (k & 0x7fffffff) if (k & 0x80000000) else (~k & 0xffffffff)
+        return float(np.array([b], np.uint32).view(np.float32)[0])
+    print(f"bootstrap bound (median): {key2f(int(np.median(P[ok, 14]))):.4f}; offers' bound: "
+          f"{key2f(int(np.median(P[ok, 15]))):.4f}")
+    print(f"kernel span (first start to last end): {us(P[ok, 11].max() - t0):.2f} us")
+    if D[ok, 0].max() > 0:
+        det = {"second chunk requested (after the patch table)": us(D[:, 0] - P[:, 3]),
+               "first chunk in": us(D[:, 1] - D[:, 0]),
+               "bootstrap histogram": us(D[:, 2] - D[:, 1]),
+               "barrier": us(D[:, 3] - D[:, 2]),
+               "bound scan, barrier": us(P[:, 4] - D[:, 3])}
+        for name, v in det.items():
+            v = v[ok]
+            print(f"| {name} | {np.median(v):.2f} | {np.percentile(v, 10):.2f} | {np.percentile(v, 90):.2f} |")
+        if D[ok, 11].max() > 0:
+            v = us(D[:, 11] - D[:, 10])[ok]
+            print(f"| tail run again (warm instruction cache) | {np.median(v):.2f} | {np.percentile(v, 10):.2f} | "
+                  f"{np.percentile(v, 90):.2f} |")
+            v = us(P[:, 11] - P[:, 8])[ok]
+            print(f"| tail, first run | {np.median(v):.2f} | {np.percentile(v, 10):.2f} | {np.percentile(v, 90):.2f} |")
+        m = ok & (D[:, 9] > D[:, 8])
+        if m.any():
+            ghz = (D[m, 9] - D[m, 8]) / ((P[m, 11] - P[m, 5]) / 100.0) / 1e3
+            print(f"shader clock over the last wave's work: {np.median(ghz):.2f} GHz (median)")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -377,9 +475,13 @@ def main():
     ap.add_argument("--write-dir")
     ap.add_argument("--out")
     ap.add_argument("--commit", default="")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="per-phase times of the k64 kernel from the phases build of the library")
     args = ap.parse_args()
     if args.traffic_summary:
         return traffic_summary(args)
+    if args.phase_stamps:
+        return phase_stamps(args)
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (rows shard across GPUs with no "
               "collective; see DESIGN.md); --gpus must be 1", file=sys.stderr)

@@ -148,6 +148,7 @@ struct nls_sampler {
   int S = 1, L = 0, xcd_map = 0;
   int ccap = 0, nwords = 0, pcap = 0, mcap = 0, kcap = 0, offA = 0, pc = 0;
   int parity = 0;  // which generic counter this call uses
+  int hbits = 0;   // k64_kernel's hash table: 2^hbits slots
 
   RowParams* rp = nullptr;
   int32_t* bias_ids = nullptr;
@@ -514,6 +515,20 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   s->plan.q = g.q;
   s->plan.wave = g.wave;
   s->plan.lds = g.lds;
+  // Greedy and top-k <= 64 rows streamed whole by 1024-thread workgroups run
+  // k64_kernel, its patch hash table as large as the LDS allows.
+  s->plan.k64 = false;
+  s->hbits = 0;
+  if (stream_ok && g.wave && g.nt == 1024 && g.S == 1 && env_int("NLS_K64", 1)) {
+    int hb = 0;
+    for (int b = 8; b <= 12; ++b)
+      if (k64_lds_bytes(vocab, b) <= kK64MaxDynLds) hb = b;
+    if (hb > 0) {
+      s->plan.k64 = true;
+      s->hbits = hb;
+      s->plan.lds = k64_lds_bytes(vocab, hb);
+    }
+  }
   // Without full-sort rows the whole-row kernel only serves the rare row the
   // streaming kernel hands on: one workgroup keeps that launch cheap.
   s->plan.gen_blocks = any_full ? std::min(B, 256) : 1;
@@ -754,6 +769,7 @@ int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t
   ga.grouped = s->plan.gen_lds > 0 ? 1 : 0;
   a.gen_inline = s->gen_inline;
   a.done = s->done;
+  a.hbits = s->hbits;
   a.ga = ga;
   LaunchPlan lp = s->plan;
   lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);

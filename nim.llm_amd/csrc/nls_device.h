@@ -36,6 +36,58 @@
 
 namespace nls {
 
+// Phase timestamps (the `phases` build only: -DNLS_PHASE_STAMPS): per row,
+// slot i of nls_phase_stamp holds the real-time counter (100 MHz) when the
+// row's workgroup reached phase i (or, for NLS_STAMP_VALUE, a count);
+// nls_wave_stamp holds each wave's end of stream.  Each unit has its own
+// copy; the k64 unit's is read back (nls_phase_stamps).
+#ifdef NLS_PHASE_STAMPS
+constexpr int kStampRows = 4096;
+static __device__ uint64_t nls_phase_stamp[kStampRows * 16];
+static __device__ uint64_t nls_wave_stamp[kStampRows * 16];
+static __device__ uint64_t nls_detail_stamp[kStampRows * 16];
+#define NLS_STAMP(row, i)                                                                        \
+  do {                                                                                           \
+    if (__lane_id() == 0 && (row) < kStampRows)                                                 \
+      nls_phase_stamp[(row) * 16 + (i)] = __builtin_amdgcn_s_memrealtime();                      \
+  } while (0)
+#define NLS_STAMP_VALUE(row, i, v)                                                               \
+  do {                                                                                           \
+    if (__lane_id() == 0 && (row) < kStampRows) nls_phase_stamp[(row) * 16 + (i)] = (uint64_t)(v); \
+  } while (0)
+#define NLS_DETAIL_STAMP(row, i)                                                                 \
+  do {                                                                                           \
+    if (__lane_id() == 0 && (row) < kStampRows)                                                 \
+      nls_detail_stamp[(row) * 16 + (i)] = __builtin_amdgcn_s_memrealtime();                     \
+  } while (0)
+#define NLS_DETAIL_CLOCK(row, i)                                                                 \
+  do {                                                                                           \
+    if (__lane_id() == 0 && (row) < kStampRows)                                                 \
+      nls_detail_stamp[(row) * 16 + (i)] = __builtin_amdgcn_s_memtime();                         \
+  } while (0)
+#define NLS_WAVE_STAMP(row, w)                                                                   \
+  do {                                                                                           \
+    if (__lane_id() == 0 && (row) < kStampRows)                                                 \
+      nls_wave_stamp[(row) * 16 + (w)] = __builtin_amdgcn_s_memrealtime();                       \
+  } while (0)
+#else
+#define NLS_STAMP(row, i) \
+  do {                    \
+  } while (0)
+#define NLS_STAMP_VALUE(row, i, v) \
+  do {                             \
+  } while (0)
+#define NLS_WAVE_STAMP(row, w) \
+  do {                         \
+  } while (0)
+#define NLS_DETAIL_STAMP(row, i) \
+  do {                           \
+  } while (0)
+#define NLS_DETAIL_CLOCK(row, i) \
+  do {                           \
+  } while (0)
+#endif
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Penalties first (:71-74), then bias (:76), on the original logit.
@@ -394,6 +446,7 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
     if (lane < k) mem[rank] = x;  // the whole wave has read mem[] above
     x = (lane < k) ? mem[lane] : 0ull;
   }
+  NLS_STAMP(row, 8);
   const bool valid = lane < k;
   const int id = (int)(uint32_t)x;
   const float v = key2f((uint32_t)(x >> 32));
@@ -405,6 +458,7 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
 #pragma unroll
   for (int i = 0; i < kWave; ++i) ssum = ssum + lane_fc(e, i);
   const float p = valid ? e / ssum : 0.0f;
+  NLS_STAMP(row, 9);
   float acc = 0.0f, cum = 0.0f;
 #pragma unroll
   for (int i = 0; i < kWave; ++i) {
@@ -422,6 +476,7 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
     if (m) n = __ffsll((unsigned long long)m) - 1;
   }
   const float total = lane_fc(cum, n - 1);
+  NLS_STAMP(row, 10);
   const double u = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(u_lane0), 0),
                                     __builtin_amdgcn_readlane(__double2loint(u_lane0), 0));
   float r = (float)u * total;

@@ -53,6 +53,25 @@ constexpr int kWaveTopK = 64;        // largest k of the wave path
 constexpr size_t kDualStreamLds = 68 * 1024;  // dynamic LDS of a 512-thread workgroup, two per CU
 constexpr int64_t kSmallRowV = 49152;  // rows up to this size stream in one workgroup
 
+// k64_kernel (greedy and top-k <= 64 rows, one 1024-thread workgroup per
+// row): LDS = patch bitmap | hash table (4 words per slot) | per-wave
+// candidate buffers | bootstrap histogram (later the candidate list) | list
+// of patched slots to evaluate.
+constexpr int kK64Threads = 1024;
+constexpr int kK64BootBins = 4096;
+constexpr size_t kK64BootBytes = (size_t)kK64BootBins * 4;
+constexpr int kK64CandCap = (int)(kK64BootBytes / 8);
+constexpr int kK64PListCap = 1024;
+constexpr int kK64MaxHash = 4096;
+constexpr int kK64SelRegs = 4;  // candidates per lane of the register select (256 per row)
+constexpr size_t kK64MaxDynLds = 138 * 1024;  // 160 KB of LDS less the kernel's static part
+constexpr int kK64RankCap = 256;  // candidates ranked by the whole workgroup at the end
+inline size_t k64_lds_bytes(int64_t V, int hbits) {
+  const size_t nw = (size_t)((V + 31) / 32);
+  return ((nw * 4 + 15) & ~(size_t)15) + ((size_t)16 << hbits) + (size_t)(kK64Threads / 64) * kWaveCap * 8 +
+         kK64BootBytes + (size_t)kK64PListCap * 4;
+}
+
 // Slice-exchange record of one (row, slice) when a row is split over S
 // workgroups.
 enum SliceFlags : int32_t { kSliceOverflow = 1, kSliceNan0 = 2 /* element 0 of the row is NaN */ };
@@ -146,12 +165,14 @@ struct StreamArgs {
   // kernel (counted in `done`, zero between calls) instead of a second launch
   int gen_inline;
   uint32_t* done;
+  int hbits;    // k64_kernel: log2 of the patch hash table's slots
   GenericArgs ga;
 };
 
 
 struct LaunchPlan {
   int nt;        // streaming workgroup size: 256, 512 (k > 64, two per CU) or 1024
+  bool k64;      // k64_kernel instead of stream_kernel (wave path, one workgroup per row)
   bool wave;     // every top-k row has k <= kWaveTopK: per-wave candidate buffers
   int q;         // per-thread top-Q of the threshold refresh: 1, 2, 4 or 8
   bool vec4;     // 16-byte loads (V % 4 == 0 and aligned logits)

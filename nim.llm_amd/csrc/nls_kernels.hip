@@ -387,7 +387,7 @@ hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const Laun
                          hipEvent_t gev_stop) {
   hipError_t e;
   if (ev_start && (e = hipEventRecord(ev_start, s)) != hipSuccess) return e;
-  if ((e = launch_stream(sa, lp, s)) != hipSuccess) return e;
+  if ((e = lp.k64 ? launch_k64(sa, lp, s) : launch_stream(sa, lp, s)) != hipSuccess) return e;
   if (ev_stop && (e = hipEventRecord(ev_stop, s)) != hipSuccess) return e;
   if (!sa.gen_inline) {
     if (gev_start && (e = hipEventRecord(gev_start, s)) != hipSuccess) return e;
@@ -416,6 +416,7 @@ size_t max_dynamic_lds() { return 143 * 1024; }  // 160 KB of LDS less the large
 hipError_t set_kernel_attributes() {
   hipError_t e;
   if ((e = set_generic_attributes()) != hipSuccess) return e;
+  if ((e = set_k64_attributes()) != hipSuccess) return e;
   if ((e = set_stream_attributes<512, true>()) != hipSuccess) return e;
   if ((e = set_stream_attributes<512, false>()) != hipSuccess) return e;
   if ((e = set_stream_attributes<256, true>()) != hipSuccess) return e;

@@ -15,6 +15,9 @@ hipError_t launch_stream_variant(const StreamArgs& a, const LaunchPlan& p, hipSt
 template <int NT, bool VEC>
 hipError_t set_stream_attributes();
 
+hipError_t launch_k64(const StreamArgs& a, const LaunchPlan& p, hipStream_t s);
+hipError_t set_k64_attributes();
+
 hipError_t launch_generic(const GenericArgs& ga, const LaunchPlan& lp, hipStream_t s);
 hipError_t set_generic_attributes();
 
