@@ -8,8 +8,9 @@ exceed the 256 MB Infinity Cache, so every step reads its logits from HBM.
     python bench.py [--steps K] [--warmup W] [--workload headline] [--no-cpu-baseline]
 
 Prints one JSON line.  `roofline` is for the dominant kernel of a call: the
-streaming kernel (stream_kernel: the single read of the logits, running the
-whole pipeline of greedy and top-k rows) or, when full-sort rows take longer,
+streaming kernel (the single read of the logits, running the whole pipeline
+of greedy and top-k rows: k64_kernel for k <= 64 with 1024-thread workgroups,
+stream_kernel otherwise) or, when full-sort rows take longer,
 the whole-row kernel (generic_kernel).  Each kernel is charged with the
 algorithmic bytes of the rows it serves (`kernels` lists both) and timed with
 HIP events on the sampler's stream: around K back-to-back calls when a call is
@@ -572,7 +573,8 @@ def main():
     generic_bytes = float(sum(per_row[b] for b in range(B) if not streamed[b]))
     pipe_bytes = float(sum(per_row))
     s_avg, s_med = stats(ev_s)
-    kernels = {"stream_kernel": {"rows": int(sum(streamed)), "algorithmic_bytes_per_launch": stream_bytes,
+    sname = "k64_kernel" if plan.k64 else "stream_kernel"
+    kernels = {sname: {"rows": int(sum(streamed)), "algorithmic_bytes_per_launch": stream_bytes,
                                  "event_pair_avg_us": s_avg * 1e3, "event_pair_median_us": s_med * 1e3}}
     if ev_g:
         g_avg, g_med = stats(ev_g)

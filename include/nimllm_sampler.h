@@ -199,6 +199,8 @@ typedef struct nls_plan {
   int32_t generic_launch;  /* 1: a second kernel serves the full-sort rows       */
   int32_t streamed_rows;   /* rows the streaming kernel runs to the end          */
   int64_t first_unit_bytes;/* logits a non-streamed row's workgroup requests before it leaves */
+  int32_t k64;             /* 1: the streaming kernel is k64_kernel (1024 threads, k <= 64) */
+  int32_t reserved;
 } nls_plan;
 /* row_streamed: NULL or host [batch], 1 where the streaming kernel runs the row. */
 int nls_get_plan(const nls_sampler* s, nls_plan* out, int32_t* row_streamed);

@@ -76,6 +76,8 @@ class NlsPlan(ctypes.Structure):
         ("generic_launch", ctypes.c_int32),
         ("streamed_rows", ctypes.c_int32),
         ("first_unit_bytes", ctypes.c_int64),
+        ("k64", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

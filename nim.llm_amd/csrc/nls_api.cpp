@@ -165,6 +165,8 @@ struct nls_sampler {
   int gen_inline = 0;
   uint32_t* gen_scratch = nullptr;
   int64_t gen_vpad = 0;
+  int gen_scratch_blocks = 0;  // whole-row workgroups gen_scratch holds
+  int ncu = 256;
   int32_t* stage_ids = nullptr;  // staged ids, then one append count per staged row
   size_t stage_cap = 0;
   std::vector<int32_t> h_stage;
@@ -192,6 +194,22 @@ struct nls_sampler {
     dfree(stage_ids);
     dfree(tmp_logits);
     dfree(tmp_out);
+  }
+
+  // True when a row the streaming kernel runs may patch more distinct ids
+  // (history window + bias entries) than its LDS table holds: such a row is
+  // handed on to the whole-row path, which then gets a launch of its own
+  // across the CUs rather than the streaming kernel's last workgroup.
+  bool window_may_overflow() const {
+    const int64_t cap = plan.k64 ? (int64_t)((1 << hbits) - (1 << hbits) / 4) : (int64_t)pcap;
+    for (int b = 0; b < B; ++b) {
+      const RowParams& r = h_rp[b];
+      if (!r.fast) continue;
+      int64_t w = 0;
+      if (need_window[b] != 0) w = need_window[b] > 0 ? std::min<int64_t>(need_window[b], h_len[b]) : h_len[b];
+      if (w + r.bias_cnt > cap) return true;
+    }
+    return false;
   }
 
   // Grows the history ring so that every row's window fits after `extra`
@@ -580,6 +598,8 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   while (vpad < vocab) vpad <<= 1;
   s->gen_vpad = vpad;
   if ((rc = dalloc(&s->gen_scratch, (size_t)s->plan.gen_blocks * vpad * 5))) return fail(rc);
+  s->gen_scratch_blocks = s->plan.gen_blocks;
+  s->ncu = ncu;
   if ((rc = s->ensure_history(-1, 0))) return fail(rc);
 
   hipStream_t st = s->stream;
@@ -699,8 +719,11 @@ int nls_clear_history(nls_sampler* s) {
   return NLS_OK;
 }
 
-int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t* d_out,
-               const nls_debug* dbg) {
+namespace {
+// One nls_sample call; may_alloc = false for the no-allocation entry point
+// (which then leaves handed-on rows to the streaming kernel's last workgroup).
+int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_t* d_out,
+                const nls_debug* dbg, bool may_alloc) {
   if (!s || !d_logits || !d_out) return NLS_ERR_INVALID_ARGUMENT;
   if (dbg && dbg->cap < 0) return NLS_ERR_INVALID_ARGUMENT;
   DebugPtrs dp;
@@ -767,17 +790,40 @@ int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t
   ga.out = d_out;
   ga.dbg = dp;
   ga.grouped = s->plan.gen_lds > 0 ? 1 : 0;
+  LaunchPlan lp = s->plan;
   a.gen_inline = s->gen_inline;
+  if (a.gen_inline && s->window_may_overflow()) {
+    const int want = std::min(s->B, s->ncu);
+    if (s->gen_scratch_blocks < want && may_alloc) {
+      uint32_t* ns = nullptr;
+      const int rc = dalloc(&ns, (size_t)want * s->gen_vpad * 5);
+      if (rc) return rc;
+      NLS_HIP(hipStreamSynchronize(s->stream));  // the old scratch may still be in use
+      dfree(s->gen_scratch);
+      s->gen_scratch = ns;
+      s->gen_scratch_blocks = want;
+      ga.scratch = ns;
+    }
+    if (s->gen_scratch_blocks >= want) {
+      a.gen_inline = 0;
+      lp.gen_blocks = want;
+    }
+  }
   a.done = s->done;
   a.hbits = s->hbits;
   a.ga = ga;
-  LaunchPlan lp = s->plan;
   lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
   hipEvent_t e0 = s->prof_start, e1 = s->prof_stop, g0 = s->prof_gstart, g1 = s->prof_gstop;
   s->prof_start = s->prof_stop = s->prof_gstart = s->prof_gstop = nullptr;
   NLS_HIP(launch_sample(a, ga, lp, s->stream, e0, e1, g0, g1));
   s->parity ^= 1;
   return NLS_OK;
+}
+}  // namespace
+
+int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t* d_out,
+               const nls_debug* dbg) {
+  return sample_impl(s, d_logits, d_u, d_out, dbg, true);
 }
 
 int nls_profile_next(nls_sampler* s, void* start_event, void* stop_event) {
@@ -800,6 +846,7 @@ int nls_get_plan(const nls_sampler* s, nls_plan* out, int32_t* row_streamed) {
   out->stream_threads = s->plan.lds > 0 ? s->plan.nt : 0;
   out->slices = s->S;
   out->generic_launch = s->gen_inline ? 0 : 1;
+  out->k64 = s->plan.k64 ? 1 : 0;
   // a workgroup requests its first unit (kStreamVec4 float4 per thread)
   // before it reads the row's constants
   out->first_unit_bytes =
@@ -845,7 +892,7 @@ int nls_sample_host_noalloc(nls_sampler* s, const float* h_logits, int64_t* h_ou
   float* d_logits = reinterpret_cast<float*>(base);
   int32_t* d_out = reinterpret_cast<int32_t*>(base + ids_off);
   NLS_HIP(hipMemcpyAsync(d_logits, h_logits, n * 4, hipMemcpyHostToDevice, s->stream));
-  const int rc = nls_sample(s, d_logits, nullptr, d_out, nullptr);
+  const int rc = sample_impl(s, d_logits, nullptr, d_out, nullptr, false);
   if (rc) return rc;
   // the int32 ids land in the first half of h_out and are widened in place,
   // from the last one down (no host buffer either)

@@ -434,7 +434,7 @@ __device__ __forceinline__ float lane_fc(float x, int l) {
 // `total`, which the reference accumulates with the same operations.
 __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams& P,
                                           double u_lane0, int row, int32_t* out,
-                                          const DebugPtrs& dbg) {
+                                          const DebugPtrs& dbg, int path = 2) {
   const int lane = lane_id();
   // rank sort: each member's position is the number of members above it
   // (entries are distinct (key, id) pairs; the zero padding ranks last)
@@ -494,7 +494,7 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
     if (dbg.n) dbg.n[row] = n;
     if (dbg.ncand) dbg.ncand[row] = k;
     if (dbg.total) dbg.total[row] = total;
-    if (dbg.path) dbg.path[row] = 2;
+    if (dbg.path) dbg.path[row] = path;
   }
   if (lane < min(n, dbg.cap)) {
     if (dbg.cand_ids) dbg.cand_ids[(int64_t)row * dbg.cap + lane] = id;
@@ -2304,6 +2304,76 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   return res;
 }
 
+// Top-k rows (k <= NT) of the whole-row path without the sort: kA holds the
+// row's ~keys (final values, patches and temperature applied), and each
+// thread's largest key (tmax) is a distinct element, so the k-th largest of
+// the NT thread maxima bounds the row's k-th largest key from below.  The
+// elements at or above it go to an LDS list, the heap rule picks the k
+// members (sampler.nim:85-95) and the tail runs (:98-121).  False, before
+// the row's uniform is taken, when the list or the tie set does not fit:
+// the caller sorts the row instead.
+constexpr int kWinEnt = 8192;  // listed elements
+constexpr int kWinMem = 2048;  // members / tie set
+constexpr size_t kWinLdsBytes = (size_t)kWinEnt * 8 + (size_t)kWinMem * 8 + 3 * 1024 * 4;
+static_assert(kWinLdsBytes <= (size_t)kGrpPatchCap * 16 + (size_t)kGrpHashCap * 16,
+              "the list fits the whole-row kernel's dynamic LDS (group_lds_bytes)");
+template <int NT>
+__device__ __forceinline__ bool window_topk(const GenericArgs& a, int row, const RowParams& P,
+                                            const uint32_t* kA, uint32_t tmax, uint32_t* hist,
+                                            int* smem, double* s_u_p, int* s_i, unsigned char* glds) {
+  static_assert(NT <= 1024, "vals/ids/e hold k <= 1024 members");
+  const int n = (int)a.V;
+  const int k = P.k;
+  const int tid = threadIdx.x;
+  uint64_t* ent = reinterpret_cast<uint64_t*>(glds);
+  uint64_t* mem = ent + kWinEnt;
+  float* vals = reinterpret_cast<float*>(mem + kWinMem);
+  int32_t* ids = reinterpret_cast<int32_t*>(vals + 1024);
+  float* ebuf = reinterpret_cast<float*>(ids + 1024);
+  for (int q = tid; q < kSelWords; q += NT) hist[q] = 0u;
+  if (tid == 0) {
+    s_i[2] = 0;
+    s_i[3] = 0;
+  }
+  __syncthreads();
+  const SelectResult b0 = block_select<NT>([&](auto fn) { fn(tmax, tid < n); }, k, -1, hist, smem);
+  const uint32_t t0 = b0.tau;
+  for (int i = tid; i < n; i += NT) {
+    const uint32_t key = ~kA[i];
+    if (key >= t0) {
+      const int p = atomicAdd(&s_i[2], 1);
+      if (p < kWinEnt) ent[p] = ((uint64_t)key << 32) | (uint32_t)i;
+    }
+  }
+  __syncthreads();
+  const int N = s_i[2];
+  if (N > kWinEnt || !topk_members<NT>(ent, N, k, mem, kWinMem, hist, smem, &s_i[3])) {
+    __syncthreads();
+    return false;
+  }
+  if (tid == 0) *s_u_p = row_uniform(a.d_u, a.rng, row);
+  __syncthreads();
+  if (k <= kWave) {
+    if ((tid >> 6) == 0) wave_tail(mem, k, P, *s_u_p, row, a.out, a.dbg, 5);
+    __syncthreads();
+    return true;
+  }
+  const int kpow = next_pow2(k);
+  for (int i = k + tid; i < kpow; i += NT) mem[i] = 0ull;
+  __syncthreads();
+  bitonic_sort_u64<NT>(mem, kpow, true);
+  for (int i = tid; i < k; i += NT) {
+    vals[i] = key2f((uint32_t)(mem[i] >> 32));
+    ids[i] = (int32_t)(uint32_t)mem[i];
+  }
+  __syncthreads();
+  const TailOut to = softmax_cutoff_draw<NT>(vals, ids, ebuf, k, P, *s_u_p, smem);
+  if (tid == 0) a.out[row] = to.id;
+  write_debug<NT>(a.dbg, row, 5, to.n, k, to.total, ids, ebuf);
+  __syncthreads();
+  return true;
+}
+
 // Rows of the list from index w0 on, every nw-th: the whole-row path.  LDS
 // scratch is passed in (wcnt: NW * 256 words, dbase and drun: 256 each), so
 // that the streaming kernel's last workgroup can run it too.
@@ -2375,6 +2445,7 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
     const bool greedy = P.mode == kModeGreedy;
     float bv = -__builtin_inff();
     int bi = 0x7fffffff;
+    uint32_t tmax = 0u;  // the thread's largest key (a distinct element per thread)
     for (int i = tid; i < n; i += NT) {
       float v = src[i];
       const uint32_t c = kB[i];
@@ -2387,7 +2458,9 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
       if (greedy) {
         argmax_merge(bv, bi, v, i);
       } else {
-        kA[i] = ~f2key(v * P.invT);
+        const uint32_t key = f2key(v * P.invT);
+        tmax = max(tmax, key);
+        kA[i] = ~key;
         iA[i] = (uint32_t)i;
       }
     }
@@ -2419,6 +2492,11 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
       continue;
     }
     __syncthreads();
+    if constexpr (GROUPED) {
+      if (P.mode == kModeTopK && P.k <= NT && glds && a.grouped &&
+          window_topk<NT>(a, row, P, kA, tmax, wcnt, smem, s_u_p, s_i, glds))
+        continue;
+    }
     radix_sort_pass<NT>(kA, iA, kB, iB, n, 0, wcnt, dbase, drun);
     radix_sort_pass<NT>(kB, iB, kA, iA, n, 8, wcnt, dbase, drun);
     radix_sort_pass<NT>(kA, iA, kB, iB, n, 16, wcnt, dbase, drun);

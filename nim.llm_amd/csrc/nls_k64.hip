@@ -407,10 +407,13 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
     __syncthreads();
     if (wv == 0) NLS_STAMP(row, 2);
     // hash slot of a patched id (inserting it when `insert`); -1 when the
-    // table is full
+    // table is full, or for an insert that has probed 8 slots of a table past
+    // its load limit (the row is handed on then, so a long window stops early
+    // instead of probing a full table)
     auto hash_slot = [&](int id, bool insert) -> int {
       uint32_t h = hash_home(id, a.hbits);
       for (int probe = 0; probe < hcap; ++probe) {
+        if (insert && probe == 8 && s_hdist > hcap - hcap / 4) return -1;
         int cur;
         if (insert) {
           cur = atomicCAS(&hkey[h], kHashEmpty, id);

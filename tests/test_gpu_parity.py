@@ -252,6 +252,64 @@ def test_topk_rows_with_window_and_bias_two_per_cu(pkg, torch):
     compare_rows(x, plist, [list(hist[b]) for b in range(B)], biases, u, ids_, dbg, "two_per_cu")
 
 
+@pytest.mark.parametrize("B,V,k", [(256, 128256, 50), (64, 50000, 300)])
+def test_long_windows_full_batch(pkg, torch, B, V, k):
+    """Whole-history penalties (repeatLastN = 0) over 6000 accepted ids per row,
+    4500 of them distinct, plus 50 bias ids: more patched ids than the
+    streaming kernel's LDS table holds, on every row of a full batch.  The
+    rows go to the whole-row kernel, launched across the CUs; ids,
+    candidates, probabilities, n and total against the oracle, and the call
+    stays within a few times the streaming kernel's time (no serial cliff)."""
+    rng = np.random.default_rng(4096 + k)
+    H, distinct = 6000, 4500
+    say(f"[long_windows] B={B} V={V} k={k} H={H} distinct={distinct}")
+    x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
+    hist = np.empty((B, H), dtype=np.int64)
+    for b in range(B):
+        ids = rng.choice(V, distinct, replace=False)
+        hist[b] = np.concatenate([ids, ids[:H - distinct]])[rng.permutation(H)]
+    plist, biases = [], []
+    for b in range(B):
+        plist.append(dict(temperature=0.0 if b % 8 == 7 else 1.0, topK=k, topP=0.95, minP=0.0,
+                          repeatPenalty=1.0 if k == 50 else 1.1, repeatLastN=0,
+                          presencePenalty=0.3, frequencyPenalty=0.5, seed=1))
+        bid = rng.choice(V, 50, replace=False)
+        bias = {int(i): float(rng.uniform(-5, 5)) for i in bid}
+        for i in bid[:5]:
+            bias[int(i)] = -math.inf
+        biases.append(bias)
+    u = rng.random(B)
+    params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
+    s = pkg.BatchSampler(params, V)
+    try:
+        s.accept(hist)
+        d = torch.from_numpy(x).cuda()
+        du = torch.from_numpy(u).cuda()
+        ids_, dbg = s.sample(d, du, debug_cap=64)
+        torch.cuda.synchronize()
+        ids_ = ids_.cpu().numpy()
+        dbg = {kk: v.cpu().numpy() for kk, v in dbg.items()}
+        out = torch.empty(B, dtype=torch.int32, device="cuda")
+        for _ in range(3):
+            s.sample(d, du, out)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(10):
+            s.sample(d, du, out)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 100.0
+        say(f"[long_windows] B={B} V={V} k={k}: {us:.1f} us per call; paths "
+            f"{np.bincount(dbg['path'], minlength=6).tolist()}")
+    finally:
+        s.close()
+    compare_rows(x, plist, [list(hist[b]) for b in range(B)], biases, u, ids_, dbg, "long_windows")
+    topk_rows = np.array([p["temperature"] > 0 for p in plist])
+    assert np.all(dbg["path"][topk_rows] == 5), np.bincount(dbg["path"][topk_rows], minlength=6).tolist()
+    assert us < 5000.0, us
+
+
 def test_golden_fixtures(pkg, torch):
     import json
     import os
