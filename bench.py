@@ -354,6 +354,92 @@ def bench_row_nll(args):
     print(json.dumps(res), flush=True)
 
 
+def bench_softmax(args, logp):
+    """softmaxInPlace (sampler.nim:51-57) over whole rows of the workload's
+    logits (nls_softmax_rows), or logProb's per-token term with one random
+    target per row (nls_log_prob).  One line of JSON like the sampler's."""
+    import numpy as np
+    import torch
+
+    pkg = load_pkg()
+    from nimllm_amd import workloads
+
+    w = workloads.make(args.workload, seed=args.seed)
+    B, V = w.B, w.V
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    nbuf = max(2, math.ceil(640e6 / (B * V * 4)))
+    base = torch.from_numpy(w.logits).to(dev)
+    bufs = [base] + [base.clone() for _ in range(nbuf - 1)]
+    out = torch.empty_like(base)
+    rng = np.random.default_rng(args.seed)
+    tgt = torch.from_numpy(rng.integers(0, V, size=B).astype(np.int32)).to(dev)
+
+    def call(x):
+        if logp:
+            return pkg.log_prob_device(x, tgt)
+        return pkg.softmax_device(x, out)
+
+    res0 = call(bufs[0])
+    torch.cuda.synchronize()
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    ok = True
+    for r in (0, B // 2, B - 1):
+        if logp:
+            wp, _ = O.log_prob(w.logits[r], int(tgt[r]))
+            ok &= bool(res0[0][r].cpu().numpy().view(np.uint32) == wp.view(np.uint32))
+        else:
+            ok &= bool(np.array_equal(out[r].cpu().numpy().view(np.uint32),
+                                      O.softmax(w.logits[r]).view(np.uint32)))
+    for i in range(args.warmup):
+        call(bufs[i % nbuf])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.steps):
+        call(bufs[i % nbuf])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    # logits read once; softmax writes every probability, logProb a target,
+    # a float32 and a float64 per row
+    nbytes = float(B * V * 4 + (B * V * 4 if not logp else B * 16))
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    name = "logProb terms" if logp else "softmaxInPlace rows"
+    kern = "softmax_kernel<true>" if logp else "softmax_kernel<false>"
+    res = {"metric": f"{name} (rows/sec) at B={B} x V={V} fp32", "value": B / (ms * 1e-3),
+           "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f32", "data": "synthetic (the sampler workload's logits, rotated over "
+                                   f"{nbuf} buffers" + ("; random targets)" if logp else ")"),
+           "config": {"workload": f"{args.workload} logits, {'nls_log_prob' if logp else 'nls_softmax_rows'}",
+                      "B": B, "V": V},
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": kern,
+                        "kernel_avg_us": ms * 1e3, "algorithmic_bytes_per_launch": nbytes},
+           "parity_spot_check": {"rows": 3, "bit_exact": ok}}
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        done = 0
+        while time.perf_counter() - t0 < args.cpu_budget:
+            r = done % B
+            if logp:
+                O.log_prob(w.logits[r], int(tgt[r]), O.EXPF_LIBM)
+            else:
+                O.softmax(w.logits[r], O.EXPF_LIBM)
+            done += 1
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": done / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+                               "sample": f"{done} rows on one thread for {dt:.1f} s; C restatement of "
+                                         "src/nimllm/sampler.nim:51-57 (-O2 -ffp-contract=off, libm expf"
+                                         + (", log)" if logp else ")")}
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
 def phase_stamps(args):
     """Per-phase wall-clock of the k64 kernel on the workload, from the
     `phases` build of the library (make -C nim.llm_amd/csrc phases):
@@ -467,6 +553,10 @@ def main():
     ap.add_argument("--top-tokens", action="store_true",
                     help="time topTokens (n = --top-n per row) on the workload's logits instead")
     ap.add_argument("--top-n", type=int, default=5)
+    ap.add_argument("--softmax", action="store_true",
+                    help="time nls_softmax_rows (softmaxInPlace over whole rows) instead of the sampler")
+    ap.add_argument("--log-prob", action="store_true",
+                    help="time nls_log_prob (logProb's per-token term) instead of the sampler")
     ap.add_argument("--row-nll", action="store_true",
                     help="time perplexity's per-position term (one target per row) on the workload's logits")
     ap.add_argument("--traffic-summary", action="store_true",
@@ -492,6 +582,8 @@ def main():
         return bench_top_tokens(args)
     if args.row_nll:
         return bench_row_nll(args)
+    if args.softmax or args.log_prob:
+        return bench_softmax(args, args.log_prob)
     import numpy as np
     import torch
 

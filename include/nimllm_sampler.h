@@ -179,6 +179,25 @@ int nls_top_tokens(const float* d_logits, int32_t rows, int64_t vocab, int32_t n
 int nls_row_nll(const float* d_logits, int32_t rows, int64_t vocab, const int32_t* d_targets,
                 double* d_out, void* stream);
 
+/* softmaxInPlace (src/nimllm/sampler.nim:51-57) on each of `rows` rows of
+ * d_logits [rows x vocab] (device, row-major): d_out[r * vocab + i] =
+ * exp(l_i - mx) / s, with mx the row's float32 maximum (NaN entries skipped, as
+ * Nim's max keeps mx), exp correctly rounded (the sampler's exp) and s the
+ * fp32 sum of the exponentials added one at a time in index order -- bit for
+ * bit the reference's values under that exp.  d_out may equal d_logits (the
+ * reference's in-place form).  Asynchronous on `stream`. */
+int nls_softmax_rows(const float* d_logits, int32_t rows, int64_t vocab, float* d_out, void* stream);
+
+/* logProb's per-token term (nimllm-doc-en.md:1700-1707: `var p = logits;
+ * softmaxInPlace(p); result += ln(p[id].float)`): for each of `rows` rows and
+ * its target id d_targets[r], d_prob[r] = p[target] as float32 (bit for bit,
+ * as nls_softmax_rows computes it) and d_logp[r] = ln(float64(d_prob[r])) (the
+ * device's float64 log, within 1 ulp of the C library's).  Summing d_logp over
+ * a continuation's positions gives logProb.  Targets outside [0, vocab) give
+ * NaN.  Asynchronous on `stream`. */
+int nls_log_prob(const float* d_logits, int32_t rows, int64_t vocab, const int32_t* d_targets, float* d_prob,
+                 double* d_logp, void* stream);
+
 /* Correctly rounded exp on fp32 inputs, on the device: d_out[i] = exp(d_in[i]). */
 int nls_expf_device(const float* d_in, float* d_out, int64_t n, void* stream);
 

@@ -35,7 +35,8 @@ EXPORTED = (
     "nls_accept_device", "nls_clear_history", "nls_sample", "nls_sample_host",
     "nls_sample_host_noalloc",
     "nls_synchronize", "nls_rng_uniforms", "nls_get_rng_state", "nls_set_rng_state",
-    "nls_top_tokens", "nls_row_nll", "nls_expf_device", "nls_profile_next",
+    "nls_top_tokens", "nls_row_nll", "nls_softmax_rows", "nls_log_prob", "nls_expf_device",
+    "nls_profile_next",
     "nls_profile_next_generic", "nls_get_plan", "nls_status_string", "nls_last_error",
 )
 
@@ -119,6 +120,8 @@ def lib():
         L.nls_set_rng_state.argtypes = [vp, ctypes.c_int32, ctypes.c_uint64, ctypes.c_uint64]
         L.nls_top_tokens.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, vp, vp, vp]
         L.nls_row_nll.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, vp, vp, vp]
+        L.nls_softmax_rows.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, vp, vp]
+        L.nls_log_prob.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, vp, vp, vp, vp]
         L.nls_expf_device.argtypes = [vp, vp, ctypes.c_int64, vp]
         L.nls_profile_next.argtypes = [vp, vp, vp]
         L.nls_profile_next_generic.argtypes = [vp, vp, vp]
@@ -412,6 +415,55 @@ def row_nll_device(logits, targets):
     check(lib().nls_row_nll(ctypes.c_void_p(x.data_ptr()), rows, V, ctypes.c_void_p(t.data_ptr()),
                             ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream)), "nls_row_nll")
     return out
+
+
+def softmax_device(logits, out=None):
+    """softmaxInPlace (src/nimllm/sampler.nim:51-57) of every row of a
+    [rows, V] (or [V]) float32 device tensor; `out` may be `logits` itself
+    (the reference's in-place form).  Returns out."""
+    import torch
+
+    x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    rows, V = x.shape
+    if out is None:
+        out = torch.empty_like(logits)
+    assert out.is_cuda and out.dtype == torch.float32 and out.is_contiguous() and out.numel() == x.numel()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    check(lib().nls_softmax_rows(ctypes.c_void_p(x.data_ptr()), rows, V, ctypes.c_void_p(out.data_ptr()),
+                                 ctypes.c_void_p(stream)), "nls_softmax_rows")
+    return out
+
+
+def log_prob_device(logits, targets):
+    """logProb's per-token term (nimllm-doc-en.md:1700-1707) for a [rows, V]
+    float32 device tensor and int32 target ids [rows]: (p[target] float32,
+    ln(float64(p[target])) float64) per row, p = softmaxInPlace of the row."""
+    import torch
+
+    x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    t = targets.to(device=x.device, dtype=torch.int32).contiguous()
+    rows, V = x.shape
+    assert t.numel() == rows
+    prob = torch.empty(rows, dtype=torch.float32, device=x.device)
+    logp = torch.empty(rows, dtype=torch.float64, device=x.device)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    check(lib().nls_log_prob(ctypes.c_void_p(x.data_ptr()), rows, V, ctypes.c_void_p(t.data_ptr()),
+                             ctypes.c_void_p(prob.data_ptr()), ctypes.c_void_p(logp.data_ptr()),
+                             ctypes.c_void_p(stream)), "nls_log_prob")
+    return prob, logp
+
+
+def log_prob(context_logits, continuation):
+    """logProb (nimllm-doc-en.md:1700-1707) given the logits the model
+    produced before each continuation token ([len, V] device tensor) and the
+    continuation's ids: the float64 sum of ln(p[id]) in token order."""
+    _, lp = log_prob_device(context_logits, continuation)
+    total = 0.0
+    for v in lp.cpu().tolist():
+        total += v
+    return total
 
 
 def perplexity(logits, targets):

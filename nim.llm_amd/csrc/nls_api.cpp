@@ -953,6 +953,27 @@ int nls_row_nll(const float* d_logits, int32_t rows, int64_t vocab, const int32_
   return NLS_OK;
 }
 
+int nls_softmax_rows(const float* d_logits, int32_t rows, int64_t vocab, float* d_out, void* stream) {
+  // (the kernel addresses a row in bytes with 32-bit offsets)
+  if (rows < 0 || vocab < 0 || vocab >= (int64_t{1} << 29)) return NLS_ERR_INVALID_ARGUMENT;
+  if (rows == 0) return NLS_OK;
+  if (vocab == 0) return NLS_ERR_EMPTY_VOCAB;
+  if (!d_logits || !d_out) return NLS_ERR_INVALID_ARGUMENT;
+  NLS_HIP(launch_softmax_rows(d_logits, rows, vocab, d_out, reinterpret_cast<hipStream_t>(stream)));
+  return NLS_OK;
+}
+
+int nls_log_prob(const float* d_logits, int32_t rows, int64_t vocab, const int32_t* d_targets, float* d_prob,
+                 double* d_logp, void* stream) {
+  if (rows < 0 || vocab < 0 || vocab >= (int64_t{1} << 29)) return NLS_ERR_INVALID_ARGUMENT;
+  if (rows == 0) return NLS_OK;
+  if (vocab == 0) return NLS_ERR_EMPTY_VOCAB;
+  if (!d_logits || !d_targets || !d_prob || !d_logp) return NLS_ERR_INVALID_ARGUMENT;
+  NLS_HIP(launch_log_prob(d_logits, rows, vocab, d_targets, d_prob, d_logp,
+                          reinterpret_cast<hipStream_t>(stream)));
+  return NLS_OK;
+}
+
 int nls_expf_device(const float* d_in, float* d_out, int64_t n, void* stream) {
   if (n < 0 || (n > 0 && (!d_in || !d_out))) return NLS_ERR_INVALID_ARGUMENT;
   NLS_HIP(launch_expf(d_in, d_out, n, reinterpret_cast<hipStream_t>(stream)));

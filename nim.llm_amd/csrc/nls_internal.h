@@ -197,6 +197,11 @@ hipError_t launch_row_nll(const float* logits, int rows, int64_t V, const int32_
                           hipStream_t s);
 hipError_t launch_top_tokens(const float* logits, int rows, int64_t V, int n, int32_t* ids,
                              float* probs, hipStream_t s);
+// softmaxInPlace over `rows` rows of V logits (out may be logits), and
+// logProb's per-token term; V < 2^29
+hipError_t launch_softmax_rows(const float* logits, int rows, int64_t V, float* out, hipStream_t s);
+hipError_t launch_log_prob(const float* logits, int rows, int64_t V, const int32_t* targets, float* prob,
+                           double* logp, hipStream_t s);
 hipError_t set_kernel_attributes();
 size_t max_dynamic_lds();
 

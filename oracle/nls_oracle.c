@@ -199,6 +199,23 @@ double nlo_row_nll(const float* logits, int64_t V, int64_t target) {
   return -((double)(logits[target] - mx) - log(s));
 }
 
+/* logProb (nimllm-doc-en.md:1700-1707): `var p = logits; softmaxInPlace(p);
+ * result += ln(p[id].float)` -- the float32 probability, widened, then the
+ * float64 natural log (Nim's ln is the C library's log). */
+double nlo_log_prob(const float* logits, int64_t V, int64_t target, int expf_mode, float* p_out) {
+  if (target < 0 || target >= V) {
+    if (p_out) *p_out = NAN;
+    return NAN;
+  }
+  float* p = (float*)malloc((size_t)V * sizeof(float));
+  memcpy(p, logits, (size_t)V * sizeof(float));
+  nlo_softmax_inplace(p, V, expf_mode);
+  const float pt = p[target];
+  free(p);
+  if (p_out) *p_out = pt;
+  return log((double)pt);
+}
+
 /* ------------------------------------------------------------------------ */
 /* HeapQueue[(float32, int)] (sampler.nim:88-95): binary min-heap ordered by */
 /* Nim's lexicographic tuple `<`, which compares fields with `cmp`.          */

@@ -117,6 +117,10 @@ int64_t nlo_top_tokens(const float* logits, int64_t V, int64_t n, int expf_mode,
                        int64_t* ids, float* probs);
 /* perplexity's per-position negative log-likelihood (model.nim:578-583). */
 double nlo_row_nll(const float* logits, int64_t V, int64_t target);
+/* logProb's per-token term (nimllm-doc-en.md:1700-1707): p = softmaxInPlace of
+ * a copy of the row (sampler.nim:51-57), then ln(float64(p[target])); *p_out
+ * receives p[target].  target outside [0, V) gives NaN. */
+double nlo_log_prob(const float* logits, int64_t V, int64_t target, int expf_mode, float* p_out);
 
 #ifdef __cplusplus
 }

@@ -105,6 +105,9 @@ def lib():
         L.nlo_top_tokens.restype = ctypes.c_int64
         L.nlo_row_nll.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64]
         L.nlo_row_nll.restype = ctypes.c_double
+        L.nlo_log_prob.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                   P(ctypes.c_float)]
+        L.nlo_log_prob.restype = ctypes.c_double
         _lib = L
     return _lib
 
@@ -183,6 +186,25 @@ def sample_batch(params_list, logits, hist=None, hlen=None, bias_ids=None, bias_
     res = (Result * max(B, 1))()
     L.nlo_sample_batch_res(*args, res, nthreads)
     return out, [res[i] for i in range(B)]
+
+
+def softmax(x, expf_mode=EXPF_CR):
+    """softmaxInPlace (src/nimllm/sampler.nim:51-57) of a copy of x."""
+    import numpy as np
+    y = np.array(x, dtype=np.float32, copy=True)
+    lib().nlo_softmax_inplace(y.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), y.size, expf_mode)
+    return y
+
+
+def log_prob(x, target, expf_mode=EXPF_CR):
+    """logProb's per-token term (nimllm-doc-en.md:1700-1707): (p[target] as
+    float32, ln(float64(p[target]))) with p = softmaxInPlace(x)."""
+    import numpy as np
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    p = ctypes.c_float()
+    lp = lib().nlo_log_prob(x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(x), int(target),
+                            expf_mode, ctypes.byref(p))
+    return np.float32(p.value), lp
 
 
 def row_nll(x, target):

@@ -676,6 +676,77 @@ def test_top_tokens_parity(pkg, torch):
         pkg.top_tokens_device(torch.zeros((1, 5000), device="cuda"), 2049)
 
 
+def _softmax_rows_input(rows, V, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, V)) * rng.choice([0.5, 2.5, 8.0], size=(rows, 1))).astype(np.float32)
+    if rows > 0:
+        x[0] = (np.round(x[0] * 4) / 4).astype(np.float32)  # ties
+    if rows > 1:
+        x[1] = np.float32(1.75)  # equal logits
+    if rows > 2 and V > 3:
+        x[2, :: max(1, V // 7)] = -np.inf
+        x[2, V // 2] = np.nan  # skipped by the maximum, NaN probabilities
+    if rows > 3:
+        x[3] *= np.float32(30.0)  # most exponentials underflow
+    return x
+
+
+@pytest.mark.parametrize("rows,V", [(4, 1), (8, 7), (16, 5001), (8, 32000), (64, 128256), (16, 151936)])
+def test_softmax_rows_parity(pkg, torch, rows, V):
+    """softmaxInPlace (sampler.nim:51-57) on the device: every probability of
+    every row bit for bit against the oracle (correctly rounded exp), out of
+    place and in place, on rows with ties, equal logits, -inf and NaN
+    entries and a wide range."""
+    x = _softmax_rows_input(rows, V, 900 + V)
+    say(f"[softmax_rows] rows={rows} V={V}")
+    d = torch.from_numpy(x).cuda()
+    got = pkg.softmax_device(d)
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    d2 = d.clone()
+    pkg.softmax_device(d2, out=d2)
+    torch.cuda.synchronize()
+    inplace = d2.cpu().numpy()
+    for r in range(rows):
+        want = O.softmax(x[r])
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got[r]), nan), (V, r)
+        assert np.array_equal(got[r][~nan].view(np.uint32), want[~nan].view(np.uint32)), (V, r)
+        assert np.array_equal(np.isnan(inplace[r]), nan), (V, r)
+        assert np.array_equal(inplace[r][~nan].view(np.uint32), want[~nan].view(np.uint32)), (V, r)
+
+
+@pytest.mark.parametrize("rows,V", [(16, 5001), (128, 128256)])
+def test_log_prob_parity(pkg, torch, rows, V):
+    """logProb's per-token term (nimllm-doc-en.md:1700-1707): p[target] bit
+    for bit against the oracle, ln(float64(p)) within 2 ulps of the C
+    library's log, and the continuation sum."""
+    x = _softmax_rows_input(rows, V, 77 + V)
+    rng = np.random.default_rng(V)
+    t = rng.integers(0, V, size=rows).astype(np.int32)
+    t[4] = int(np.argmax(x[4]))
+    t[5] = int(np.argmin(x[5]))
+    say(f"[log_prob] rows={rows} V={V}")
+    prob, logp = pkg.log_prob_device(torch.from_numpy(x).cuda(), torch.from_numpy(t).cuda())
+    torch.cuda.synchronize()
+    prob, logp = prob.cpu().numpy(), logp.cpu().numpy()
+    total = 0.0
+    for r in range(rows):
+        wp, wl = O.log_prob(x[r], int(t[r]))
+        if wp != wp:
+            assert prob[r] != prob[r] and logp[r] != logp[r], r
+            continue
+        assert prob[r].view(np.uint32) == wp.view(np.uint32), (r, prob[r], wp)
+        if wl == -math.inf:
+            assert logp[r] == -math.inf, r
+        else:
+            assert abs(logp[r] - wl) <= 2 * np.spacing(abs(wl)), (r, logp[r], wl)
+            total += wl
+    ok = [r for r in range(rows) if math.isfinite(O.log_prob(x[r], int(t[r]))[1])]
+    got_sum = pkg.log_prob(torch.from_numpy(x[ok]).cuda(), torch.from_numpy(t[ok]).cuda())
+    assert abs(got_sum - total) <= 1e-12 * max(1.0, abs(total)), (got_sum, total)
+
+
 def test_row_nll_parity(pkg, torch):
     """perplexity's per-position term (src/nimllm/model.nim:578-583) on the
     device against the oracle's index-order float64 sum.  The device sums in a

@@ -293,11 +293,11 @@ def _oracle_top_tokens(x, n, mode=None):
     return ids[:got], pr[:got]
 
 
-def _numpy_top_tokens(x, n):
-    """softmaxInPlace (:51-57) and the stable descending sort (:127-128) from
-    numpy parts: exp per element through the oracle's correctly rounded expf,
-    the fp32 sum accumulated strictly in index order (np.add.accumulate), and
-    numpy's stable argsort."""
+def _numpy_softmax(x):
+    """softmaxInPlace (:51-57) from numpy parts: Nim's max (a NaN never
+    replaces mx), exp per element through the oracle's correctly rounded expf,
+    the fp32 sum accumulated strictly in index order (np.add.accumulate) and
+    numpy's fp32 division."""
     x = np.asarray(x, dtype=np.float32)
     mx = np.float32(-np.inf)
     for v in x:
@@ -305,9 +305,41 @@ def _numpy_top_tokens(x, n):
             mx = v
     e = np.array([O.lib().nlo_expf_cr(float(np.float32(v - mx))) for v in x], dtype=np.float32)
     s = np.add.accumulate(e, dtype=np.float32)[-1]
-    p = (e / s).astype(np.float32)
-    order = np.argsort(-p, kind="stable")[:min(n, x.size)]
+    return (e / s).astype(np.float32)
+
+
+def _numpy_top_tokens(x, n):
+    """softmaxInPlace (:51-57) and the stable descending sort (:127-128) from
+    numpy parts: _numpy_softmax, then numpy's stable argsort."""
+    p = _numpy_softmax(x)
+    order = np.argsort(-p, kind="stable")[:min(n, p.size)]
     return order, p[order]
+
+
+def test_softmax_and_log_prob_oracle_pins():
+    """softmaxInPlace (sampler.nim:51-57) and logProb's per-token term
+    (nimllm-doc-en.md:1700-1707: ln of the float32 probability, widened)
+    against the numpy restatement and math.log; equal logits over a power of
+    two give exactly 1/V."""
+    rng = np.random.default_rng(17)
+    rows = [rng.normal(0, 2.5, 3000).astype(np.float32),
+            (np.round(rng.normal(0, 2, 2000) * 4) / 4).astype(np.float32),
+            np.full(50, 1.25, np.float32), np.array([0.5], np.float32),
+            np.array([-np.inf, 1.0, np.nan, 2.0], np.float32)]
+    for x in rows:
+        want = _numpy_softmax(x)
+        got = O.softmax(x)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        for t in (0, len(x) // 2, len(x) - 1):
+            p, lp = O.log_prob(x, t)
+            assert p.view(np.uint32) == want[t].view(np.uint32)
+            if want[t] == want[t]:
+                assert lp == math.log(float(want[t])) if want[t] > 0 else lp == -math.inf
+            else:
+                assert math.isnan(lp)
+    p, lp = O.log_prob(np.full(1024, -3.0, np.float32), 5)
+    assert p == np.float32(1.0 / 1024) and lp == math.log(1.0 / 1024)
+    assert math.isnan(O.log_prob(rows[0], -1)[1]) and math.isnan(O.log_prob(rows[0], 3000)[1])
 
 
 def test_top_tokens_oracle_pins():

@@ -6,6 +6,10 @@ nls_grouped.h, which the gfx950 kernel compiles as device code).
   binade crossings, runs of millions of terms, targets on exact partial sums).
 * tests/exp64_check.cpp: the float64 exp of the row log-sum-exp
   (nls_exp64.h) against the C library's exp on float32 arguments.
+* tests/seqsum_check.cpp: the workgroup evaluation of the sequential fp32 sum
+  (nls_seqsum.h: parity maps scanned per binade, replays, binade changes)
+  against one-at-a-time adds, on softmax terms, exact ties at every scale,
+  subnormals, sums parked at 2^24 and NaN / infinite terms.
 * tests/grouped_check.cpp: the whole group walk -- softmax sum, top-p, min-p,
   total, draw, and the drawn member -- against the oracle's sort path
   (src/nimllm/sampler.nim:96-121) on rows with ties, wide and narrow ranges,
@@ -33,6 +37,13 @@ def built(tmp_path_factory):
     subprocess.run(["g++", *FLAGS, "-shared", "-fPIC", "-o", so,
                     os.path.join(HERE, "grouped_check.cpp")], check=True)
     return exe, so
+
+
+def test_parallel_sequential_sum(tmp_path):
+    exe = str(tmp_path / "seqsum_check")
+    subprocess.run(["g++", *FLAGS, "-o", exe, os.path.join(HERE, "seqsum_check.cpp")], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True)
+    assert r.returncode == 0 and "all sums bit-identical" in r.stdout, r.stdout[-4000:]
 
 
 def test_exp64_matches_libm(tmp_path):
