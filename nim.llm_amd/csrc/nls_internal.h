@@ -191,7 +191,6 @@ hipError_t launch_accept_device(const int32_t* d_ids, int B, int64_t V, int32_t*
 hipError_t launch_expf(const float* x, float* y, int64_t n, hipStream_t s);
 // topTokens over `rows` rows of V logits: n results per row (stride n), n <= kTopMaxN or V <= kTopMaxN
 constexpr int kTopThreads = 1024;
-constexpr int kTopChunk = 4096;  // exponentials per chunk of the sequential sum
 constexpr int kTopMaxN = 2048;   // largest number of results per row (sorted in LDS)
 hipError_t launch_row_nll(const float* logits, int rows, int64_t V, const int32_t* targets, double* out,
                           hipStream_t s);

@@ -11,152 +11,188 @@
 // with -ffp-contract=off so no multiply-add is fused.
 #include "nls_device.h"
 #include "nls_launch.h"
+#include "nls_seqsum.h"
 
 namespace nls {
 
 // ---------------------------------------------------------------------------
 // 3. top_tokens_kernel -- topTokens (sampler.nim:123-130)
 // ---------------------------------------------------------------------------
-// One workgroup per row: softmaxInPlace (:51-57) over the whole row -- the
-// maximum, exp(l - mx), the fp32 sum in index order, the division -- and the
-// first n entries of the stable sort by probability (:127-128).  The
-// probabilities are recomputed from the logits wherever they are needed, so
-// the row is read a few times and only the n results are written.
-//   * The sum runs in index order, one add at a time, in lane 0 of wave 0,
-//     while the other waves compute the next chunk's exponentials into LDS.
-//   * The n-th largest logit L comes from an exact radix select on the logits'
-//     keys; the entries whose probability reaches p(L) are those with a logit
-//     at or above the lowest float whose probability equals p(L) (a bisection
-//     on the float's bits).  They are few: gathered with their probabilities,
-//     sorted by (probability desc, index asc) in LDS, the first n kept.
-//     (Equal probabilities can come from different logits: the exp and the
-//     division round, so the order cannot be taken from the logits.)
-//   * Rows where that set is large (or s is NaN) select on the probabilities
-//     themselves: an exact radix select of the n-th largest probability T, and
-//     among the entries equal to T the lowest indices (a second select on the
-//     index), as the stable sort keeps them.
+// One workgroup per row: softmaxInPlace (:51-57) over the whole row and the
+// first m = min(n, V) entries of the stable sort by probability (:127-128).
+// Two reads of the row when m <= 1024:
+//   1. each thread's largest logit: their maximum is mx (:52-53; Nim's
+//      max(mx, v) keeps mx for a NaN v, as fmaxf does), and the m-th largest
+//      of them bounds the row's m-th largest logit from below (they are m
+//      distinct elements);
+//   2. exp(l - mx) (correctly rounded) chunk by chunk into LDS, summed in
+//      index order exactly as one-at-a-time fp32 adds would (nls_seqsum.h),
+//      while the elements at or above the bound are listed.
+// The probability is non-decreasing in the logit (l - mx, the exp and the
+// division by s each are), so the m-th largest probability is p(L) of the m-th
+// largest logit L, found among the listed ones, and the entries whose
+// probability reaches p(L) are those whose logit is at least l_lo, the lowest
+// float with p(l_lo) == p(L) (a bisection on the float's bits).  When l_lo is
+// at or above the bound they are all listed: taken with their probabilities,
+// sorted by (probability desc, index asc), the first m written.  (Equal
+// probabilities can come from different logits: the exp and the division
+// round, so the order cannot be taken from the logits.)
+// Otherwise (m > 1024, a full list, l_lo below the bound, s not a number) the
+// row is read again: the entries at or above l_lo found by an exact radix
+// select on the logits, or -- when they are many, or s is NaN -- an exact
+// radix select on the probabilities themselves and, among the entries equal
+// to the m-th, the lowest indices (a second select on the index), as the
+// stable sort keeps them.
 // A row holding NaN, or +inf with anything else, has NaN probabilities; the
 // reference's comparator is no order on NaN, so such rows are outside the
 // parity claim (this kernel then returns the first indices).
+namespace {
+constexpr int kTopPer = 8;                      // logits per thread and chunk of the sum
+constexpr int kTopCh = kTopThreads * kTopPer;   // 8192 exponentials in LDS
+constexpr int kTopList = 2048;                  // logits listed at or above the bound
+}  // namespace
+
 template <int NT>
 __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict__ logits, int64_t V,
                                                         int n, int32_t* __restrict__ ids,
                                                         float* __restrict__ probs) {
   constexpr int NW = NT / kWave;
-  static_assert((size_t)kTopChunk * 2 * sizeof(float) >= (size_t)kTopMaxN * sizeof(uint64_t),
-                "the members reuse the chunk buffers");
-  __shared__ __align__(16) float ebuf[2][kTopChunk];
+  static_assert((size_t)kTopCh * sizeof(float) >= (size_t)kTopMaxN * 2 * sizeof(uint64_t),
+                "the members (and the fallback's candidates) reuse the exponentials' buffer");
+  static_assert(NT == kTopThreads && kTopPer % 4 == 0, "chunk layout");
+  __shared__ __align__(16) float ebuf[kTopCh];
+  __shared__ uint64_t list[kTopList];
   __shared__ uint32_t hist[kSelWords];
   __shared__ int smem[NW + 4];
   __shared__ float s_part[NW];
-  __shared__ float s_sum;
   __shared__ int s_cnt;
+  __shared__ SeqSumShared sh;
   const int row = (int)blockIdx.x;
   const int tid = (int)threadIdx.x;
   const int lane = lane_id();
   const int wv = tid >> 6;
+  const int nV = (int)V;  // V < 2^29 (checked by the host)
   const float* __restrict__ x = logits + (int64_t)row * V;
-  const __amdgpu_buffer_rsrc_t xr = slice_rsrc(x, (int)V);  // V < 2^29 (checked by the host)
+  const __amdgpu_buffer_rsrc_t xr = slice_rsrc(x, nV);
   const int m = (int)min((int64_t)n, V);  // 1 <= m <= kTopMaxN (checked by the host)
   for (int q = tid; q < kSelWords; q += NT) hist[q] = 0u;
-  // fn(i, l, in) over the row, eight requests per thread in flight at a time
-  // (past the row they read 0 with in == false); every lane makes the same
-  // number of calls
+  // 16-byte loads when every row start is 16-byte aligned; element of slot q
+  // of this thread in the chunk at c0: float4 group tid + (q / 4) * NT, or
+  // element tid + q * NT
+  const bool vec = (nV % 4 == 0) && ((reinterpret_cast<uintptr_t>(logits) & 15) == 0);
+  auto elem = [&](int c0, int q) -> int {
+    return vec ? c0 + 4 * (tid + (q >> 2) * NT) + (q & 3) : c0 + tid + q * NT;
+  };
+  auto load = [&](int c0, float (&v)[kTopPer]) __attribute__((always_inline)) {
+    if (vec) {
+#pragma unroll
+      for (int g = 0; g < kTopPer / 4; ++g) {
+        const int e0 = c0 + 4 * (tid + g * NT);
+        const f32x4 t = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, e0 < nV ? e0 * 4 : 0x7ffffff0, 0, 0));
+        v[4 * g] = t.x;
+        v[4 * g + 1] = t.y;
+        v[4 * g + 2] = t.z;
+        v[4 * g + 3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < kTopPer; ++q) {
+        const int e = c0 + tid + q * NT;
+        v[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, e < nV ? e * 4 : 0x7ffffff0, 0, 0));
+      }
+    }
+  };
+  // fn(i, l, in) over the row for the fallback's passes, eight requests per
+  // thread in flight at a time (past the row they read 0 with in == false);
+  // every lane makes the same number of calls
   constexpr int kScanU = 8;
   auto row_scan = [&](auto fn) __attribute__((always_inline)) {
-    for (int i0 = 0; i0 < (int)V; i0 += NT * kScanU) {
+    for (int i0 = 0; i0 < nV; i0 += NT * kScanU) {
       float l[kScanU];
 #pragma unroll
       for (int u = 0; u < kScanU; ++u) {
         const int i = i0 + u * NT + tid;
         l[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                             xr, i < (int)V ? i * 4 : 0x7ffffff0, 0, 0));
+                                             xr, i < nV ? i * 4 : 0x7ffffff0, 0, 0));
       }
 #pragma unroll
       for (int u = 0; u < kScanU; ++u) {
         const int i = i0 + u * NT + tid;
-        fn(i, l[u], i < (int)V);
+        fn(i, l[u], i < nV);
       }
     }
   };
 
-  // (1) mx (:53): nim's max(mx, v) takes v when mx <= v, so NaN is never
-  // taken; the float maximum of the rest (its sign of zero changes no l - mx)
+  // (1) mx and each thread's largest logit key (the next chunk requested
+  // before the current one is reduced)
   float mx = -__builtin_inff();
-  row_scan([&](int, float l, bool in) { mx = in ? __builtin_fmaxf(mx, l) : mx; });
+  uint32_t tk = 0u;
+  {
+    float a[kTopPer], b[kTopPer];
+    load(0, a);
+    for (int c0 = 0; c0 < nV; c0 += kTopCh) {
+      const bool more = c0 + kTopCh < nV;
+      if (more) load(c0 + kTopCh, b);
+#pragma unroll
+      for (int q = 0; q < kTopPer; ++q)
+        if (elem(c0, q) < nV) {
+          mx = __builtin_fmaxf(mx, a[q]);
+          tk = max(tk, f2key(a[q]));
+        }
+      if (more) {
+#pragma unroll
+        for (int q = 0; q < kTopPer; ++q) a[q] = b[q];
+      }
+    }
+  }
   for (int o = kWave / 2; o > 0; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o));
   if (lane == 0) s_part[wv] = mx;
   __syncthreads();
   mx = s_part[0];
   for (int w = 1; w < NW; ++w) mx = __builtin_fmaxf(mx, s_part[w]);
-
-  // (2) s = e_0 + e_1 + ... in index order (:54-56): chunk c is computed by
-  // waves 1.. into ebuf[c & 1] while lane 0 of wave 0 adds chunk c - 1
-  const int64_t nch = (V + kTopChunk - 1) / kTopChunk;
-  float s = 0.0f;
-  for (int64_t c = 0; c <= nch; ++c) {
-    if (wv != 0 && c < nch) {
-      // every producer thread's loads go out together (past the row they read 0)
-      constexpr int PP = (kTopChunk + NT - kWave - 1) / (NT - kWave);
-      const int c0 = (int)(c * kTopChunk);
-      float* eb = ebuf[c & 1];
-      float lv[PP];
-#pragma unroll
-      for (int q = 0; q < PP; ++q) {
-        const int j = tid - kWave + q * (NT - kWave);
-        lv[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                              xr, j < kTopChunk ? (c0 + j) * 4 : 0x7ffffff0, 0, 0));
-      }
-#pragma unroll
-      for (int q = 0; q < PP; ++q) {
-        const int j = tid - kWave + q * (NT - kWave);
-        if (j < kTopChunk) eb[j] = c0 + j < V ? expf_cr(lv[q] - mx) : 0.0f;
-      }
-    }
-    if (wv == 0 && c > 0 && lane == 0) {
-      // the whole chunk: entries past the row are +0, which leave s unchanged
-      const f32x4* e4 = reinterpret_cast<const f32x4*>(ebuf[(c - 1) & 1]);
-      // blocks of 16; the reads of the block two ahead are issued before the
-      // adds of the current one (the barrier keeps the compiler from sinking
-      // them), so the adds never wait for the LDS
-      constexpr int nb = kTopChunk / 16;
-      constexpr int kLast = nb - 1;
-      f32x4 a[4], b[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        a[q] = e4[q];
-        b[q] = e4[4 + q];
-      }
-#pragma unroll 8
-      for (int blk = 0; blk < nb; ++blk) {
-        const int nx = min(blk + 2, kLast) * 4;
-        f32x4 t[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) t[q] = e4[nx + q];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          s = s + a[q].x;
-          s = s + a[q].y;
-          s = s + a[q].z;
-          s = s + a[q].w;
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          a[q] = b[q];
-          b[q] = t[q];
-        }
-      }
-    }
-    __syncthreads();
+  // the bound: the m-th largest thread maximum, when at least m threads hold
+  // an element (else every element is listed)
+  uint32_t t0 = 0u;
+  const int holders = vec ? min(NT, (nV + 3) / 4) : min(NT, nV);
+  if (m <= holders) {
+    const SelectResult b0 = block_select<NT>([&](auto fn) { fn(tk, tid < holders); }, m, -1, hist, smem);
+    t0 = b0.tau;
   }
-  if (tid == 0) s_sum = s;
+  seq_sum_init(sh);
+  if (tid == 0) s_cnt = 0;
   __syncthreads();
-  s = s_sum;
-  // probs[i] /= s (:57)
-  auto pkey = [&](float l) -> uint32_t { return f2key(expf_cr(l - mx) / s); };
 
-  uint64_t* mem = reinterpret_cast<uint64_t*>(&ebuf[0][0]);
+  // (2) s = e_0 + e_1 + ... in index order (:54-56), listing the logits >= t0
+  float s = 0.0f;
+  {
+    int J = 1, nwin = 0;
+    float v[kTopPer];
+    load(0, v);
+    for (int c0 = 0; c0 < nV; c0 += kTopCh) {
+#pragma unroll
+      for (int q = 0; q < kTopPer; ++q) {
+        const int e = elem(c0, q);
+        if (e < nV) {
+          ebuf[e - c0] = expf_cr(v[q] - mx);
+          const uint32_t k = f2key(v[q]);
+          if (m <= NT && k >= t0) {
+            const int slot = atomicAdd(&s_cnt, 1);
+            if (slot < kTopList) list[slot] = ((uint64_t)k << 32) | (uint32_t)e;
+          }
+        }
+      }
+      __syncthreads();
+      if (c0 + kTopCh < nV) load(c0 + kTopCh, v);
+      s = seq_sum_block<NT>(ebuf, min(kTopCh, nV - c0), s, J, nwin, c0, sh);  // ends with a barrier
+    }
+  }
+  const int nl = s_cnt;
+  // probs[i] /= s (:57)
+  auto prob_of = [&](float l) -> float { return expf_cr(l - mx) / s; };
+  auto pkey = [&](float l) -> uint32_t { return f2key(prob_of(l)); };
+
+  uint64_t* mem = reinterpret_cast<uint64_t*>(ebuf);
   constexpr int kCand = (int)(sizeof(ebuf) / sizeof(uint64_t));
   auto emit = [&](int cnt) {  // mem[0..cnt): key << 32 | ~index; the first m, sorted, out
     const int np = next_pow2(cnt);
@@ -170,30 +206,60 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
       probs[(int64_t)row * n + j] = key2f((uint32_t)(e >> 32));
     }
   };
-  // (3) The probability is non-decreasing in the logit (l - mx, the exp and
-  // the division by s each are), so the m-th largest probability is p(L) of
-  // the m-th largest logit L, and the entries whose probability reaches it are
-  // exactly those whose logit is at least l_lo, the lowest float with
-  // p(l_lo) == p(L).  With s a number (no NaN or +inf in the row) those few
-  // are gathered with their probabilities and sorted.  Rows where they are
-  // many fall through to the selection on the probabilities below.
-  auto prob_of = [&](float l) -> float { return expf_cr(l - mx) / s; };
+  // the lowest key in [key(-inf), key(L)] whose probability reaches p(L)
+  auto lowest_key = [&](uint32_t kL) -> uint32_t {
+    const float pm = prob_of(key2f(kL));
+    uint32_t lo = f2key(-__builtin_inff()), hi = kL;
+    while (lo < hi) {
+      const uint32_t mid = lo + (hi - lo) / 2;
+      if (prob_of(key2f(mid)) >= pm)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    return hi;
+  };
+  if (s == s && m <= NT && nl <= kTopList) {  // uniform
+    // L among the listed logits (it is one of them: L >= t0)
+    const SelectResult sl = block_select<NT>(
+        [&](auto fn) {
+          for (int i0 = 0; i0 < kTopList; i0 += NT) {
+            const int i = i0 + tid;
+            const bool in = i < nl;
+            fn(in ? (uint32_t)(list[i] >> 32) : 0u, in);
+          }
+        },
+        m, -1, hist, smem);
+    if (tid == 0) {
+      smem[NW] = (int)lowest_key(sl.tau);
+      s_cnt = 0;
+    }
+    __syncthreads();
+    const uint32_t klo = (uint32_t)smem[NW];
+    if (klo >= t0) {  // uniform: every entry at or above l_lo is listed
+      for (int i = tid; i < nl; i += NT) {
+        const uint64_t le = list[i];
+        const uint32_t k = (uint32_t)(le >> 32);
+        if (k >= klo) {
+          const int slot = atomicAdd(&s_cnt, 1);
+          mem[slot] = ((uint64_t)f2key(prob_of(key2f(k))) << 32) | (0xffffffffu - (uint32_t)le);
+        }
+      }
+      __syncthreads();
+      emit(s_cnt);
+      return;
+    }
+    __syncthreads();
+  }
+  // (3) the fallback.  With s a number: the entries whose logit reaches
+  // l_lo, found by a select over the whole row, gathered and sorted when they
+  // fit.
   if (s == s) {  // uniform
     const SelectResult sl = block_select<NT>(
         [&](auto fn) { row_scan([&](int, float l, bool in) { fn(in ? f2key(l) : 0u, in); }); }, m, -1,
         hist, smem);
     if (tid == 0) {
-      // the lowest key in [key(-inf), key(L)] whose probability reaches p(L)
-      const float pm = prob_of(key2f(sl.tau));
-      uint32_t lo = f2key(-__builtin_inff()), hi = sl.tau;
-      while (lo < hi) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        if (prob_of(key2f(mid)) >= pm)
-          hi = mid;
-        else
-          lo = mid + 1;
-      }
-      smem[NW] = (int)hi;
+      smem[NW] = (int)lowest_key(sl.tau);
       s_cnt = 0;
     }
     __syncthreads();
