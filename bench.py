@@ -508,14 +508,14 @@ def phase_stamps(args):
     for name, v in rows.items():
         v = v[ok]
         print(f"| {name} | {np.median(v):.2f} | {np.percentile(v, 10):.2f} | {np.percentile(v, 90):.2f} |")
-    print(f"candidates above the shared bound per row (median / p90 / max): {np.median(P[ok, 12]):.0f} / "
-          f"{np.percentile(P[ok, 12], 90):.0f} / {P[ok, 12].max()}; above the offers' bound: "
+    print(f"candidates at or above the shared bound per row (median / p90 / max): {np.median(P[ok, 12]):.0f} / "
+          f"{np.percentile(P[ok, 12], 90):.0f} / {P[ok, 12].max()}; listed patched ids: "
           f"{np.median(P[ok, 13]):.0f} / {np.percentile(P[ok, 13], 90):.0f} / {P[ok, 13].max()}")
     def key2f(k):
         k = np.uint32(k)
         b = (k & 0x7fffffff) if (k & 0x80000000) else (~k & 0xffffffff)
         return float(np.array([b], np.uint32).view(np.float32)[0])
-    print(f"bootstrap bound (median): {key2f(int(np.median(P[ok, 14]))):.4f}; offers' bound: "
+    print(f"bootstrap bound (median): {key2f(int(np.median(P[ok, 14]))):.4f}; final shared bound: "
           f"{key2f(int(np.median(P[ok, 15]))):.4f}")
     print(f"kernel span (first start to last end): {us(P[ok, 11].max() - t0):.2f} us")
     if D[ok, 0].max() > 0:

@@ -256,6 +256,7 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
   __shared__ int s_next;                       // next unclaimed chunk
   __shared__ int s_nf;                         // entries in the candidate list
   __shared__ int s_rank[kK64RankCap];          // each candidate's rank, summed over four threads
+  __shared__ int s_mcnt;                       // members placed by the workgroup select
   __shared__ int s_wn[kNW];                    // entries each wave kept (-1: its buffer overflowed)
   __shared__ uint32_t s_off[kWave];            // each wave's kM0 largest kept keys, at its hand-in
   __shared__ __align__(16) uint64_t s_flist[kWave];  // the last wave's candidates above its bound
@@ -961,14 +962,26 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
       const int r = s_rank[tid];
       if (r < kWave) s_flist[r] = cand[tid];
     }
+    // A list longer than the rank table (a flat top of the row: many values
+    // near the k-th): the heap rule's k members by a workgroup radix select
+    // over the list, into the wave buffers (free now).
+    bool sel_done = false;
+    if (!ovf && s_ovf == 0 && N > kK64RankCap && N >= kk) {  // uniform
+      if (tid == 0) s_mcnt = 0;
+      __syncthreads();
+      sel_done = topk_members<kNT>(cand, N, kk, wbuf, kNW * kWaveCap, whist, smem, &s_mcnt);  // uniform
+      if (sel_done && tid < kk) s_flist[tid] = wbuf[tid];
+    }
     __syncthreads();
     NLS_STAMP(row, 6);
     if (wv != 0) return;
     // wave 0: the members in order; ties at the k-th value beyond k take the
     // heap rule's closed form
-    bool rovf = !rank_ok;
+    bool rovf = !rank_ok && !sel_done;
     uint64_t x = 0ull;
-    if (!rovf) {
+    if (sel_done) {
+      x = rank_sort64(s_flist, kk);
+    } else if (!rovf) {
       const int nl = min(N, kWave);  // s_flist[0..nl) holds ranks 0..nl-1
       x = lane < nl ? s_flist[lane] : 0ull;
       const uint32_t T = (uint32_t)__builtin_amdgcn_readlane((int)(x >> 32), kk - 1);

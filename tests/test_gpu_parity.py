@@ -310,6 +310,35 @@ def test_long_windows_full_batch(pkg, torch, B, V, k):
     assert us < 5000.0, us
 
 
+def test_k64_long_candidate_lists(pkg, torch):
+    """Top-k rows (k <= 64) whose candidate list at the end of the stream is
+    longer than the rank table (the penalties recipe at V = 151936 with the
+    benchmark's seed) take the workgroup select over the list, not the
+    whole-row path; rows with a flat top (logits on a coarse grid, whose ties
+    can also fill a wave's buffer and hand the row on) stay exact; every row
+    against the oracle."""
+    from nimllm_amd import workloads
+
+    rng = np.random.default_rng(2024)
+    B, V = 64, 128256
+    x = (np.round(rng.standard_normal((B, V)) * 2.0) / 2.0).astype(np.float32)
+    plist = [dict(temperature=1.0, topK=[50, 64, 20, 33][b % 4], topP=0.95, minP=0.0, repeatPenalty=1.0,
+                  repeatLastN=0, presencePenalty=0.0, frequencyPenalty=0.0, seed=1) for b in range(B)]
+    u = rng.random(B)
+    say(f"[k64_long_lists] grid rows B={B} V={V}")
+    ids, dbg = run_gpu(pkg, torch, x, [to_pkg_params(pkg, p, {}) for p in plist], None, u, debug_cap=64)
+    say(f"[k64_long_lists] grid rows: paths {np.bincount(dbg['path'], minlength=6).tolist()}")
+    compare_rows(x, plist, [[] for _ in range(B)], [{} for _ in range(B)], u, ids, dbg, "grid")
+    w = workloads.make("penalties_152k", seed=1234)
+    say(f"[k64_long_lists] penalties_152k seed 1234 B={w.B} V={w.V}")
+    ids, dbg = run_gpu(pkg, torch, w.logits, workloads.sampler_params(w, pkg), w.hist, w.u, debug_cap=64)
+    assert np.all(dbg["path"] == 2), np.bincount(dbg["path"], minlength=6).tolist()
+    bid, bval, bcnt = w.bias_arrays()
+    ref = O.sample_batch([O.make_params(**r.as_kwargs()) for r in w.rows], w.logits, w.hist,
+                         np.full(w.B, w.hist.shape[1]), bid, bval, bcnt, w.u, O.EXPF_CR, nthreads=8)
+    assert np.array_equal(ids, ref), np.nonzero(ids != ref)[0][:10]
+
+
 def test_golden_fixtures(pkg, torch):
     import json
     import os
