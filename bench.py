@@ -478,7 +478,32 @@ def phase_stamps(args):
         if L.nls_phase_stamps(which, buf.ctypes.data_as(ctypes.c_void_p)) != 0:
             raise SystemExit("nls_phase_stamps failed")
         st[which] = buf.reshape(4096, 16)[:w.B].astype(np.int64).copy()
+    buf[:] = 0
+    if L.nls_generic_stamps(buf.ctypes.data_as(ctypes.c_void_p)) != 0:
+        raise SystemExit("nls_generic_stamps failed")
+    G = buf.reshape(4096, 16)[:w.B].astype(np.int64).copy()
     s.close()
+    gok = (G[:, 0] > 0) & (G[:, 7] > 0)
+    if gok.any():
+        g0 = G[gok, 0].min()
+        grows = {
+            "start after the first grouped row": (G[:, 0] - g0) / 100.0,
+            "zero tables, patch table": (G[:, 1] - G[:, 0]) / 100.0,
+            "pass 1: row maximum": (G[:, 2] - G[:, 1]) / 100.0,
+            "pass 2: count distinct values": (G[:, 3] - G[:, 2]) / 100.0,
+            "sort the groups": (G[:, 4] - G[:, 3]) / 100.0,
+            "softmax sum over groups": (G[:, 5] - G[:, 4]) / 100.0,
+            "top-p / min-p / draw over groups": (G[:, 6] - G[:, 5]) / 100.0,
+            "pass 3: the drawn member": (G[:, 7] - G[:, 6]) / 100.0,
+            "row total": (G[:, 7] - G[:, 0]) / 100.0,
+        }
+        print(f"# grouped path (whole-row kernel) phases, {int(gok.sum())} rows")
+        print("| Phase | median us | p10 | p90 |")
+        print("|---|---|---|---|")
+        for name, v in grows.items():
+            v = v[gok]
+            print(f"| {name} | {np.median(v):.2f} | {np.percentile(v, 10):.2f} | {np.percentile(v, 90):.2f} |")
+        print(f"grouped rows' span (first start to last end): {(G[gok, 7].max() - g0) / 100.0:.2f} us")
     P, W, D = st[0], st[1], st[2]
     us = lambda d: d / 100.0  # 100 MHz counter
     t0 = P[:, 0].min()
@@ -501,6 +526,9 @@ def phase_stamps(args):
         "workgroup total": us(P[:, 11] - P[:, 0]),
     }
     ok = (P[:, 11] > 0) & (P[:, 7] > 0)
+    if not ok.any():
+        print(f"# no k64_kernel rows with every stamp in workload {args.workload}")
+        return
     print(f"# k64_kernel phases, workload {args.workload} (B={w.B} V={w.V}), last of {args.steps} calls; "
           f"{int(ok.sum())} rows with every stamp")
     print("| Phase | median us | p10 | p90 |")

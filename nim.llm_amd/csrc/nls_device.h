@@ -46,6 +46,12 @@ constexpr int kStampRows = 4096;
 static __device__ uint64_t nls_phase_stamp[kStampRows * 16];
 static __device__ uint64_t nls_wave_stamp[kStampRows * 16];
 static __device__ uint64_t nls_detail_stamp[kStampRows * 16];
+static __device__ uint64_t nls_gen_stamp[kStampRows * 16];  // the grouped path's phases, per row
+#define NLS_GSTAMP(row, i)                                                                       \
+  do {                                                                                           \
+    if (threadIdx.x == 0 && (row) < kStampRows)                                                 \
+      nls_gen_stamp[(row) * 16 + (i)] = __builtin_amdgcn_s_memrealtime();                        \
+  } while (0)
 #define NLS_STAMP(row, i)                                                                        \
   do {                                                                                           \
     if (__lane_id() == 0 && (row) < kStampRows)                                                 \
@@ -71,6 +77,9 @@ static __device__ uint64_t nls_detail_stamp[kStampRows * 16];
       nls_wave_stamp[(row) * 16 + (w)] = __builtin_amdgcn_s_memrealtime();                       \
   } while (0)
 #else
+#define NLS_GSTAMP(row, i) \
+  do {                     \
+  } while (0)
 #define NLS_STAMP(row, i) \
   do {                    \
   } while (0)
@@ -1895,6 +1904,7 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   res.n = 0;
   res.total = 0.0f;
 
+  NLS_GSTAMP(row, 0);
   for (int i = tid; i < nw; i += NT) L.bitmap[i] = 0u;
   for (int i = tid; i < kGrpHashCap; i += NT) {
     L.hkey[i] = kGrpEmpty;
@@ -1980,102 +1990,58 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     L.pfin[sl] = v * P.invT;  // (:80-81)
   }
   __syncthreads();
-  // ---- the row maximum (:53) over the final values ----
+  NLS_GSTAMP(row, 1);
   const bool vec = (V % 4 == 0) && ((reinterpret_cast<uintptr_t>(src) & 15) == 0);
   const float4* __restrict__ src4 = reinterpret_cast<const float4*>(src);
   const float invT = P.invT;
-  // Visit every final value once: unpatched ones from the row, patched ones
-  // from the patch table.  f(v) gets the value; f returns false to stop early.
   const int V4 = V >> 2;
-  auto for_each_final = [&](auto&& f) {
-    if (vec) {
-      // four 16-byte loads in flight per thread
-      for (int b4 = tid; b4 < V4; b4 += 4 * NT) {
-        float4 x[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i4 = b4 + u * NT;
-          x[u] = src4[min(i4, V4 - 1)];
-        }
-        bool go = true;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i4 = b4 + u * NT;
-          if (i4 < V4) {
-            const uint32_t pb = (L.bitmap[i4 >> 3] >> ((i4 & 7) * 4)) & 15u;
-            if (!(pb & 1u)) go &= f(x[u].x * invT);
-            if (!(pb & 2u)) go &= f(x[u].y * invT);
-            if (!(pb & 4u)) go &= f(x[u].z * invT);
-            if (!(pb & 8u)) go &= f(x[u].w * invT);
-          }
-        }
-        if (!go) break;
-      }
-    } else {
-      for (int i = tid; i < V; i += NT) {
-        if ((L.bitmap[i >> 5] >> (i & 31)) & 1u) continue;
-        if (!f(src[i] * invT)) break;
-      }
-    }
-    for (int sl = tid; sl < np; sl += NT)
-      if (!f(L.pfin[sl])) break;
-  };
-  uint32_t kmax = 0u;
-  bool nan = false;
-  for_each_final([&](float v) {
-    nan |= (v != v);
-    kmax = max(kmax, f2key(v));
-    return true;
-  });
-  kmax = wave_max_u32(kmax);
-  const uint64_t nb = __ballot(nan);
-  if (lane == 0) {
-    s_wmax[tid >> 6] = kmax;
-    s_wnan[tid >> 6] = nb != 0ull;
-  }
-  __syncthreads();
-  uint32_t mk = 0u;
-  int anynan = 0;
-  for (int q = 0; q < NW; ++q) {
-    mk = max(mk, s_wmax[q]);
-    anynan |= s_wnan[q];
-  }
-  const float mx = key2f(mk);
-  if (anynan || !(mx > -__builtin_inff() && mx < __builtin_inff())) return res;
-  // ---- count every value that can move the sum ----
+  // ---- the row maximum (:53) and the values that can move the sum ----
+  // Counting needs the maximum: a value counts when fl(v - mx) >= kGroupFloor.
+  // One fused pass counts every value within kGroupFloor of a running
+  // maximum instead (the workgroup's, shared through LDS after each step):
+  // the running maximum never exceeds mx, so every occurrence of a needed
+  // value is counted, and the values that fall below the final floor are
+  // dropped afterwards.  A table that fills (a row whose running maximum
+  // rose late over many distinct values) is counted again in two passes.
   // Eight values at a time (the kernel runs at its register limit): their
   // table slots are read together, a value already in the table at its first
   // slot is counted with one atomic add, and only the others (first
   // occurrences, collisions) probe.
-  {
-    bool bad = false;
-    auto count8 = [&](const float* vv, uint32_t want) __attribute__((always_inline)) {
-      uint32_t hs[8], cur[8];
+  bool bad = false;
+  auto count8 = [&](const float* vv, uint32_t want) __attribute__((always_inline)) {
+    uint32_t hs[8], cur[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) hs[q] = (f2key(vv[q]) * 0x9E3779B1u) >> (32 - kGrpHashBits);
+    for (int q = 0; q < 8; ++q) hs[q] = (f2key(vv[q]) * 0x9E3779B1u) >> (32 - kGrpHashBits);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) cur[q] = L.hkey[hs[q]];
+    for (int q = 0; q < 8; ++q) cur[q] = L.hkey[hs[q]];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        if (!((want >> q) & 1u)) continue;
-        const uint32_t key = f2key(vv[q]);
-        if (cur[q] == key)
-          atomicAdd(&L.hcnt[hs[q]], 1u);
-        else
-          bad |= !group_insert(L, key, &s_distinct);
-      }
-    };
-    auto count16 = [&](const float (&vv)[16], uint32_t want) __attribute__((always_inline)) {
-      count8(vv, want & 0xffu);
-      count8(vv + 8, want >> 8);
-    };
+    for (int q = 0; q < 8; ++q) {
+      if (!((want >> q) & 1u)) continue;
+      const uint32_t key = f2key(vv[q]);
+      if (cur[q] == key)
+        atomicAdd(&L.hcnt[hs[q]], 1u);
+      else
+        bad |= !group_insert(L, key, &s_distinct);
+    }
+  };
+  auto count16 = [&](const float (&vv)[16], uint32_t want) __attribute__((always_inline)) {
+    count8(vv, want & 0xffu);
+    count8(vv + 8, want >> 8);
+  };
+  // the row's final values 16 per thread at a time: fn(vv, in) with in's bit
+  // q set where vv[q] is an unpatched value of the row.  The loops run the
+  // same number of times on every lane of a wave (fn reduces over the wave)
+  // and stop when a lane has filled the table.
+  const int wbase = tid - lane;
+  auto for_each16 = [&](auto&& fn) __attribute__((always_inline)) {
     if (vec) {
-      for (int b4 = tid; b4 < V4 && !bad; b4 += 4 * NT) {
+      for (int w4 = wbase; w4 < V4; w4 += 4 * NT) {
+        const int b4 = w4 + lane;
         float4 x[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) x[u] = src4[min(b4 + u * NT, V4 - 1)];
         float vv[16];
-        uint32_t want = 0u;
+        uint32_t in = 0u;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int i4 = b4 + u * NT;
@@ -2084,26 +2050,96 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
           vv[4 * u + 1] = x[u].y * invT;
           vv[4 * u + 2] = x[u].z * invT;
           vv[4 * u + 3] = x[u].w * invT;
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (!((pb >> c) & 1u) && vv[4 * u + c] - mx >= kGroupFloor) want |= 1u << (4 * u + c);
+          in |= ((~pb) & 15u) << (4 * u);
         }
-        count16(vv, want);
+        fn(vv, in);
+        if (__ballot(bad)) break;
       }
     } else {
-      for (int b = tid; b < V && !bad; b += 16 * NT) {
+      for (int w0 = wbase; w0 < V; w0 += 16 * NT) {
+        const int b = w0 + lane;
         float vv[16];
-        uint32_t want = 0u;
+        uint32_t in = 0u;
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
           const int i = b + q * NT;
           vv[q] = i < V ? src[i] * invT : 0.0f;
-          if (i < V && !((L.bitmap[i >> 5] >> (i & 31)) & 1u) && vv[q] - mx >= kGroupFloor)
-            want |= 1u << q;
+          if (i < V && !((L.bitmap[i >> 5] >> (i & 31)) & 1u)) in |= 1u << q;
         }
-        count16(vv, want);
+        fn(vv, in);
+        if (__ballot(bad)) break;
       }
     }
+  };
+  __shared__ uint32_t s_rkey;  // the workgroup's running maximum (key)
+  if (tid == 0) s_rkey = f2key(-__builtin_inff());
+  __syncthreads();
+  bool nan = false;
+  float rmx = -__builtin_inff();
+  for (int sl = tid; sl < np; sl += NT) {
+    const float v = L.pfin[sl];
+    nan |= (v != v);
+    rmx = __builtin_fmaxf(rmx, v);
+  }
+  if (rmx > -__builtin_inff()) atomicMax(&s_rkey, f2key(rmx));
+  __syncthreads();
+  rmx = key2f(s_rkey);
+  for_each16([&](const float (&vv)[16], uint32_t in) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      if ((in >> q) & 1u) {
+        nan |= (vv[q] != vv[q]);
+        rmx = __builtin_fmaxf(rmx, vv[q]);
+      }
+    // share the running maximum (the read may lag: any value up to mx is sound)
+    const uint32_t wk = wave_max_u32(f2key(rmx));
+    if (lane == 0) atomicMax(&s_rkey, wk);
+    rmx = __builtin_fmaxf(rmx, key2f(s_rkey));
+    uint32_t want = 0u;
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      if (((in >> q) & 1u) && vv[q] - rmx >= kGroupFloor) want |= 1u << q;
+    count16(vv, want);
+  });
+  for (int sl = tid; sl < np && !bad; sl += NT) {
+    const float v = L.pfin[sl];
+    if (v - rmx >= kGroupFloor) bad |= !group_insert(L, f2key(v), &s_distinct);
+  }
+  // the row maximum: every thread's running maximum (NaN never taken)
+  const uint64_t nb = __ballot(nan);
+  const uint64_t bb = __ballot(bad);
+  const uint32_t wk = wave_max_u32(f2key(rmx));
+  if (lane == 0) {
+    s_wmax[tid >> 6] = wk;
+    s_wnan[tid >> 6] = (nb != 0ull ? 1 : 0) | (bb != 0ull ? 2 : 0);
+  }
+  __syncthreads();
+  uint32_t mk = 0u;
+  int flags = 0;
+  for (int q = 0; q < NW; ++q) {
+    mk = max(mk, s_wmax[q]);
+    flags |= s_wnan[q];
+  }
+  const float mx = key2f(mk);
+  NLS_GSTAMP(row, 2);
+  if ((flags & 1) || !(mx > -__builtin_inff() && mx < __builtin_inff())) return res;
+  if (flags & 2) {
+    // the table filled: count again against the final maximum
+    __syncthreads();
+    for (int i = tid; i < kGrpHashCap; i += NT) {
+      L.hkey[i] = kGrpEmpty;
+      L.hcnt[i] = 0u;
+    }
+    if (tid == 0) s_distinct = 0;
+    bad = false;
+    __syncthreads();
+    for_each16([&](const float (&vv)[16], uint32_t in) {
+      uint32_t want = 0u;
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        if (((in >> q) & 1u) && vv[q] - mx >= kGroupFloor) want |= 1u << q;
+      count16(vv, want);
+    });
     for (int sl = tid; sl < np && !bad; sl += NT) {
       const float v = L.pfin[sl];
       if (v - mx >= kGroupFloor) bad |= !group_insert(L, f2key(v), &s_distinct);
@@ -2111,10 +2147,13 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     if (bad) s_fail = 1;
   }
   __syncthreads();
+  NLS_GSTAMP(row, 3);
   if (s_fail) return res;
   for (int h = tid; h < kGrpHashCap; h += NT) {
     const uint32_t k = L.hkey[h];
-    if (k != kGrpEmpty) {
+    // (values counted against a running maximum that fall below the floor of
+    // the final one are dropped)
+    if (k != kGrpEmpty && key2f(k) - mx >= kGroupFloor) {
       const int at = atomicAdd(&s_G, 1);
       L.gsort[at] = ((uint64_t)(~k) << 32) | (uint64_t)L.hcnt[h];
     }
@@ -2125,6 +2164,7 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   for (int i = G + tid; i < Gp; i += NT) L.gsort[i] = ~0ull;
   __syncthreads();
   bitonic_sort_u64<NT>(L.gsort, Gp, false);  // descending value
+  NLS_GSTAMP(row, 4);
   // per group: its exponential (:56) and multiplicity (hash arrays reused)
   float* ge = reinterpret_cast<float*>(L.hkey);
   uint32_t* gc = L.hcnt;
@@ -2146,6 +2186,7 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     }
   }
   __syncthreads();
+  NLS_GSTAMP(row, 5);
   if (s_fail) return res;
   const float s = s_sum;
   for (int g = tid; g < G; g += NT) ge[g] = ge[g] / s;  // (:57)
@@ -2179,6 +2220,7 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     }
   }
   __syncthreads();
+  NLS_GSTAMP(row, 6);
   if (s_draw.status != kGroupOk) return res;
   // ---- the drawn candidate: the t-th lowest index holding value vg ----
   // Blocks of 64 lanes x W values (W = 4 with 16-byte loads): each wave
@@ -2295,6 +2337,7 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     __syncthreads();
     if (s_found) break;
   }
+  NLS_GSTAMP(row, 7);
   if (s_id < 0) return res;
   res.ok = 1;
   res.id = s_id;

@@ -17,3 +17,11 @@ hipError_t set_generic_attributes() {
 }
 
 }  // namespace nls
+
+#ifdef NLS_PHASE_STAMPS
+// The grouped path's phase stamps of this unit: [4096 x 16] uint64 (host).
+extern "C" int nls_generic_stamps(uint64_t* out) {
+  const size_t bytes = sizeof(uint64_t) * nls::kStampRows * 16;
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(nls::nls_gen_stamp), bytes) == hipSuccess ? 0 : 3;
+}
+#endif

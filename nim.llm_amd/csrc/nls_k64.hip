@@ -257,8 +257,6 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
   __shared__ int s_nf;                         // entries in the candidate list
   __shared__ int s_rank[kK64RankCap];          // each candidate's rank, summed over four threads
   __shared__ int s_mcnt;                       // members placed by the workgroup select
-  __shared__ int s_wn[kNW];                    // entries each wave kept (-1: its buffer overflowed)
-  __shared__ uint32_t s_off[kWave];            // each wave's kM0 largest kept keys, at its hand-in
   __shared__ __align__(16) uint64_t s_flist[kWave];  // the last wave's candidates above its bound
   __shared__ __align__(16) float s_chain[kWave];     // the tail's chains
   __shared__ int s_npl;                        // listed patched slots
