@@ -117,6 +117,18 @@ int nls_accept_row(nls_sampler* s, int32_t row, const int64_t* ids, int32_t coun
  * nls_sample output), without a host round trip.  d_ids: device [batch];
  * a row whose entry is NLS_ACCEPT_SKIP32 appends nothing. */
 int nls_accept_device(nls_sampler* s, const int32_t* d_ids);
+
+/* One step of batched generation (several contexts' decode loops sharing this
+ * handle, one row each; src/nimllm/chat.nim:204-208 per row): every row with
+ * d_done[b] == 0 samples as nls_sample does (d_u or the row's own RNG); a row
+ * whose id is one of the end-of-generation ids d_eog[0..n_eog) gets
+ * d_done[b] = 1 and accepts nothing, the others accept their id on the device.
+ * A row with d_done[b] != 0 on entry samples nothing, draws nothing from its
+ * RNG and gets d_out[b] = -1, as a finished context stops calling sample.
+ * d_done: device [batch], zeroed by the caller before the first step;
+ * d_eog: device [n_eog].  Asynchronous on the handle's stream. */
+int nls_generate_step(nls_sampler* s, const float* d_logits, const double* d_u, int32_t* d_out,
+                      const int32_t* d_eog, int32_t n_eog, int32_t* d_done);
 /* Drops every row's history (a fresh newSampler keeps none). */
 int nls_clear_history(nls_sampler* s);
 

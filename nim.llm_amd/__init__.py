@@ -32,7 +32,7 @@ ACCEPT_SKIP32 = -(1 << 31)
 EXPORTED = (
     "nls_default_sampling", "nls_greedy_sampling", "nls_create", "nls_destroy",
     "nls_set_stream", "nls_batch", "nls_vocab", "nls_accept", "nls_accept_row",
-    "nls_accept_device", "nls_clear_history", "nls_sample", "nls_sample_host",
+    "nls_accept_device", "nls_generate_step", "nls_clear_history", "nls_sample", "nls_sample_host",
     "nls_sample_host_noalloc",
     "nls_synchronize", "nls_rng_uniforms", "nls_get_rng_state", "nls_set_rng_state",
     "nls_top_tokens", "nls_row_nll", "nls_softmax_rows", "nls_log_prob", "nls_expf_device",
@@ -110,6 +110,7 @@ def lib():
         L.nls_accept.argtypes = [vp, P(ctypes.c_int64), ctypes.c_int32]
         L.nls_accept_row.argtypes = [vp, ctypes.c_int32, P(ctypes.c_int64), ctypes.c_int32]
         L.nls_accept_device.argtypes = [vp, vp]
+        L.nls_generate_step.argtypes = [vp, vp, vp, vp, vp, ctypes.c_int32, vp]
         L.nls_clear_history.argtypes = [vp]
         L.nls_sample.argtypes = [vp, vp, vp, vp, P(NlsDebug)]
         L.nls_sample_host.argtypes = [vp, P(ctypes.c_float), P(ctypes.c_int64)]
@@ -293,6 +294,29 @@ class BatchSampler:
                                ctypes.c_void_p(out.data_ptr()),
                                ctypes.byref(dbgp) if dbgp is not None else None), "nls_sample")
         return (out, dbg) if debug_cap > 0 else out
+
+    def generate_step(self, logits, eog, done, u=None, out=None):
+        """One step of batched generation (chat.nim:204-208 for every row): rows
+        with done == 0 sample; a row drawing an id in `eog` (int32 device
+        tensor) gets done = 1 and accepts nothing, the others accept their id.
+        Finished rows sample nothing (out = -1) and keep their RNG state.
+        `done`: int32 device tensor [B], zero before the first step.  Returns out."""
+        torch = self._torch
+        assert logits.is_cuda and logits.dtype == torch.float32 and logits.is_contiguous()
+        assert tuple(logits.shape) == (self.B, self.V)
+        assert done.is_cuda and done.dtype == torch.int32 and done.numel() == self.B and done.is_contiguous()
+        assert eog.is_cuda and eog.dtype == torch.int32 and eog.is_contiguous()
+        if u is not None:
+            assert u.is_cuda and u.dtype == torch.float64 and u.numel() == self.B and u.is_contiguous()
+        if out is None:
+            out = torch.empty(self.B, dtype=torch.int32, device=logits.device)
+        check(lib().nls_generate_step(self._h, ctypes.c_void_p(logits.data_ptr()),
+                                      ctypes.c_void_p(_ptr(u)) if u is not None else None,
+                                      ctypes.c_void_p(out.data_ptr()),
+                                      ctypes.c_void_p(eog.data_ptr()) if eog.numel() else None,
+                                      int(eog.numel()), ctypes.c_void_p(done.data_ptr())),
+              "nls_generate_step")
+        return out
 
     def sample_host(self, logits):
         """Blocking: host [B, V] float32 logits -> host int64 [B] ids."""

@@ -723,7 +723,7 @@ namespace {
 // One nls_sample call; may_alloc = false for the no-allocation entry point
 // (which then leaves handed-on rows to the streaming kernel's last workgroup).
 int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_t* d_out,
-                const nls_debug* dbg, bool may_alloc) {
+                const nls_debug* dbg, bool may_alloc, const int32_t* d_done = nullptr) {
   if (!s || !d_logits || !d_out) return NLS_ERR_INVALID_ARGUMENT;
   if (dbg && dbg->cap < 0) return NLS_ERR_INVALID_ARGUMENT;
   DebugPtrs dp;
@@ -811,6 +811,7 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   }
   a.done = s->done;
   a.hbits = s->hbits;
+  a.row_done = d_done;
   a.ga = ga;
   lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
   hipEvent_t e0 = s->prof_start, e1 = s->prof_stop, g0 = s->prof_gstart, g1 = s->prof_gstop;
@@ -824,6 +825,21 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
 int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t* d_out,
                const nls_debug* dbg) {
   return sample_impl(s, d_logits, d_u, d_out, dbg, true);
+}
+
+int nls_generate_step(nls_sampler* s, const float* d_logits, const double* d_u, int32_t* d_out,
+                      const int32_t* d_eog, int32_t n_eog, int32_t* d_done) {
+  if (!s || !d_logits || !d_out || !d_done || n_eog < 0 || (n_eog > 0 && !d_eog)) return NLS_ERR_INVALID_ARGUMENT;
+  int rc = s->ensure_history(-1, 1);
+  if (rc) return rc;
+  rc = sample_impl(s, d_logits, d_u, d_out, nullptr, true, d_done);
+  if (rc) return rc;
+  NLS_HIP(launch_generate_step(d_out, s->B, s->V, d_eog, n_eog, d_done, s->hist, s->hist_len, s->hcap, s->stream));
+  // rows that finished (or had finished) append nothing: the host lengths
+  // become upper bounds
+  for (int b = 0; b < s->B; ++b) s->h_len[b] += 1;
+  s->len_exact = false;
+  return NLS_OK;
 }
 
 int nls_profile_next(nls_sampler* s, void* start_event, void* stop_event) {

@@ -638,6 +638,10 @@ void stream_kernel(const StreamArgs a) {
     // the compiler that nothing in this kernel writes them.
     const RowParams P = load_const(a.rp + row);
     const int64_t hlen = load_const(a.hist_len + row);
+    if (a.row_done && load_const(a.row_done + row) != 0) {  // a finished row of a batched loop
+      if (sl == 0 && tid == 0) a.out[row] = -1;
+      return;
+    }
     if (P.mode == kModeFull || !P.fast) {
       if (sl == 0 && tid == 0) pushed = push_generic(a.generic_list, a.generic_count, row);
       return;

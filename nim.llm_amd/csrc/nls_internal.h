@@ -166,6 +166,7 @@ struct StreamArgs {
   int gen_inline;
   uint32_t* done;
   int hbits;    // k64_kernel: log2 of the patch hash table's slots
+  const int32_t* row_done;  // [B] or null: a nonzero row samples nothing (out = -1)
   GenericArgs ga;
 };
 
@@ -186,6 +187,10 @@ hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const Laun
                          hipEvent_t gev_stop);
 hipError_t launch_accept_host(const int32_t* d_ids, const int32_t* d_cnt, int B, int count,
                               int32_t* hist, int64_t* hist_len, int hcap, int row_only, hipStream_t s);
+// one batched generation step after the sampling: rows not done finish on an
+// end-of-generation id, else accept theirs
+hipError_t launch_generate_step(const int32_t* d_out, int B, int64_t V, const int32_t* eog, int n_eog,
+                                int32_t* row_done, int32_t* hist, int64_t* hist_len, int hcap, hipStream_t s);
 hipError_t launch_accept_device(const int32_t* d_ids, int B, int64_t V, int32_t* hist,
                                 int64_t* hist_len, int hcap, hipStream_t s);
 hipError_t launch_expf(const float* x, float* y, int64_t n, hipStream_t s);

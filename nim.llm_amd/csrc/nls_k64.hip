@@ -335,6 +335,10 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
     __builtin_amdgcn_sched_barrier(0);  // keep the requests here
     const RowParams P = load_const(a.rp + row);
     const int64_t hlen = load_const(a.hist_len + row);
+    if (a.row_done && load_const(a.row_done + row) != 0) {  // a finished row of a batched loop
+      if (tid == 0) a.out[row] = -1;
+      return;
+    }
     double u_in = 0.0;
     uint64_t st0 = 0ull, st1 = 0ull;
     if (a.d_u) {

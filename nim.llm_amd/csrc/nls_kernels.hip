@@ -433,6 +433,27 @@ __global__ void accept_device_kernel(const int32_t* __restrict__ ids, int B, int
   hist_len[b] = len + 1;
 }
 
+// One step of batched generation after nls_sample (chat.nim:204-208 per
+// row): a row not yet done whose id is an end-of-generation id finishes (the
+// id is not accepted); the others accept their id into the history ring
+// (out-of-range ids take a -1 slot, as accept_device_kernel stores them).
+__global__ void generate_step_kernel(const int32_t* __restrict__ out, int B, int64_t V,
+                                     const int32_t* __restrict__ eog, int n_eog, int32_t* __restrict__ row_done,
+                                     int32_t* __restrict__ hist, int64_t* __restrict__ hist_len, int hcap) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B || row_done[b] != 0) return;
+  int32_t id = out[b];
+  for (int j = 0; j < n_eog; ++j)
+    if (eog[j] == id) {
+      row_done[b] = 1;
+      return;
+    }
+  const int64_t len = hist_len[b];
+  if (id < 0 || id >= V) id = -1;
+  hist[(int64_t)b * hcap + (int)(len % hcap)] = id;
+  hist_len[b] = len + 1;
+}
+
 __global__ void expf_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = expf_cr(x[i]);
@@ -467,6 +488,13 @@ hipError_t launch_accept_host(const int32_t* d_ids, const int32_t* d_cnt, int B,
                               int32_t* hist, int64_t* hist_len, int hcap, int row_only, hipStream_t s) {
   hipLaunchKernelGGL(accept_host_kernel, dim3(row_only >= 0 ? 1 : B), dim3(256), 0, s, d_ids, d_cnt,
                      count, hist, hist_len, hcap, row_only);
+  return hipGetLastError();
+}
+
+hipError_t launch_generate_step(const int32_t* d_out, int B, int64_t V, const int32_t* eog, int n_eog,
+                                int32_t* row_done, int32_t* hist, int64_t* hist_len, int hcap, hipStream_t s) {
+  hipLaunchKernelGGL(generate_step_kernel, dim3((B + 255) / 256), dim3(256), 0, s, d_out, B, V, eog, n_eog,
+                     row_done, hist, hist_len, hcap);
   return hipGetLastError();
 }
 

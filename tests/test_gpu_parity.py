@@ -581,6 +581,55 @@ def test_batched_generate_loop_skips_end_of_generation(pkg, torch):
     assert skipped > 0
 
 
+def test_generate_step_batched_contexts(pkg, torch):
+    """nls_generate_step: several contexts' decode loops in one handle, one
+    row each (chat.nim:204-208 per row): rows sample with their own RNG
+    streams (u = NULL), a row drawing an end-of-generation id finishes without
+    accepting it, finished rows sample nothing (-1) and keep their RNG;
+    checked step by step against per-row oracle loops."""
+    rng = np.random.default_rng(404)
+    V, B, steps = 3000, 6, 30
+    eog = [7, 11, V - 1]
+    say(f"[generate_step] V={V} B={B} steps={steps}")
+    plist = [dict(temperature=[0.9, 0.0, 1.1, 0.7, 1.0, 0.8][b], topK=[40, 0, 0, 300, 5, 0][b],
+                  topP=[0.95, 1.0, 0.9, 1.0, 1.0, 0.8][b], minP=[0.0, 0.0, 0.05, 0.0, 0.0, 0.1][b],
+                  repeatPenalty=1.3, repeatLastN=[0, 8, 16, 0, 4, 0][b], presencePenalty=0.2,
+                  frequencyPenalty=0.4, seed=[3, 0, 17, 99, 5, 2024][b]) for b in range(B)]
+    s = pkg.BatchSampler([to_pkg_params(pkg, p, {}) for p in plist], V)
+    streams = [list(O.uniforms(plist[b]["seed"], steps)) for b in range(B)]
+    used = [0] * B
+    hist = [[] for _ in range(B)]
+    done = [False] * B
+    d_done = torch.zeros(B, dtype=torch.int32, device="cuda")
+    d_eog = torch.tensor(eog, dtype=torch.int32, device="cuda")
+    try:
+        for t in range(steps):
+            x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+            # make end-of-generation ids likely on some rows at some steps
+            if t % 7 == 3:
+                x[t % B, eog[t % 3]] += 12.0
+            out = s.generate_step(torch.from_numpy(x).cuda(), d_eog, d_done).cpu().numpy()
+            got_done = d_done.cpu().numpy()
+            for b in range(B):
+                if done[b]:
+                    assert out[b] == -1, (t, b, int(out[b]))
+                    continue
+                u = 0.0
+                if plist[b]["temperature"] > 0:
+                    u = streams[b][used[b]]
+                    used[b] += 1
+                res, _, _, _ = oracle_row(x[b], plist[b], hist[b], {}, u, O.EXPF_CR)
+                assert out[b] == res.id, (t, b, int(out[b]), res.id)
+                if res.id in eog:
+                    done[b] = True
+                else:
+                    hist[b].append(res.id)
+            assert [bool(v) for v in got_done] == done, (t, got_done, done)
+        assert any(done) and not all(done), done  # both kinds of rows were exercised
+    finally:
+        s.close()
+
+
 def test_nim_binding_call_sequence(pkg, torch):
     """tests/nim_binding_check.c makes exactly the calls of the Nim binding in
     INTEGRATION.md (create, set the RNG state from the Nim Rand, replay the
