@@ -441,6 +441,68 @@ def bench_softmax(args, logp):
     print(json.dumps(res), flush=True)
 
 
+def bench_sample_host(args):
+    """nls_sample_host end to end -- the Nim drop-in's path (host logits in,
+    a host id out: the copy to the device, the sampler, the copy back and the
+    synchronisation) -- and its no-allocation variant, on the workload's rows
+    one call at a time, beside the CPU restatement of the same rows.  One
+    line of JSON like the sampler's."""
+    import numpy as np
+    import torch
+
+    pkg = load_pkg()
+    from nimllm_amd import workloads
+
+    w = workloads.make(args.workload, seed=args.seed)
+    B, V = w.B, w.V
+    torch.cuda.init()
+    s = pkg.BatchSampler(workloads.sampler_params(w, pkg), V)
+    if w.hist.shape[1]:
+        s.accept(w.hist)
+    x = np.ascontiguousarray(w.logits)
+    noalloc = B * V * 4 + B * 4 + 256 <= 16 << 20
+    times = {}
+    for name, fn in (("nls_sample_host", s.sample_host),
+                     ("nls_sample_host_noalloc", s.sample_host_noalloc if noalloc else None)):
+        if fn is None:
+            continue
+        for _ in range(args.warmup):
+            fn(x)
+        t = []
+        for _ in range(args.steps):
+            t0 = time.perf_counter()
+            fn(x)
+            t.append(time.perf_counter() - t0)
+        t.sort()
+        times[name] = {"median_us": t[len(t) // 2] * 1e6, "p10_us": t[len(t) // 10] * 1e6,
+                       "p90_us": t[(9 * len(t)) // 10] * 1e6}
+    s.close()
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    bid, bval, bcnt = w.bias_arrays()
+    plist = [O.make_params(**r.as_kwargs()) for r in w.rows]
+    hl = np.full(B, w.hist.shape[1])
+    hist = w.hist if w.hist.shape[1] else None
+    t = []
+    for _ in range(max(5, min(args.steps, 50))):
+        t0 = time.perf_counter()
+        O.sample_batch(plist, x, hist, hl, bid, bval, bcnt, w.u, O.EXPF_LIBM, nthreads=1)
+        t.append(time.perf_counter() - t0)
+    t.sort()
+    cpu_us = t[len(t) // 2] * 1e6
+    med = times["nls_sample_host"]["median_us"]
+    res = {"metric": f"nls_sample_host end to end (us per call) at B={B} x V={V}", "value": med,
+           "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": med / 1e3,
+           "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+           "data": "synthetic (seeded numpy logits in host memory, one blocking call at a time)",
+           "config": {"workload": args.workload, "B": B, "V": V}, "calls": times,
+           "cpu_baseline": {"value": cpu_us, "unit": "us per call", "cores": 1, "kind": "port",
+                            "sample": f"median of the same {B}-row call on one thread; C restatement of "
+                                      "src/nimllm/sampler.nim:59-121 (libm expf)"}}
+    print(json.dumps(res), flush=True)
+
+
 def phase_stamps(args):
     """Per-phase wall-clock of the k64 kernel on the workload, from the
     `phases` build of the library (make -C nim.llm_amd/csrc phases):
@@ -586,6 +648,8 @@ def main():
                     help="time nls_softmax_rows (softmaxInPlace over whole rows) instead of the sampler")
     ap.add_argument("--log-prob", action="store_true",
                     help="time nls_log_prob (logProb's per-token term) instead of the sampler")
+    ap.add_argument("--sample-host", action="store_true",
+                    help="time nls_sample_host end to end (host logits in, host id out) for the workload")
     ap.add_argument("--row-nll", action="store_true",
                     help="time perplexity's per-position term (one target per row) on the workload's logits")
     ap.add_argument("--traffic-summary", action="store_true",
@@ -613,6 +677,8 @@ def main():
         return bench_row_nll(args)
     if args.softmax or args.log_prob:
         return bench_softmax(args, args.log_prob)
+    if args.sample_host:
+        return bench_sample_host(args)
     import numpy as np
     import torch
 

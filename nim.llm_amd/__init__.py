@@ -328,6 +328,17 @@ class BatchSampler:
                                     o.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))), "nls_sample_host")
         return o
 
+    def sample_host_noalloc(self, logits):
+        """sample_host through the library's static staging (nothing allocated)."""
+        import numpy as np
+
+        x = np.ascontiguousarray(np.asarray(logits, dtype=np.float32).reshape(self.B, self.V))
+        o = np.zeros(self.B, dtype=np.int64)
+        check(lib().nls_sample_host_noalloc(self._h, x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                            o.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))),
+              "nls_sample_host_noalloc")
+        return o
+
     def profile_next(self, start_event, stop_event):
         """Time the next sample()'s streaming kernel with two torch.cuda.Events
         (recorded on this sampler's stream)."""
