@@ -761,17 +761,20 @@ def main():
     pipe_bytes = float(sum(per_row))
     s_avg, s_med = stats(ev_s)
     sname = "k64_kernel" if plan.k64 else "stream_kernel"
-    kernels = {sname: {"rows": int(sum(streamed)), "algorithmic_bytes_per_launch": stream_bytes,
-                                 "event_pair_avg_us": s_avg * 1e3, "event_pair_median_us": s_med * 1e3}}
+    kernels = {}
+    if plan.streamed_rows > 0:  # (a batch of full sorts only runs the whole-row kernel alone)
+        kernels[sname] = {"rows": int(sum(streamed)), "algorithmic_bytes_per_launch": stream_bytes,
+                          "event_pair_avg_us": s_avg * 1e3, "event_pair_median_us": s_med * 1e3}
     if ev_g:
         g_avg, g_med = stats(ev_g)
         kernels["generic_kernel"] = {"rows": int(B - sum(streamed)), "algorithmic_bytes_per_launch": generic_bytes,
                                      "event_pair_avg_us": g_avg * 1e3, "event_pair_median_us": g_med * 1e3}
     # When a call is one launch (no full-sort rows: rows the streaming kernel
-    # hands on are served by its last workgroup) the kernel's average launch
+    # hands on are served by its last workgroup; or full sorts only: the
+    # whole-row kernel alone) the kernel's average launch
     # duration is the time of the K back-to-back calls of (1) over K; otherwise
     # the event pairs of (2).
-    single = not plan.generic_launch
+    single = not plan.generic_launch or plan.streamed_rows == 0
     for name, k in kernels.items():
         k["avg_us"] = ms * 1e3 if single else k["event_pair_avg_us"]
         k["avg_from"] = "back-to-back calls" if single else "event pairs"

@@ -161,6 +161,7 @@ struct nls_sampler {
   uint64_t* rng = nullptr;
   int32_t* generic_list = nullptr;
   int32_t* generic_count = nullptr;  // [2]
+  int32_t* all_rows = nullptr;       // no streaming rows: 0 .. B-1, then B (the count), then a spare
   uint32_t* done = nullptr;          // workgroups finished (whole-row rows served inline)
   int gen_inline = 0;
   uint32_t* gen_scratch = nullptr;
@@ -189,6 +190,7 @@ struct nls_sampler {
     dfree(rng);
     dfree(generic_list);
     dfree(generic_count);
+    dfree(all_rows);
     dfree(done);
     dfree(gen_scratch);
     dfree(stage_ids);
@@ -549,6 +551,11 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   }
   // Without full-sort rows the whole-row kernel only serves the rare row the
   // streaming kernel hands on: one workgroup keeps that launch cheap.
+  bool any_fast = false;
+  for (int b = 0; b < B; ++b) any_fast |= s->h_rp[b].fast != 0;
+  // A batch without streaming rows (full sorts only) runs the whole-row
+  // kernel alone over a fixed list of every row.
+  s->plan.no_stream = !any_fast;
   s->plan.gen_blocks = any_full ? std::min(B, 256) : 1;
   s->plan.gen_lds = group_lds_bytes(vocab);
   // ... and then its last workgroup serves that row itself, saving a launch
@@ -593,6 +600,15 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   if ((rc = dalloc(&s->rng, (size_t)2 * B))) return fail(rc);
   if ((rc = dalloc(&s->generic_list, B))) return fail(rc);
   if ((rc = dalloc(&s->generic_count, 2))) return fail(rc);
+  if (s->plan.no_stream) {
+    std::vector<int32_t> rows((size_t)B + 2);
+    for (int b = 0; b < B; ++b) rows[b] = b;
+    rows[B] = B;
+    rows[B + 1] = 0;
+    if ((rc = dalloc(&s->all_rows, rows.size()))) return fail(rc);
+    const hipError_t e0 = hipMemcpy(s->all_rows, rows.data(), rows.size() * 4, hipMemcpyHostToDevice);
+    if (e0 != hipSuccess) return fail(hip_fail(e0, "upload row list"));
+  }
   if ((rc = dalloc(&s->done, 1))) return fail(rc);
   int64_t vpad = 1;
   while (vpad < vocab) vpad <<= 1;
@@ -812,6 +828,15 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   a.done = s->done;
   a.hbits = s->hbits;
   a.row_done = d_done;
+  ga.row_done = d_done;
+  if (lp.no_stream) {
+    // every row, a constant count (the spare slot takes the kernel's reset of
+    // the next call's counter)
+    ga.generic_list = s->all_rows;
+    ga.generic_count = s->all_rows + s->B;
+    ga.next_count = s->all_rows + s->B + 1;
+    a.gen_inline = 0;
+  }
   a.ga = ga;
   lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
   hipEvent_t e0 = s->prof_start, e1 = s->prof_stop, g0 = s->prof_gstart, g1 = s->prof_gstop;
@@ -865,8 +890,9 @@ int nls_get_plan(const nls_sampler* s, nls_plan* out, int32_t* row_streamed) {
   out->k64 = s->plan.k64 ? 1 : 0;
   // a workgroup requests its first unit (kStreamVec4 float4 per thread)
   // before it reads the row's constants
-  out->first_unit_bytes =
-      s->plan.lds > 0 ? std::min<int64_t>((int64_t)s->S * s->plan.nt * kStreamVec4 * 16, s->V * 4) : 0;
+  out->first_unit_bytes = (s->plan.lds > 0 && !s->plan.no_stream)
+                              ? std::min<int64_t>((int64_t)s->S * s->plan.nt * kStreamVec4 * 16, s->V * 4)
+                              : 0;
   for (int b = 0; b < s->B; ++b) {
     const int f = s->h_rp[b].fast ? 1 : 0;
     out->streamed_rows += f;

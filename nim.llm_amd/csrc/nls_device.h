@@ -2438,6 +2438,10 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
   float* work = reinterpret_cast<float*>(iB + a.vpad);
   for (int li = w0; li < count; li += nw) {
     const int row = load_agent(&a.generic_list[li]);
+    if (a.row_done && a.row_done[row] != 0) {  // a finished row of a batched loop
+      if (tid == 0) a.out[row] = -1;
+      continue;
+    }
     const RowParams P = a.rp[row];
     const float* __restrict__ src = a.logits + (int64_t)row * a.V;
     bool u_taken = false;

@@ -126,6 +126,7 @@ struct GenericArgs {
   int32_t* out;
   DebugPtrs dbg;
   int grouped;  // 1: the launch carries group_lds_bytes(V) of dynamic LDS
+  const int32_t* row_done;  // [B] or null: a nonzero row samples nothing (out = -1)
 };
 
 struct StreamArgs {
@@ -180,6 +181,7 @@ struct LaunchPlan {
   size_t lds;    // dynamic LDS bytes of the streaming kernel
   int gen_blocks;
   size_t gen_lds;  // dynamic LDS bytes of the whole-row kernel (grouped path), 0 = none
+  bool no_stream;  // no row is a streaming row: the whole-row kernel alone, over every row
 };
 
 hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const LaunchPlan& lp,

@@ -473,9 +473,11 @@ hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const Laun
                          hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, hipEvent_t gev_start,
                          hipEvent_t gev_stop) {
   hipError_t e;
-  if (ev_start && (e = hipEventRecord(ev_start, s)) != hipSuccess) return e;
-  if ((e = lp.k64 ? launch_k64(sa, lp, s) : launch_stream(sa, lp, s)) != hipSuccess) return e;
-  if (ev_stop && (e = hipEventRecord(ev_stop, s)) != hipSuccess) return e;
+  if (!lp.no_stream) {
+    if (ev_start && (e = hipEventRecord(ev_start, s)) != hipSuccess) return e;
+    if ((e = lp.k64 ? launch_k64(sa, lp, s) : launch_stream(sa, lp, s)) != hipSuccess) return e;
+    if (ev_stop && (e = hipEventRecord(ev_stop, s)) != hipSuccess) return e;
+  }
   if (!sa.gen_inline) {
     if (gev_start && (e = hipEventRecord(gev_start, s)) != hipSuccess) return e;
     if ((e = launch_generic(ga, lp, s)) != hipSuccess) return e;
