@@ -441,6 +441,111 @@ def bench_softmax(args, logp):
     print(json.dumps(res), flush=True)
 
 
+def bench_lm_head(args):
+    """The output projection (nls_lm_head, matmul(m.output, x, y, nb),
+    src/nimllm/model.nim:179-200) on synthetic GGUF rows: one step = one call
+    writing nb x rows logits.  The weight matrix is rotated over copies that
+    together exceed the Infinity Cache.  Roofline: the weight bytes plus x and
+    y, over the kernel time."""
+    import threading
+
+    import numpy as np
+    import torch
+
+    pkg = load_pkg()
+    from nimllm_amd import workloads
+
+    t = workloads.LM_TYPE_NAMES[args.lm_type]
+    rows, cols, nb = args.lm_rows, args.lm_cols, args.lm_nb
+    w_np = workloads.make_lm_weights(t, rows, cols, seed=args.seed)
+    x_np = workloads.make_lm_hidden(nb, cols, seed=args.seed)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    wbytes = w_np.nbytes
+    nbuf = max(2, math.ceil(640e6 / wbytes))
+    base = torch.from_numpy(w_np).to(dev)
+    bufs = [base] + [base.clone() for _ in range(nbuf - 1)]
+    x = torch.from_numpy(x_np).to(dev)
+    y = torch.empty((nb, rows), dtype=torch.float32, device=dev)
+    work = torch.empty(max(1, pkg.lm_head_workspace(t, cols, nb, 0, args.lm_exact)), dtype=torch.uint8,
+                       device=dev)
+
+    def call(wb):
+        pkg.lm_head(wb, t, rows, cols, x, exact=args.lm_exact, out=y, work=work)
+
+    call(bufs[0])
+    torch.cuda.synchronize()
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    # parity spot check: the first and the last 512 rows against the oracle
+    got = y.cpu().numpy()
+    ok = True
+    for lo, hi in ((0, min(rows, 512)), (max(0, rows - 512), rows)):
+        ref = O.matmul(t, w_np, rows, cols, x_np, exact=args.lm_exact, first=lo, last=hi)
+        ok &= bool(np.array_equal(got[:, lo:hi].view(np.uint32), ref[:, lo:hi].view(np.uint32)))
+    for i in range(args.warmup):
+        call(bufs[i % nbuf])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(args.steps):
+        call(bufs[i % nbuf])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = float(wbytes + nb * cols * 4 + nb * rows * 4)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    path = "int8 activations" if O.matmul_uses_act(t, cols, nb, args.lm_exact) else "dequantise + dotF32"
+    kern = ("lm_int_kernel" if path == "int8 activations" else "lm_float_kernel")
+    res = {"metric": f"LM head calls/sec ({rows} x {cols} {args.lm_type}, nb={nb})",
+           "value": 1e3 / ms, "unit": "calls/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "int8 x int8 -> int32, fp32 terms" if path == "int8 activations" else "f32",
+           "data": f"synthetic GGUF rows (random blocks, finite scales), rotated over {nbuf} copies",
+           "config": {"workload": f"output projection {rows} x {cols} {args.lm_type}, {path}",
+                      "rows": rows, "cols": cols, "nb": nb, "exact": bool(args.lm_exact)},
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": kern,
+                        "kernel_avg_us": ms * 1e3, "algorithmic_bytes_per_launch": nbytes},
+           "parity_spot_check": {"rows": 1024, "bit_exact": ok}}
+    if not args.no_cpu_baseline:
+        def run(nthreads, budget):
+            # rows in chunks of 256 per thread until the budget is spent
+            done = [0] * nthreads
+            t0 = time.perf_counter()
+
+            def worker(k):
+                r = (k * 7919 * 256) % rows
+                while time.perf_counter() - t0 < budget:
+                    hi = min(rows, r + 256)
+                    O.matmul(t, w_np, rows, cols, x_np, exact=args.lm_exact, first=r, last=hi)
+                    done[k] += hi - r
+                    r = hi % rows
+            ths = [threading.Thread(target=worker, args=(k,)) for k in range(nthreads)]
+            for th in ths:
+                th.start()
+            for th in ths:
+                th.join()
+            dt = time.perf_counter() - t0
+            return sum(done), dt
+
+        n1, dt1 = run(1, args.cpu_budget / 2)
+        res["cpu_baseline"] = {"value": n1 / rows / dt1, "unit": "calls/s", "cores": 1, "kind": "port",
+                               "sample": f"{n1} of the {rows} rows in {dt1:.1f} s on one thread, scaled to a "
+                                         "whole call; C restatement of model.nim:144-200 with "
+                                         "quant.nim:164-798 (-O2 -ffp-contract=off)"}
+        nt = host_cores()
+        nn, dtn = run(nt, args.cpu_budget / 2)
+        res["cpu_baseline_all_cores"] = {"value": nn / rows / dtn, "unit": "calls/s", "cores": nt,
+                                         "kind": "port",
+                                         "sample": f"{nn} rows in {dtn:.1f} s over {nt} threads (rows in "
+                                                   "chunks of 256, as parallelFor splits them)"}
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
 def bench_sample_host(args):
     """nls_sample_host end to end -- the Nim drop-in's path (host logits in,
     a host id out: the copy to the device, the sampler, the copy back and the
@@ -659,6 +764,13 @@ def main():
     ap.add_argument("--write-dir")
     ap.add_argument("--out")
     ap.add_argument("--commit", default="")
+    ap.add_argument("--lm-head", action="store_true",
+                    help="time the output projection nls_lm_head instead of the sampler")
+    ap.add_argument("--lm-type", default="Q6_K")
+    ap.add_argument("--lm-rows", type=int, default=128256)
+    ap.add_argument("--lm-cols", type=int, default=2048)
+    ap.add_argument("--lm-nb", type=int, default=1)
+    ap.add_argument("--lm-exact", action="store_true", help="exactMatmul: the float path")
     ap.add_argument("--phase-stamps", action="store_true",
                     help="per-phase times of the k64 kernel from the phases build of the library")
     args = ap.parse_args()
@@ -679,6 +791,8 @@ def main():
         return bench_softmax(args, args.log_prob)
     if args.sample_host:
         return bench_sample_host(args)
+    if args.lm_head:
+        return bench_lm_head(args)
     import numpy as np
     import torch
 

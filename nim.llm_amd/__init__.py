@@ -38,7 +38,15 @@ EXPORTED = (
     "nls_top_tokens", "nls_row_nll", "nls_softmax_rows", "nls_log_prob", "nls_expf_device",
     "nls_profile_next",
     "nls_profile_next_generic", "nls_get_plan", "nls_status_string", "nls_last_error",
+    "nls_lm_head_workspace", "nls_lm_head",
 )
+
+
+class NlsLora(ctypes.Structure):
+    """nls_lora: a LoRA adapter on the output matrix (LoraPair, model.nim:34-39)."""
+
+    _fields_ = [("d_a", ctypes.c_void_p), ("d_b", ctypes.c_void_p), ("rank", ctypes.c_int32),
+                ("scale", ctypes.c_float)]
 
 
 class NlsParams(ctypes.Structure):
@@ -130,6 +138,12 @@ def lib():
         L.nls_status_string.argtypes = [ctypes.c_int]
         L.nls_status_string.restype = ctypes.c_char_p
         L.nls_last_error.restype = ctypes.c_char_p
+        L.nls_lm_head_workspace.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                            ctypes.c_int32]
+        L.nls_lm_head_workspace.restype = ctypes.c_size_t
+        L.nls_lm_head.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, vp, ctypes.c_int32, vp,
+                                  ctypes.c_int32, P(NlsLora), vp, ctypes.c_size_t, vp]
+        L.nls_lm_head.restype = ctypes.c_int32
         _lib = L
     return _lib
 
@@ -524,3 +538,47 @@ def expf_device(x, out=None):
 
 def inf_bias() -> float:
     return -math.inf
+
+
+# GGML type codes (src/nimllm/quant.nim:14-19) nls_lm_head reads
+GGML_TYPES = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q2_K": 10,
+              "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "Q8_K": 15, "BF16": 30}
+
+
+def lm_head_workspace(ggml_type: int, cols: int, nb: int, lora_rank: int = 0, exact: bool = False) -> int:
+    return int(lib().nls_lm_head_workspace(ggml_type, cols, nb, lora_rank, int(exact)))
+
+
+def lm_head(weight, ggml_type: int, rows: int, cols: int, x, exact: bool = False, lora=None, out=None,
+            work=None):
+    """matmul(m.output, x, y, nb) (src/nimllm/model.nim:179-200) on the device:
+    weight is a uint8 device tensor of rows * rowBytes(type, cols) GGUF bytes,
+    x a float32 device tensor [nb, cols] (or [cols]); returns y [nb, rows]
+    float32 ([rows] for a 1-D x).  exact is the reference's exactMatmul;
+    lora = (a [rank, cols], b [rows, rank], scale) device tensors.  `work`
+    may pass a preallocated uint8 device workspace."""
+    import torch
+
+    x2 = x if x.dim() == 2 else x.reshape(1, -1)
+    assert x2.is_cuda and x2.dtype == torch.float32 and x2.is_contiguous() and x2.shape[1] == cols
+    assert weight.is_cuda and weight.is_contiguous()
+    nb = x2.shape[0]
+    if out is None:
+        out = torch.empty((nb, rows), dtype=torch.float32, device=x2.device)
+    assert out.is_cuda and out.dtype == torch.float32 and out.is_contiguous() and out.numel() == nb * rows
+    lo = None
+    rank = 0
+    if lora is not None:
+        a, b, scale = lora
+        assert a.is_contiguous() and b.is_contiguous() and a.dtype == torch.float32 and b.dtype == torch.float32
+        rank = a.shape[0]
+        lo = NlsLora(a.data_ptr(), b.data_ptr(), rank, float(scale))
+    need = lm_head_workspace(ggml_type, cols, nb, rank, exact)
+    if work is None or work.numel() < need:
+        work = torch.empty(max(need, 1), dtype=torch.uint8, device=x2.device)
+    stream = torch.cuda.current_stream(x2.device).cuda_stream
+    check(lib().nls_lm_head(ctypes.c_void_p(weight.data_ptr()), ggml_type, rows, cols,
+                            ctypes.c_void_p(x2.data_ptr()), nb, ctypes.c_void_p(out.data_ptr()), int(exact),
+                            ctypes.byref(lo) if lo is not None else None, ctypes.c_void_p(work.data_ptr()),
+                            work.numel(), ctypes.c_void_p(stream)), "nls_lm_head")
+    return out if x.dim() == 2 else out.reshape(rows)

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "../../include/nimllm_sampler.h"
+#include "../../include/nimllm_lmhead.h"
 #include "nls_internal.h"
 
 using namespace nls;
@@ -1019,6 +1020,118 @@ int nls_log_prob(const float* d_logits, int32_t rows, int64_t vocab, const int32
 int nls_expf_device(const float* d_in, float* d_out, int64_t n, void* stream) {
   if (n < 0 || (n > 0 && (!d_in || !d_out))) return NLS_ERR_INVALID_ARGUMENT;
   NLS_HIP(launch_expf(d_in, d_out, n, reinterpret_cast<hipStream_t>(stream)));
+  return NLS_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- LM head
+
+namespace {
+
+// blockSize / typeSize (quant.nim:38-63) of the types the reference reads
+int lm_block_size(int t) {
+  switch (t) {
+    case 0: case 1: case 30: return 1;
+    case 2: case 3: case 6: case 7: case 8: return 32;
+    case 10: case 11: case 12: case 13: case 14: case 15: return 256;
+    default: return 0;
+  }
+}
+int lm_type_bytes(int t) {
+  switch (t) {
+    case 0: return 4;
+    case 1: case 30: return 2;
+    case 2: return 18;
+    case 3: return 20;
+    case 6: return 22;
+    case 7: return 24;
+    case 8: return 34;
+    case 10: return 84;
+    case 11: return 110;
+    case 12: return 144;
+    case 13: return 176;
+    case 14: return 210;
+    case 15: return 292;
+    default: return 0;
+  }
+}
+size_t align256(size_t n) { return (n + 255) & ~size_t{255}; }
+
+// model.nim:184-185
+bool lm_uses_act(int type, int64_t cols, int nb, bool exact) {
+  const int bl = lm_act_block_len(type);
+  return !exact && bl > 0 && cols % bl == 0 && (nb <= 4 || type != 8);
+}
+
+// workspace: [act qs][act d][lora tmp], each 256-byte aligned
+struct LmLayout {
+  size_t qs = 0, d = 0, tmp = 0, total = 0;
+};
+LmLayout lm_layout(int type, int64_t cols, int nb, int rank, bool exact) {
+  LmLayout L;
+  if (lm_uses_act(type, cols, nb, exact)) {
+    const int64_t n = (int64_t)nb * cols;
+    L.d = align256((size_t)n);
+    L.tmp = L.d + align256(sizeof(float) * (size_t)(n / lm_act_block_len(type)));
+  }
+  L.total = L.tmp + (rank > 0 ? align256(sizeof(float) * (size_t)nb * (size_t)rank) : 0);
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t nls_lm_head_workspace(int32_t type, int64_t cols, int32_t nb, int32_t lora_rank, int32_t exact) {
+  if (!lm_type_supported(type) || cols <= 0 || nb < 0 || lora_rank < 0) return 0;
+  if (cols % lm_block_size(type) != 0) return 0;
+  return lm_layout(type, cols, nb, lora_rank, exact != 0).total;
+}
+
+int32_t nls_lm_head(const void* d_weight, int32_t type, int64_t rows, int64_t cols, const float* d_x, int32_t nb,
+                    float* d_y, int32_t exact, const nls_lora* lora, void* d_work, size_t work_bytes,
+                    void* stream) {
+  if (!lm_type_supported(type) || rows < 0 || cols <= 0 || nb < 0) return NLS_ERR_INVALID_ARGUMENT;
+  // rowBytes raises for a row that is not whole blocks (quant.nim:65-70)
+  if (cols % lm_block_size(type) != 0 || cols >= (int64_t{1} << 28) || rows >= (int64_t{1} << 40))
+    return NLS_ERR_INVALID_ARGUMENT;
+  if (rows == 0 || nb == 0) return NLS_OK;
+  if (!d_weight || !d_x || !d_y) return NLS_ERR_INVALID_ARGUMENT;
+  if ((reinterpret_cast<uintptr_t>(d_weight) & 15) || (reinterpret_cast<uintptr_t>(d_x) & 15) ||
+      (reinterpret_cast<uintptr_t>(d_y) & 3))
+    return NLS_ERR_INVALID_ARGUMENT;
+  const int rank = lora ? lora->rank : 0;
+  if (rank < 0 || (rank > 0 && (!lora->d_a || !lora->d_b))) return NLS_ERR_INVALID_ARGUMENT;
+  const bool ex = exact != 0;
+  const LmLayout L = lm_layout(type, cols, nb, rank, ex);
+  if (L.total > 0 && (!d_work || work_bytes < L.total || (reinterpret_cast<uintptr_t>(d_work) & 255)))
+    return NLS_ERR_INVALID_ARGUMENT;
+  LmHeadCall c{};
+  c.w = d_weight;
+  c.type = type;
+  c.rows = rows;
+  c.cols = cols;
+  c.row_bytes = cols / lm_block_size(type) * lm_type_bytes(type);
+  c.x = d_x;
+  c.nb = nb;
+  c.y = d_y;
+  c.use_act = lm_uses_act(type, cols, nb, ex);
+  if (c.use_act && cols / lm_act_block_len(type) > kLmMaxIntBlocks) {
+    g_last_error = "nls_lm_head: more than 1024 blocks per row on the int8 path";
+    return NLS_ERR_UNSUPPORTED;
+  }
+  char* wk = static_cast<char*>(d_work);
+  c.act_qs = c.use_act ? reinterpret_cast<int8_t*>(wk + L.qs) : nullptr;
+  c.act_d = c.use_act ? reinterpret_cast<float*>(wk + L.d) : nullptr;
+  c.lora_rank = rank;
+  if (rank > 0) {
+    c.lora_a = lora->d_a;
+    c.lora_b = lora->d_b;
+    c.lora_scale = lora->scale;
+    c.lora_tmp = reinterpret_cast<float*>(wk + L.tmp);
+  }
+  NLS_HIP(launch_lm_head(c, reinterpret_cast<hipStream_t>(stream)));
   return NLS_OK;
 }
 

@@ -211,4 +211,26 @@ hipError_t launch_log_prob(const float* logits, int rows, int64_t V, const int32
 hipError_t set_kernel_attributes();
 size_t max_dynamic_lds();
 
+// The output projection (nls_lmhead.hip): one matmul(m.output, x, y, nb).
+struct LmHeadCall {
+  const void* w;      // rows x row_bytes GGUF bytes
+  int type;           // GGML type code
+  int64_t rows, cols, row_bytes;
+  const float* x;     // [nb, cols]
+  int nb;
+  float* y;           // [nb, rows]
+  bool use_act;       // the int8 activation path (model.nim:185)
+  int8_t* act_qs;     // [nb * cols] workspace
+  float* act_d;       // [nb * cols / block] workspace
+  const float* lora_a;
+  const float* lora_b;
+  int lora_rank;
+  float lora_scale;
+  float* lora_tmp;    // [nb * rank] workspace
+};
+constexpr int kLmMaxIntBlocks = 1024;  // blocks per row the int8 path's LDS holds
+int lm_act_block_len(int type);
+bool lm_type_supported(int type);
+hipError_t launch_lm_head(const LmHeadCall& c, hipStream_t s);
+
 }  // namespace nls

@@ -207,3 +207,56 @@ def sampler_params(w: Workload, mod):
         p.logitBias = dict(r.logitBias or {})
         out.append(p)
     return out
+
+
+# --- the output projection (LM head) -------------------------------------
+
+# GGML type codes and their blocks (src/nimllm/quant.nim:14-63): code ->
+# (weights per block, bytes per block, byte offsets of the fp16 scale fields)
+LM_TYPES = {
+    0: (1, 4, ()), 1: (1, 2, ()), 30: (1, 2, ()),
+    2: (32, 18, (0,)), 3: (32, 20, (0, 2)), 6: (32, 22, (0,)), 7: (32, 24, (0, 2)), 8: (32, 34, (0,)),
+    10: (256, 84, (80, 82)), 11: (256, 110, (108,)), 12: (256, 144, (0, 2)), 13: (256, 176, (0, 2)),
+    14: (256, 210, (208,)), 15: (256, 292, ()),
+}
+LM_TYPE_NAMES = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q2_K": 10,
+                 "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "Q8_K": 15, "BF16": 30}
+
+
+def lm_row_bytes(t: int, cols: int) -> int:
+    bs, ts, _ = LM_TYPES[t]
+    assert cols % bs == 0
+    return cols // bs * ts
+
+
+def make_lm_weights(t: int, rows: int, cols: int, seed: int = 1234) -> np.ndarray:
+    """Synthetic GGUF weight rows [rows, rowBytes] of type t: random bytes
+    (every bit pattern is a valid block), with the fp16 / fp32 scale fields
+    set to finite values of the size a quantiser writes; F32 / F16 / BF16
+    rows hold N(0, 0.5^2) weights."""
+    rng = np.random.default_rng(seed)
+    bs, ts, halves = LM_TYPES[t]
+    rb = lm_row_bytes(t, cols)
+    if bs == 1:
+        v = (rng.standard_normal(size=(rows, cols), dtype=np.float32) * np.float32(0.5))
+        if t == 0:
+            return v.view(np.uint8).reshape(rows, rb)
+        if t == 1:
+            return v.astype(np.float16).view(np.uint8).reshape(rows, rb)
+        return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(rows, rb)
+    raw = rng.integers(0, 256, size=(rows, rb), dtype=np.uint8)
+    blocks = raw.reshape(rows, rb // ts, ts)
+    if t == 15:
+        d = rng.uniform(1e-3, 2e-2, size=blocks.shape[:2]).astype(np.float32)
+        blocks[:, :, 0:4] = d.view(np.uint8).reshape(rows, rb // ts, 4)
+    for off in halves:
+        h = (rng.uniform(-1, 1, size=blocks.shape[:2]) *
+             np.exp2(rng.integers(-12, -4, size=blocks.shape[:2]))).astype(np.float16)
+        blocks[:, :, off:off + 2] = h.view(np.uint8).reshape(rows, rb // ts, 2)
+    return raw
+
+
+def make_lm_hidden(nb: int, cols: int, seed: int = 1234) -> np.ndarray:
+    """Normalised hidden states [nb, cols] (rmsnorm output scale)."""
+    rng = np.random.default_rng(seed + 1)
+    return (rng.standard_normal(size=(nb, cols), dtype=np.float32) * np.float32(2.0))

@@ -3,7 +3,9 @@
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
 module.  It loads ``oracle/libnls_oracle.so`` (built by ``oracle/Makefile``) and
 exposes the restated sampler (src/nimllm/sampler.nim:59-121), argmax (:45-49),
-softmaxInPlace (:51-57), topTokens (:123-130) and Nim std/random.
+softmaxInPlace (:51-57), topTokens (:123-130), Nim std/random, and the output
+projection `matmul` (src/nimllm/model.nim:144-200) over the weight formats of
+src/nimllm/quant.nim.
 """
 from __future__ import annotations
 
@@ -108,6 +110,34 @@ def lib():
         L.nlo_log_prob.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                    P(ctypes.c_float)]
         L.nlo_log_prob.restype = ctypes.c_double
+        vp = ctypes.c_void_p
+        L.nlo_block_size.argtypes = [ctypes.c_int32]
+        L.nlo_block_size.restype = ctypes.c_int32
+        L.nlo_type_size.argtypes = [ctypes.c_int32]
+        L.nlo_type_size.restype = ctypes.c_int32
+        L.nlo_row_bytes.argtypes = [ctypes.c_int32, ctypes.c_int64]
+        L.nlo_row_bytes.restype = ctypes.c_int64
+        L.nlo_half_to_float.argtypes = [ctypes.c_uint16]
+        L.nlo_half_to_float.restype = ctypes.c_float
+        L.nlo_dequant_row.argtypes = [ctypes.c_int32, vp, P(ctypes.c_float), ctypes.c_int64]
+        L.nlo_dequant_row.restype = ctypes.c_int32
+        L.nlo_dot_f32.argtypes = [P(ctypes.c_float), P(ctypes.c_float), ctypes.c_int64]
+        L.nlo_dot_f32.restype = ctypes.c_float
+        L.nlo_act_block_len.argtypes = [ctypes.c_int32]
+        L.nlo_act_block_len.restype = ctypes.c_int32
+        L.nlo_quantize_act.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int32,
+                                       P(ctypes.c_float), P(ctypes.c_int8), P(ctypes.c_int32)]
+        L.nlo_dot_row_act.argtypes = [ctypes.c_int32, vp, P(ctypes.c_float), P(ctypes.c_int8),
+                                      P(ctypes.c_int32), ctypes.c_int64, ctypes.c_int64]
+        L.nlo_dot_row_act.restype = ctypes.c_float
+        L.nlo_matmul_uses_act.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+                                          ctypes.c_int32]
+        L.nlo_matmul_uses_act.restype = ctypes.c_int32
+        L.nlo_matmul.argtypes = [ctypes.c_int32, vp, ctypes.c_int64, ctypes.c_int64,
+                                 P(ctypes.c_float), ctypes.c_int32, P(ctypes.c_float),
+                                 ctypes.c_int32, P(ctypes.c_float), P(ctypes.c_float),
+                                 ctypes.c_int32, ctypes.c_float, ctypes.c_int64, ctypes.c_int64]
+        L.nlo_matmul.restype = ctypes.c_int32
         _lib = L
     return _lib
 
@@ -212,3 +242,95 @@ def row_nll(x, target):
     import numpy as np
     x = np.ascontiguousarray(x, dtype=np.float32)
     return lib().nlo_row_nll(x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(x), int(target))
+
+
+# --- output projection (src/nimllm/quant.nim, src/nimllm/model.nim:144-200) ---
+
+GGML = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8,
+        "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "Q8_K": 15, "BF16": 30}
+
+
+def block_size(t: int) -> int:
+    return lib().nlo_block_size(t)
+
+
+def type_size(t: int) -> int:
+    return lib().nlo_type_size(t)
+
+
+def row_bytes(t: int, n: int) -> int:
+    return lib().nlo_row_bytes(t, n)
+
+
+def half_to_float(h: int) -> np.float32:
+    return np.float32(lib().nlo_half_to_float(h))
+
+
+def dequant_row(t: int, raw, n: int) -> np.ndarray:
+    """dequantRow (quant.nim:336-352) of one row of raw bytes."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    y = np.zeros(n, dtype=np.float32)
+    if lib().nlo_dequant_row(t, raw.ctypes.data, _ptr(y, ctypes.c_float), n) != 0:
+        raise ValueError(f"unsupported type {t}")
+    return y
+
+
+def dot_f32(a, b) -> np.float32:
+    """dotF32 (quant.nim:362-374)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return np.float32(lib().nlo_dot_f32(_ptr(a, ctypes.c_float), _ptr(b, ctypes.c_float), a.size))
+
+
+def act_block_len(t: int) -> int:
+    return lib().nlo_act_block_len(t)
+
+
+def quantize_act(x, block_len: int):
+    """quantizeAct (quant.nim:646-667): (d, qs, bsums)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    n = x.size
+    d = np.zeros(n // block_len, dtype=np.float32)
+    qs = np.zeros(n, dtype=np.int8)
+    bs = np.zeros(max(n // 16, 1), dtype=np.int32)
+    lib().nlo_quantize_act(_ptr(x, ctypes.c_float), n, block_len, _ptr(d, ctypes.c_float),
+                           _ptr(qs, ctypes.c_int8), _ptr(bs, ctypes.c_int32))
+    return d, qs, bs[: n // 16]
+
+
+def dot_row_act(t: int, row, act, off: int, n: int) -> np.float32:
+    """dotRowAct (quant.nim:788-798) of one raw row against quantize_act's output."""
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    d, qs, bs = act
+    bs = np.ascontiguousarray(bs if bs.size else np.zeros(1, np.int32), dtype=np.int32)
+    return np.float32(lib().nlo_dot_row_act(t, row.ctypes.data, _ptr(d, ctypes.c_float),
+                                            _ptr(qs, ctypes.c_int8), _ptr(bs, ctypes.c_int32),
+                                            off, n))
+
+
+def matmul_uses_act(t: int, cols: int, nb: int, exact: bool = False) -> bool:
+    return bool(lib().nlo_matmul_uses_act(t, cols, nb, int(exact)))
+
+
+def matmul(t: int, w, rows: int, cols: int, x, exact: bool = False, lora=None,
+           first: int = 0, last: int | None = None) -> np.ndarray:
+    """matmul (model.nim:179-200): y[nb, rows] = x[nb, cols] . W^T for raw
+    weight bytes w (rows x rowBytes).  lora = (a [rank, cols], b [rows, rank],
+    scale).  With first/last only those rows are computed (the rest stay 0)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, cols)
+    nb = x.shape[0]
+    last = rows if last is None else last
+    y = np.zeros((nb, rows), dtype=np.float32)
+    la = lb = None
+    rank, scale = 0, 0.0
+    if lora is not None:
+        la = np.ascontiguousarray(lora[0], dtype=np.float32)
+        lb = np.ascontiguousarray(lora[1], dtype=np.float32)
+        rank, scale = la.shape[0], float(lora[2])
+    rc = lib().nlo_matmul(t, w.ctypes.data, rows, cols, _ptr(x, ctypes.c_float), nb,
+                          _ptr(y, ctypes.c_float), int(exact), _ptr(la, ctypes.c_float),
+                          _ptr(lb, ctypes.c_float), rank, scale, first, last)
+    if rc != 0:
+        raise ValueError("unsupported type or shape")
+    return y

@@ -1,6 +1,7 @@
 """C-ABI checks that need no GPU: the library loads, exports every symbol
-include/nimllm_sampler.h declares, and its host-only entry points behave."""
+include/*.h declares, and its host-only entry points behave."""
 import ctypes
+import glob
 import os
 import re
 
@@ -10,13 +11,15 @@ import pytest
 import oracle as O
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "nimllm_sampler.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def declared_symbols():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(nls_[a-z_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(nls_[a-z_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_and_binding_agree(pkg):
@@ -99,3 +102,22 @@ def test_fixture_file_is_consistent_with_oracle():
         r2, _, _, _ = O.sample(O.make_params(**c["params"]), x, c["history"], bias, c["u"],
                                O.EXPF_LIBM)
         assert r2.id == c["id_libm"]
+
+
+def test_lm_head_host_checks(pkg):
+    """nls_lm_head's argument checks run on the host before any launch."""
+    L = pkg.lib()
+    # workspace: int8 activations (nb * cols bytes) + block scales, each
+    # 256-byte aligned; none on the float path
+    assert L.nls_lm_head_workspace(14, 2048, 1, 0, 0) == 2048 + 256
+    assert L.nls_lm_head_workspace(14, 2048, 1, 0, 1) == 0
+    assert L.nls_lm_head_workspace(8, 2048, 5, 0, 0) == 0          # Q8_0, nb > 4: float path
+    assert L.nls_lm_head_workspace(8, 2048, 4, 0, 0) == 8192 + 1024
+    assert L.nls_lm_head_workspace(1, 1000, 2, 3, 0) == 256         # LoRA tmp only
+    assert L.nls_lm_head_workspace(9, 2048, 1, 0, 0) == 0           # Q8_1: not readable
+    INVALID = 1
+    assert L.nls_lm_head(None, 9, 10, 256, None, 1, None, 0, None, None, 0, None) == INVALID
+    assert L.nls_lm_head(None, 14, 10, 100, None, 1, None, 0, None, None, 0, None) == INVALID
+    assert L.nls_lm_head(None, 14, 0, 256, None, 1, None, 0, None, None, 0, None) == 0
+    assert L.nls_lm_head(None, 14, 10, 256, None, 0, None, 0, None, None, 0, None) == 0
+    assert L.nls_lm_head(None, 14, 10, 256, None, 1, None, 0, None, None, 0, None) == INVALID
