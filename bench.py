@@ -497,7 +497,12 @@ def bench_lm_head(args):
     nbytes = float(wbytes + nb * cols * 4 + nb * rows * 4)
     achieved = nbytes / (ms * 1e-3) / 1e9
     path = "int8 activations" if O.matmul_uses_act(t, cols, nb, args.lm_exact) else "dequantise + dotF32"
-    kern = ("lm_int_kernel" if path == "int8 activations" else "lm_float_kernel")
+    if path != "int8 activations":
+        kern = "lm_float_kernel"
+    elif nb == 1 and (cols // 32 + 63) // 64 <= 4:
+        kern = "lm_int1_kernel (activations quantised in the kernel)"
+    else:
+        kern = "quant_act_kernel + lm_int_kernel"
     res = {"metric": f"LM head calls/sec ({rows} x {cols} {args.lm_type}, nb={nb})",
            "value": 1e3 / ms, "unit": "calls/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

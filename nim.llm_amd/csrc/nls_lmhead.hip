@@ -53,6 +53,38 @@ __device__ __forceinline__ uint4 ld_16(const void* p) {
   __builtin_memcpy(&v, p, 16);
   return v;
 }
+// 8 or 32 bytes at a 2-byte aligned address, read as 4-byte aligned words
+// and funnel-shifted (the words past the field are read only when the
+// address is not 4-byte aligned, and never past the field's last word).
+__device__ __forceinline__ uint2 ld_8a(const uint8_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t sh = (uint32_t)(a & 3) * 8;
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(p - (a & 3));
+  uint2 w;
+  __builtin_memcpy(&w, q, 8);
+  const uint32_t w2 = sh ? q[2] : 0u;
+  return make_uint2(__builtin_amdgcn_alignbit(w.y, w.x, sh), __builtin_amdgcn_alignbit(w2, w.y, sh));
+}
+template <int NW>
+__device__ __forceinline__ void ld_words_a(const uint8_t* p, uint32_t (&out)[NW]) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t sh = (uint32_t)(a & 3) * 8;
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(p - (a & 3));
+  uint32_t w[NW + 1];
+#pragma unroll
+  for (int k = 0; k < NW; k += 4) {
+    uint4 v;
+    __builtin_memcpy(&v, q + k, 16);
+    w[k] = v.x;
+    w[k + 1] = v.y;
+    w[k + 2] = v.z;
+    w[k + 3] = v.w;
+  }
+  w[NW] = sh ? q[NW] : 0u;
+#pragma unroll
+  for (int k = 0; k < NW; ++k) out[k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
+}
+
 // IEEE half to float: exact for every finite half (subnormals included).
 __device__ __forceinline__ float half_f(uint32_t bits) {
   _Float16 h;
@@ -123,13 +155,15 @@ struct Fmt<14> {
     w.d = ld_u16(blk + 208);
     return w;
   }
-  __device__ static Act load_a(const int8_t* ablk, int p) {
-    const int h = p >> 2, l0 = 8 * (p & 3);
+  static constexpr bool HAS_MIN = false;
+  // byte group gi (8 activations) of slice p: weights 128 h + 32 gi + l0 ..
+  __device__ static int group_base(int p, int gi) { return 128 * (p >> 2) + 32 * gi + 8 * (p & 3); }
+  __device__ static Act make_act(const uint32_t (&wd)[8]) {
     Act a;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      a.a[m] = ld_8(ablk + 128 * h + 32 * m + l0);
-      a.a32[m] = 32 * dot4(kOnes, a.a[m].y, dot4(kOnes, a.a[m].x, 0));
+      a.a[m] = make_uint2(wd[2 * m], wd[2 * m + 1]);
+      a.a32[m] = 32 * dot4(kOnes, wd[2 * m + 1], dot4(kOnes, wd[2 * m], 0));
     }
     return a;
   }
@@ -150,7 +184,7 @@ struct Fmt<14> {
       const uint32_t scw = (m & 2) ? w.sc.y : w.sc.x;
       const int sc = __builtin_amdgcn_sbfe((int)scw, 8 * (g + (m & 1) * 2), 8);
       const int dm = dot4(q[m][1], a.a[m].y, dot4(q[m][0], a.a[m].x, 0)) - a.a32[m];
-      s += sc * dm;
+      s += __mul24(sc, dm);  // |sc| < 2^7, |dm| < 2^17: 24-bit products
     }
     sumi = s;
     summ = 0;
@@ -184,13 +218,17 @@ struct FmtK45 {
     if (FIVE) w.qh = ld_16(blk + 16 + l0);
     return w;
   }
-  __device__ static Act load_a(const int8_t* ablk, int p) {
-    const int j = p >> 1, l0 = 16 * (p & 1);
+  static constexpr bool HAS_MIN = true;
+  // byte groups 0, 1: weights 64 j + l0 ..; groups 2, 3: 64 j + 32 + l0 ..
+  __device__ static int group_base(int p, int gi) {
+    return 64 * (p >> 1) + 16 * (p & 1) + (gi < 2 ? 8 * gi : 32 + 8 * (gi - 2));
+  }
+  __device__ static Act make_act(const uint32_t (&wd)[8]) {
     Act a;
-    a.lo = ld_16(ablk + 64 * j + l0);
-    a.hi = ld_16(ablk + 64 * j + 32 + l0);
-    a.slo = dot4(kOnes, a.lo.w, dot4(kOnes, a.lo.z, dot4(kOnes, a.lo.y, dot4(kOnes, a.lo.x, 0))));
-    a.shi = dot4(kOnes, a.hi.w, dot4(kOnes, a.hi.z, dot4(kOnes, a.hi.y, dot4(kOnes, a.hi.x, 0))));
+    a.lo = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    a.hi = make_uint4(wd[4], wd[5], wd[6], wd[7]);
+    a.slo = dot4(kOnes, wd[3], dot4(kOnes, wd[2], dot4(kOnes, wd[1], dot4(kOnes, wd[0], 0))));
+    a.shi = dot4(kOnes, wd[7], dot4(kOnes, wd[6], dot4(kOnes, wd[5], dot4(kOnes, wd[4], 0))));
     return a;
   }
   // getScaleMinK4 (quant.nim:156-162) of sub-block jj from the header words
@@ -225,8 +263,9 @@ struct FmtK45 {
     int sc0, m0, sc1, m1;
     scale_min(w.hd, 2 * j, sc0, m0);
     scale_min(w.hd, 2 * j + 1, sc1, m1);
-    sumi = sc0 * s0 + sc1 * s1;
-    summ = m0 * a.slo + m1 * a.shi;
+    // scales < 2^6, |s0|, |s1| < 2^16, |slo|, |shi| < 2^11: 24-bit products
+    sumi = __mul24(sc0, s0) + __mul24(sc1, s1);
+    summ = __mul24(m0, a.slo) + __mul24(m1, a.shi);
   }
   // acc += a.d * (d * sumi - dmin * summ)  (quant.nim:694, :728)
   __device__ static float term(const Wt& w, int sumi, int summ, float ad) {
@@ -253,12 +292,16 @@ struct Fmt<8> {
   __device__ static Wt load_w(const uint8_t* blk, int) {
     Wt w;
     w.d = ld_u16(blk);
-    w.q0 = ld_16(blk + 2);
-    w.q1 = ld_16(blk + 18);
+    uint32_t q[8];
+    ld_words_a<8>(blk + 2, q);
+    w.q0 = make_uint4(q[0], q[1], q[2], q[3]);
+    w.q1 = make_uint4(q[4], q[5], q[6], q[7]);
     return w;
   }
-  __device__ static Act load_a(const int8_t* ablk, int) {
-    return Act{ld_16(ablk), ld_16(ablk + 16)};
+  static constexpr bool HAS_MIN = false;
+  __device__ static int group_base(int, int gi) { return 8 * gi; }
+  __device__ static Act make_act(const uint32_t (&wd)[8]) {
+    return Act{make_uint4(wd[0], wd[1], wd[2], wd[3]), make_uint4(wd[4], wd[5], wd[6], wd[7])};
   }
   __device__ static void partial(const Wt& w, const Act& a, int, int& sumi, int& summ) {
     int s = dot4(w.q0.x, a.a0.x, 0);
@@ -293,22 +336,20 @@ struct Fmt<2> {
   __device__ static Wt load_w(const uint8_t* blk, int) {
     Wt w;
     w.d = ld_u16(blk);
-    w.q = ld_16(blk + 2);
+    uint32_t q[4];
+    ld_words_a<4>(blk + 2, q);
+    w.q = make_uint4(q[0], q[1], q[2], q[3]);
     return w;
   }
-  __device__ static Act load_a(const int8_t* ablk, int) {
+  static constexpr bool HAS_MIN = false;
+  __device__ static int group_base(int, int gi) { return 8 * gi; }
+  __device__ static Act make_act(const uint32_t (&wd)[8]) {
     Act a;
-    a.lo = ld_16(ablk);
-    a.hi = ld_16(ablk + 16);
+    a.lo = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    a.hi = make_uint4(wd[4], wd[5], wd[6], wd[7]);
     int s = 0;
-    s = dot4(kOnes, a.lo.x, s);
-    s = dot4(kOnes, a.lo.y, s);
-    s = dot4(kOnes, a.lo.z, s);
-    s = dot4(kOnes, a.lo.w, s);
-    s = dot4(kOnes, a.hi.x, s);
-    s = dot4(kOnes, a.hi.y, s);
-    s = dot4(kOnes, a.hi.z, s);
-    s = dot4(kOnes, a.hi.w, s);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s = dot4(kOnes, wd[k], s);
     a.s8 = 8 * s;
     return a;
   }
@@ -330,17 +371,31 @@ struct Fmt<2> {
   }
 };
 
+// A lane's activation slice from the int8 activations of its block.
+template <int T>
+__device__ __forceinline__ typename Fmt<T>::Act load_act(const int8_t* ablk, int p) {
+  uint32_t wd[8];
+#pragma unroll
+  for (int gi = 0; gi < 4; ++gi) {
+    const uint2 v = ld_8(ablk + Fmt<T>::group_base(p, gi));
+    wd[2 * gi] = v.x;
+    wd[2 * gi + 1] = v.y;
+  }
+  return Fmt<T>::make_act(wd);
+}
+
 // ------------------------------------------------ quantizeAct
 
 // quantizeAct (quant.nim:646-667) of nb * cols activations in blocks of BL:
 // each lane owns 4 consecutive values; BL / 4 lanes share a block's maximum.
+// Values i4 * 4 .. i4 * 4 + 3 of one lane; BL / 4 consecutive lanes hold a
+// block and share its maximum.  Every lane of the wave calls this (the
+// maximum is exchanged across lanes); `on` is false past the end.
 template <int BL>
-__global__ __launch_bounds__(kLmNT) void quant_act_kernel(const float* __restrict__ x, int64_t n,
-                                                         int8_t* __restrict__ qs, float* __restrict__ dout) {
+__device__ __forceinline__ void quant4(const float* __restrict__ x, int64_t i4, bool on, int8_t* qs,
+                                       float* dout) {
   constexpr int G = BL / 4;
-  const int64_t i4 = (int64_t)blockIdx.x * kLmNT + threadIdx.x;  // which 4 values
-  const bool on = i4 * 4 < n;                                     // n is a multiple of BL
-  float4 v = on ? *reinterpret_cast<const float4*>(x + i4 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4 v = on ? *reinterpret_cast<const float4*>(x + i4 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
   float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 #pragma unroll
   for (int o = 1; o < G; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
@@ -358,7 +413,14 @@ __global__ __launch_bounds__(kLmNT) void quant_act_kernel(const float* __restric
     packed |= (uint32_t)(q & 0xFF) << (8 * k);
   }
   *reinterpret_cast<uint32_t*>(qs + i4 * 4) = packed;
-  if ((threadIdx.x & (G - 1)) == 0) dout[(i4 * 4) / BL] = d;
+  if ((i4 & (G - 1)) == 0) dout[(i4 * 4) / BL] = d;
+}
+
+template <int BL>
+__global__ __launch_bounds__(kLmNT) void quant_act_kernel(const float* __restrict__ x, int64_t n,
+                                                         int8_t* __restrict__ qs, float* __restrict__ dout) {
+  const int64_t i4 = (int64_t)blockIdx.x * kLmNT + threadIdx.x;  // which 4 values
+  quant4<BL>(x, i4, i4 * 4 < n, qs, dout);                       // n is a multiple of BL
 }
 
 // ------------------------------------------------ int8 path kernel
@@ -375,92 +437,141 @@ struct IntArgs {
 // One wave per group of `rw` rows.  For each row the wave's lanes form the
 // integer partials of their slices (64 slices = 2048 weights per pass), the
 // 8 lanes of a block add theirs, and the block's last lane writes the block's
-// fp32 term to LDS.  Then one lane per row adds its row's terms in block order.
-// FIXED: one pass and one activation row, so each lane's activation slice is
-// loaded once for all rows, and the next row's weights are loaded while the
-// current row is computed.
-template <int T, bool FIXED>
+// fp32 term to LDS.  Then one lane per row adds its row's terms in block
+// order.  Up to kLmNBC activation rows share each load of a weight slice.
+template <int T>
 __global__ __launch_bounds__(kLmNT) void lm_int_kernel(IntArgs a) {
   using F = Fmt<T>;
   extern __shared__ float s_term[];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int64_t row0 = ((int64_t)blockIdx.x * (kLmNT / 64) + wave) * a.rw;
   if (row0 >= a.rows) return;
   const int nrow = (int)min<int64_t>(a.rw, a.rows - row0);
   const int nbc_max = min(a.nb, kLmNBC);
   float* term = s_term + (size_t)wave * nbc_max * a.rw * a.nblk;
   const int S = (int)(a.cols / 32);  // 32-weight slices per row
-  if (FIXED) {
-    const bool on = lane < S;
-    const int ib = lane / F::LPB, p = lane % F::LPB;
-    typename F::Act act{};
-    if (on) act = F::load_a(a.aqs + (int64_t)ib * F::BL, p);
-    const float ad = on ? a.ad[ib] : 0.0f;
-    typename F::Wt cur{};
-    if (on) cur = F::load_w(a.w + row0 * a.row_bytes + (int64_t)ib * F::TS, p);
+  for (int b0 = 0; b0 < a.nb; b0 += kLmNBC) {
+    const int nbc = min(kLmNBC, a.nb - b0);
     for (int rr = 0; rr < nrow; ++rr) {
-      typename F::Wt nxt{};
-      if (on && rr + 1 < nrow) nxt = F::load_w(a.w + (row0 + rr + 1) * a.row_bytes + (int64_t)ib * F::TS, p);
-      int si = 0, sm = 0;
-      if (on) F::partial(cur, act, p, si, sm);
-      if (F::LPB == 8) {
-        si = group8_sum(si);
-        sm = group8_sum(sm);
-      }
-      if (on && p == F::LPB - 1) term[rr * a.nblk + ib] = F::term(cur, si, sm, ad);
-      cur = nxt;
-    }
-  } else {
-    for (int b0 = 0; b0 < a.nb; b0 += kLmNBC) {
-      const int nbc = min(kLmNBC, a.nb - b0);
-      for (int rr = 0; rr < nrow; ++rr) {
-        const uint8_t* rp = a.w + (row0 + rr) * a.row_bytes;
-        for (int pass = 0; pass < a.passes; ++pass) {
-          const int s = pass * 64 + lane;
-          const bool on = s < S;
-          const int ib = s / F::LPB, p = s % F::LPB;
-          typename F::Wt w{};
-          if (on) w = F::load_w(rp + (int64_t)ib * F::TS, p);
-          for (int bb = 0; bb < nbc; ++bb) {
-            const int64_t brow = b0 + bb;
-            int si = 0, sm = 0;
-            if (on) {
-              const typename F::Act act = F::load_a(a.aqs + brow * a.cols + (int64_t)ib * F::BL, p);
-              F::partial(w, act, p, si, sm);
-            }
-            if (F::LPB == 8) {
-              si = group8_sum(si);
-              sm = group8_sum(sm);
-            }
-            if (on && p == F::LPB - 1)
-              term[(bb * a.rw + rr) * a.nblk + ib] = F::term(w, si, sm, a.ad[brow * a.nblk + ib]);
+      const uint8_t* rp = a.w + (row0 + rr) * a.row_bytes;
+      for (int pass = 0; pass < a.passes; ++pass) {
+        const int s = pass * 64 + lane;
+        const bool on = s < S;
+        const int ib = s / F::LPB, p = s % F::LPB;
+        typename F::Wt w{};
+        if (on) w = F::load_w(rp + (int64_t)ib * F::TS, p);
+        for (int bb = 0; bb < nbc; ++bb) {
+          const int64_t brow = b0 + bb;
+          int si = 0, sm = 0;
+          if (on) {
+            const typename F::Act act = load_act<T>(a.aqs + brow * a.cols + (int64_t)ib * F::BL, p);
+            F::partial(w, act, p, si, sm);
           }
+          if (F::LPB == 8) {
+            si = group8_sum(si);
+            if (F::HAS_MIN) sm = group8_sum(sm);
+          }
+          if (on && p == F::LPB - 1)
+            term[(bb * a.rw + rr) * a.nblk + ib] = F::term(w, si, sm, a.ad[brow * a.nblk + ib]);
         }
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      for (int idx = lane; idx < nbc * nrow; idx += 64) {
-        const int bb = idx / nrow, rr = idx % nrow;
-        const float* t = term + (bb * a.rw + rr) * a.nblk;
-        float acc = 0.0f;
-        for (int ib = 0; ib < a.nblk; ++ib) acc = __fadd_rn(acc, t[ib]);
-        a.y[(b0 + bb) * a.rows + row0 + rr] = acc;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    return;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int idx = lane; idx < nbc * nrow; idx += 64) {
+      const int bb = idx / nrow, rr = idx % nrow;
+      const float* t = term + (bb * a.rw + rr) * a.nblk;
+      float acc = 0.0f;
+      for (int ib = 0; ib < a.nblk; ++ib) acc = __fadd_rn(acc, t[ib]);
+      a.y[(b0 + bb) * a.rows + row0 + rr] = acc;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  // FIXED: the row sums (one lane per row, blocks in order)
+}
+
+struct Int1Args {
+  const uint8_t* w;
+  int64_t rows, cols, row_bytes;
+  const float* x;
+  int nblk, rw;
+  float* y;
+};
+
+// One hidden state (nb = 1), cols <= P * 2048: the workgroup quantises x
+// into LDS itself (quantizeAct), each lane keeps its P activation slices in
+// registers, and the weight slices stream through a ring of kRing
+// (row, pass) units, each reloaded right after its use with the unit kRing
+// on, so every wave keeps the next unit's loads in flight while it computes
+// (deeper rings measured no faster: the grid's waves already cover the
+// memory latency).  Terms and row sums as in lm_int_kernel.
+template <int T, int P>
+__global__ __launch_bounds__(kLmNT) void lm_int1_kernel(Int1Args a) {
+  using F = Fmt<T>;
+  constexpr int SPP = 64 / F::LPB;  // blocks per pass
+  constexpr int kRing = P > 2 ? P : 2;  // (row, pass) units in the ring: one row or more
+  constexpr int RPI = kRing / P;         // rows per turn of the ring (>= 1)
+  extern __shared__ __align__(16) unsigned char s_mem[];
+  int8_t* s_act = reinterpret_cast<int8_t*>(s_mem);                  // [cols]
+  float* s_ad = reinterpret_cast<float*>(s_mem + a.cols);            // [nblk]
+  float* s_term = s_ad + ((a.nblk + 3) & ~3);                        // [waves][rw][nblk]
+  for (int base = 0; base < (int)(a.cols / 4); base += kLmNT) {
+    const int i4 = base + threadIdx.x;
+    quant4<F::BL>(a.x, i4, i4 * 4 < a.cols, s_act, s_ad);
+  }
+  __syncthreads();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  // the rows split evenly over the grid's waves (at most a.rw each)
+  const int64_t waves = (int64_t)gridDim.x * (kLmNT / 64), g = (int64_t)blockIdx.x * (kLmNT / 64) + wave;
+  const int64_t row0 = g * a.rows / waves;
+  const int nrow = (int)((g + 1) * a.rows / waves - row0);
+  if (nrow <= 0) return;
+  float* term = s_term + (size_t)wave * a.rw * a.nblk;
+  const int p = lane % F::LPB;
+  typename F::Act act[P];
+  float ad[P];
+  int ib[P], ibc[P];
+#pragma unroll
+  for (int ps = 0; ps < P; ++ps) {
+    ib[ps] = ps * SPP + lane / F::LPB;
+    ibc[ps] = min(ib[ps], a.nblk - 1);  // lanes past the row load a real block and write nothing
+    act[ps] = load_act<T>(s_act + ibc[ps] * F::BL, p);
+    ad[ps] = s_ad[ibc[ps]];
+  }
+  const uint8_t* wrow = a.w + row0 * a.row_bytes;  // wave-uniform
+  int loff[P];                                     // the lane's block offset in a row
+#pragma unroll
+  for (int ps = 0; ps < P; ++ps) loff[ps] = ibc[ps] * F::TS;
+  auto unit = [&](int rr, int ps) { return wrow + (int64_t)min(rr, nrow - 1) * a.row_bytes + loff[ps]; };
+  typename F::Wt ring[kRing];
+#pragma unroll
+  for (int d = 0; d < kRing; ++d) ring[d] = F::load_w(unit(d / P, d % P), p);
+  for (int rr0 = 0; rr0 < nrow; rr0 += RPI) {
+#pragma unroll
+    for (int d = 0; d < kRing; ++d) {
+      const int rr = rr0 + d / P, ps = d % P;
+      int si, sm;
+      F::partial(ring[d], act[ps], p, si, sm);
+      if (F::LPB == 8) {
+        si = group8_sum(si);
+        if (F::HAS_MIN) sm = group8_sum(sm);
+      }
+      if (rr < nrow && ib[ps] < a.nblk && p == F::LPB - 1)
+        term[rr * a.nblk + ib[ps]] = F::term(ring[d], si, sm, ad[ps]);
+      // the slot's next unit, kRing units on: loaded into the registers just
+      // freed, so the ring needs no copies between turns
+      ring[d] = F::load_w(unit(rr + RPI, ps), p);
+    }
+  }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (lane < nrow) {
     const float* t = term + lane * a.nblk;
     float acc = 0.0f;
-    for (int ib = 0; ib < a.nblk; ++ib) acc = __fadd_rn(acc, t[ib]);
+    for (int j = 0; j < a.nblk; ++j) acc = __fadd_rn(acc, t[j]);
     a.y[row0 + lane] = acc;
   }
 }
@@ -672,9 +783,56 @@ __global__ __launch_bounds__(kLmNT) void lora_apply_kernel(const float* __restri
 
 // ------------------------------------------------ launch helpers
 
+// Compute units of the current device and resident workgroups of a kernel
+// per CU, looked up once per process (one device's shape is assumed).
+int device_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                 hipSuccess || n <= 0)
+      n = 256;
+  }
+  return n;
+}
+
+template <int T, int P>
+hipError_t launch_int1(const LmHeadCall& c, int nblk, hipStream_t s) {
+  Int1Args a{static_cast<const uint8_t*>(c.w), c.rows, c.cols, c.row_bytes, c.x, nblk, 0, c.y};
+  // rows per wave: at most what a 4 KiB term buffer holds (and 32)
+  int cap = 32;
+  while (cap > 1 && (int64_t)cap * nblk * 4 > 4096) cap >>= 1;
+  const size_t lds = (size_t)c.cols + 4 * (size_t)((nblk + 3) & ~3) + (size_t)(kLmNT / 64) * cap * nblk * 4;
+  static int occ = 0;  // resident workgroups per CU at this LDS size
+  if (occ == 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, lm_int1_kernel<T, P>, kLmNT, lds) !=
+                       hipSuccess || occ <= 0))
+    occ = 4;
+  // one resident round of workgroups with the rows split evenly over their
+  // waves, unless that gives a wave more rows than the term buffer holds
+  const int64_t waves_min = (c.rows + cap - 1) / cap;
+  int64_t waves = std::max<int64_t>((int64_t)device_cus() * occ * (kLmNT / 64), waves_min);
+  waves = std::min<int64_t>(waves, c.rows);
+  const int64_t grid = (waves + kLmNT / 64 - 1) / (kLmNT / 64);
+  a.rw = (int)((c.rows + grid * (kLmNT / 64) - 1) / (grid * (kLmNT / 64)));
+  hipLaunchKernelGGL((lm_int1_kernel<T, P>), dim3((unsigned)grid), dim3(kLmNT), lds, s, a);
+  return hipGetLastError();
+}
+
 template <int T>
 hipError_t launch_int(const LmHeadCall& c, hipStream_t s) {
   using F = Fmt<T>;
+  const int nblk = (int)(c.cols / F::BL);
+  const int passes = (int)((c.cols / 32 + 63) / 64);
+  if (c.nb == 1 && passes <= 4) {
+    if (passes == 1) return launch_int1<T, 1>(c, nblk, s);
+    if (passes == 2) return launch_int1<T, 2>(c, nblk, s);
+    return launch_int1<T, 4>(c, nblk, s);
+  }
+  const int64_t n = (int64_t)c.nb * c.cols;
+  const int64_t qgrid = (n / 4 + kLmNT - 1) / kLmNT;
+  hipLaunchKernelGGL(quant_act_kernel<F::BL>, dim3((unsigned)qgrid), dim3(kLmNT), 0, s, c.x, n, c.act_qs, c.act_d);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   IntArgs a;
   a.w = static_cast<const uint8_t*>(c.w);
   a.rows = c.rows;
@@ -683,21 +841,17 @@ hipError_t launch_int(const LmHeadCall& c, hipStream_t s) {
   a.aqs = c.act_qs;
   a.ad = c.act_d;
   a.nb = c.nb;
-  a.nblk = (int)(c.cols / F::BL);
-  a.passes = (int)((c.cols / 32 + 63) / 64);
+  a.nblk = nblk;
+  a.passes = passes;
   a.y = c.y;
-  const bool fixed = a.passes == 1 && c.nb == 1;
-  const int nbc = fixed ? 1 : std::min(c.nb, kLmNBC);
+  const int nbc = std::min(c.nb, kLmNBC);
   // rows per wave: 16, fewer when the per-wave term buffer would pass 4 KiB
   int rw = 16;
   while (rw > 1 && (int64_t)nbc * rw * a.nblk * 4 > 4096) rw >>= 1;
   a.rw = rw;
   const size_t lds = (size_t)(kLmNT / 64) * nbc * rw * a.nblk * sizeof(float);
   const int64_t grid = (c.rows + (int64_t)rw * (kLmNT / 64) - 1) / ((int64_t)rw * (kLmNT / 64));
-  if (fixed)
-    hipLaunchKernelGGL((lm_int_kernel<T, true>), dim3((unsigned)grid), dim3(kLmNT), lds, s, a);
-  else
-    hipLaunchKernelGGL((lm_int_kernel<T, false>), dim3((unsigned)grid), dim3(kLmNT), lds, s, a);
+  hipLaunchKernelGGL(lm_int_kernel<T>, dim3((unsigned)grid), dim3(kLmNT), lds, s, a);
   return hipGetLastError();
 }
 
@@ -732,14 +886,6 @@ bool lm_type_supported(int type) {
 hipError_t launch_lm_head(const LmHeadCall& c, hipStream_t s) {
   hipError_t e = hipSuccess;
   if (c.use_act) {
-    const int bl = lm_act_block_len(c.type);
-    const int64_t n = (int64_t)c.nb * c.cols;
-    const int64_t grid = (n / 4 + kLmNT - 1) / kLmNT;
-    if (bl == 256)
-      hipLaunchKernelGGL(quant_act_kernel<256>, dim3((unsigned)grid), dim3(kLmNT), 0, s, c.x, n, c.act_qs, c.act_d);
-    else
-      hipLaunchKernelGGL(quant_act_kernel<32>, dim3((unsigned)grid), dim3(kLmNT), 0, s, c.x, n, c.act_qs, c.act_d);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
     switch (c.type) {
       case 14: e = launch_int<14>(c, s); break;
       case 12: e = launch_int<12>(c, s); break;

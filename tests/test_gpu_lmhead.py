@@ -74,6 +74,10 @@ def test_int8_path_parity(pkg, name):
         for nb in (1, 2, 4):
             print(f"lm_head int8 {name} rows=1000 cols={cols} nb={nb}", flush=True)
             run_case(pkg, t, 1000, cols, nb, seed=10 * ci + nb)
+    # one hidden state over 3 or 4 passes of 2048 weights (rows streamed in a ring)
+    big = 8192 if bs == 256 else 6144
+    print(f"lm_head int8 {name} rows=300 cols={big} nb=1", flush=True)
+    run_case(pkg, t, 300, big, 1, seed=77)
     if t != TYPES["Q8_0"]:  # Q8_0 takes the float path above 4 rows (model.nim:185)
         print(f"lm_head int8 {name} rows=333 cols={cols_list[1]} nb=9", flush=True)
         run_case(pkg, t, 333, cols_list[1], 9, seed=99)
