@@ -160,6 +160,22 @@ def traffic_summary(args):
     print("\n".join(lines))
 
 
+def copy_ref(dev):
+    """A plain 256 MiB device copy, three times: the kernel of known size that
+    scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes."""
+    import torch
+
+    n = 64 * 1024 * 1024  # 64 Mi floats = 256 MiB read and 256 MiB written per copy
+    a = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+    return n * 4
+
+
 def host_cores():
     """Cores this process may use, capped at the 16 a one-GPU box grants."""
     try:
@@ -514,6 +530,14 @@ def bench_lm_head(args):
                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": kern,
                         "kernel_avg_us": ms * 1e3, "algorithmic_bytes_per_launch": nbytes},
            "parity_spot_check": {"rows": 1024, "bit_exact": ok}}
+    if (t, rows, cols, nb, bool(args.lm_exact)) == (14, 128256, 2048, 1, False):
+        traffic, why = read_traffic("lm_head_q6k")
+        if traffic.get("lm_int1_kernel"):
+            res["roofline"]["traffic"] = traffic["lm_int1_kernel"]
+        else:
+            res["roofline"]["traffic_note"] = why or "no lm_int1_kernel line"
+    if args.copy_ref:
+        res["copy_ref_bytes"] = copy_ref(dev)
     if not args.no_cpu_baseline:
         def run(nthreads, budget):
             # rows in chunks of 256 per thread until the budget is spent
@@ -938,15 +962,7 @@ def main():
         res["roofline"]["traffic_note"] = stale
     s.close()
     if args.copy_ref:
-        n = 64 * 1024 * 1024  # 64 Mi floats = 256 MiB read and 256 MiB written per copy
-        a = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
-        b = torch.empty_like(a)
-        torch.cuda.synchronize()
-        for _ in range(3):
-            b.copy_(a)
-        torch.cuda.synchronize()
-        res["copy_ref_bytes"] = n * 4
-        del a, b
+        res["copy_ref_bytes"] = copy_ref(dev)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, args.cpu_budget)
         res["cpu_baseline_all_cores"] = cpu_baseline(w, args.cpu_budget, nthreads=host_cores())
