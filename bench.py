@@ -85,7 +85,7 @@ def read_traffic(workload):
         if line.startswith("source_hash:"):
             stamp = line.split(":", 1)[1].strip()
         elif line.startswith("traffic_bytes_per_launch "):
-            k, v = line[len("traffic_bytes_per_launch "):].split(":", 1)
+            k, v = line[len("traffic_bytes_per_launch "):].rsplit(":", 1)
             out[k.strip()] = float(v)
     if stamp != source_hash():
         return {}, f"traffic profile measured on sources {stamp}, not these ({source_hash()})"
@@ -151,7 +151,7 @@ def traffic_summary(args):
              "|---|---|---|---|---|"]
     totals = {}
     for k, (fv, n, _) in sorted(per["FETCH_SIZE"].items()):
-        if "copyBuffer" in k or "fillBuffer" in k:
+        if "copyBuffer" in k or "fillBuffer" in k or k.startswith("at::") or "at::native" in k:
             continue
         wv = per["WRITE_SIZE"].get(k, (0.0, 0, 0.0))[0]
         b = fv * 1024 * f_fac + wv * 1024 * w_fac
