@@ -585,6 +585,7 @@ void stream_kernel(const StreamArgs a) {
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wv = tid >> 6;
+    if (wv == 0) NLS_STAMP(row, 0);
     // The row's history ring and bias entries are requested first: they do not
     // depend on the row constants, so they go out while those load, before any
     // tile traffic.  Thread tid reads ring slots h * NT + tid and bias entry
@@ -849,6 +850,7 @@ void stream_kernel(const StreamArgs a) {
     float x0raw = 0.0f;
 
     // ---- the stream ----
+    if (wv == 0) NLS_STAMP(row, 1);
     float bv = -__builtin_inff();
     int bi = 0x7fffffff;
     int buf_n = 0, cur = 0;
@@ -866,6 +868,11 @@ void stream_kernel(const StreamArgs a) {
       spec_rank = r < k ? (int)r : 0;
     }
     bool spec_used = false;
+#ifdef NLS_PHASE_STAMPS
+    uint64_t st_refresh_ticks = 0;  // time inside block-path refreshes
+    int st_refreshes = 0;
+    uint64_t st_tiles = 0;
+#endif
     // wave path (k <= 64): this wave's buffer count, threshold and overflow
     int wn = 0;
     uint32_t wtau = 0u;
@@ -1146,6 +1153,10 @@ void stream_kernel(const StreamArgs a) {
           return;
         }
         // threshold refresh (uniform): raise tau, compact into the other buffer
+#ifdef NLS_PHASE_STAMPS
+        const uint64_t st_r0 = __builtin_amdgcn_s_memrealtime();
+        ++st_refreshes;
+#endif
         uint64_t* nb = cand + (size_t)(cur ^ 1) * a.ccap;
         uint32_t tops[Q];
   #pragma unroll
@@ -1219,6 +1230,9 @@ void stream_kernel(const StreamArgs a) {
         for (int q = 0; q < NE; ++q)
           if (use(q) && key[q] >= t1) nb[pos++] = ((uint64_t)key[q] << 32) | gid(q);
         __syncthreads();
+#ifdef NLS_PHASE_STAMPS
+        st_refresh_ticks += __builtin_amdgcn_s_memrealtime() - st_r0;
+#endif
         cur ^= 1;
         buf_n = tot;
         tau = t1;
@@ -1261,10 +1275,21 @@ void stream_kernel(const StreamArgs a) {
           R0[j] = load_group<GS, VEC>(rs, tn * UE, j, uth);
         }
         process(v, t, first);
+#ifdef NLS_PHASE_STAMPS
+        ++st_tiles;
+#endif
         if (stop() || tn >= nunits) break;
         t = tn;
       }
     }
+    if (wv == 0) NLS_STAMP(row, 2);
+#ifdef NLS_PHASE_STAMPS
+    if (wv == 0) {
+      NLS_STAMP_VALUE(row, 13, st_refreshes);
+      NLS_STAMP_VALUE(row, 14, st_refresh_ticks);
+      NLS_STAMP_VALUE(row, 15, st_tiles);
+    }
+#endif
     // The final value of patched slot p from its original logit: penalties then
     // bias (:71-76), then temperature (:80-81) on the sampling rows.
     auto patched_final = [&](int p, float v, uint32_t fl) -> float {
@@ -1643,11 +1668,14 @@ void stream_kernel(const StreamArgs a) {
     }
     // ---- the row's heap-path members, then the reference's tail ----
     uint64_t* mem = reinterpret_cast<uint64_t*>(regA);
+    if (wv == 0) NLS_STAMP(row, 3);
+    NLS_STAMP_VALUE(row, 12, N);
     // (after a speculative threshold fewer than k elements may reach it)
     if ((spec_used && N < k) || !topk_members<NT>(ent, N, k, mem, a.mcap, shist, smem, &s_cnt)) {
       if (tid == 0) pushed = push_generic(a.generic_list, a.generic_count, row);
       return;
     }
+    if (wv == 0) NLS_STAMP(row, 4);
     if (k <= kWave) {
       if (wv != 0) return;
       double u = 0.0;
@@ -1669,7 +1697,9 @@ void stream_kernel(const StreamArgs a) {
     }
     if (tid == 0) s_u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
     __syncthreads();
+    if (wv == 0) NLS_STAMP(row, 5);
     const TailOut to = softmax_cutoff_draw<NT>(vals, ids, ebuf, k, P, s_u, smem);
+    if (wv == 0) NLS_STAMP(row, 6);
     if (tid == 0) a.out[row] = to.id;
     write_debug<NT>(a.dbg, row, 2, to.n, k, to.total, ids, ebuf);
   };

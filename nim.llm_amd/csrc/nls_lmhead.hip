@@ -496,30 +496,32 @@ struct Int1Args {
   const uint8_t* w;
   int64_t rows, cols, row_bytes;
   const float* x;
-  int nblk, rw;
+  int nb, nblk, rw;
   float* y;
 };
 
-// One hidden state (nb = 1), cols <= P * 2048: the workgroup quantises x
-// into LDS itself (quantizeAct), each lane keeps its P activation slices in
-// registers, and the weight slices stream through a ring of kRing
-// (row, pass) units, each reloaded right after its use with the unit kRing
-// on, so every wave keeps the next unit's loads in flight while it computes
-// (deeper rings measured no faster: the grid's waves already cover the
-// memory latency).  Terms and row sums as in lm_int_kernel.
-template <int T, int P>
+// Up to NB hidden states (nb <= NB), cols <= P * 2048: the workgroup
+// quantises x into LDS itself (quantizeAct), each lane keeps its NB x P
+// activation slices in registers, and the weight slices stream through a ring
+// of kRing (row, pass) units, each reloaded right after its use with the unit
+// kRing on, so every wave keeps the next unit's loads in flight while it
+// computes (deeper rings measured no faster: the grid's waves already cover
+// the memory latency).  Each weight slice, loaded once, serves all nb rows.
+// Terms and row sums as in lm_int_kernel.
+template <int T, int P, int NB>
 __global__ __launch_bounds__(kLmNT) void lm_int1_kernel(Int1Args a) {
   using F = Fmt<T>;
   constexpr int SPP = 64 / F::LPB;  // blocks per pass
   constexpr int kRing = P > 2 ? P : 2;  // (row, pass) units in the ring: one row or more
   constexpr int RPI = kRing / P;         // rows per turn of the ring (>= 1)
   extern __shared__ __align__(16) unsigned char s_mem[];
-  int8_t* s_act = reinterpret_cast<int8_t*>(s_mem);                  // [cols]
-  float* s_ad = reinterpret_cast<float*>(s_mem + a.cols);            // [nblk]
-  float* s_term = s_ad + ((a.nblk + 3) & ~3);                        // [waves][rw][nblk]
-  for (int base = 0; base < (int)(a.cols / 4); base += kLmNT) {
+  const int nb = a.nb;
+  int8_t* s_act = reinterpret_cast<int8_t*>(s_mem);                          // [nb][cols]
+  float* s_ad = reinterpret_cast<float*>(s_mem + (size_t)nb * a.cols);       // [nb][nblk]
+  float* s_term = s_ad + ((nb * a.nblk + 3) & ~3);                           // [waves][nb][rw][nblk]
+  for (int base = 0; base < (int)(nb * a.cols / 4); base += kLmNT) {
     const int i4 = base + threadIdx.x;
-    quant4<F::BL>(a.x, i4, i4 * 4 < a.cols, s_act, s_ad);
+    quant4<F::BL>(a.x, i4, i4 * 4 < nb * a.cols, s_act, s_ad);
   }
   __syncthreads();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -528,17 +530,24 @@ __global__ __launch_bounds__(kLmNT) void lm_int1_kernel(Int1Args a) {
   const int64_t row0 = g * a.rows / waves;
   const int nrow = (int)((g + 1) * a.rows / waves - row0);
   if (nrow <= 0) return;
-  float* term = s_term + (size_t)wave * a.rw * a.nblk;
+  float* term = s_term + (size_t)wave * nb * a.rw * a.nblk;
   const int p = lane % F::LPB;
-  typename F::Act act[P];
-  float ad[P];
+  typename F::Act act[NB][P];
+  float ad[NB][P];
   int ib[P], ibc[P];
 #pragma unroll
   for (int ps = 0; ps < P; ++ps) {
     ib[ps] = ps * SPP + lane / F::LPB;
     ibc[ps] = min(ib[ps], a.nblk - 1);  // lanes past the row load a real block and write nothing
-    act[ps] = load_act<T>(s_act + ibc[ps] * F::BL, p);
-    ad[ps] = s_ad[ibc[ps]];
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int bc = min(b, nb - 1);  // rows past nb repeat the last and write nothing
+#pragma unroll
+    for (int ps = 0; ps < P; ++ps) {
+      act[b][ps] = load_act<T>(s_act + (size_t)bc * a.cols + ibc[ps] * F::BL, p);
+      ad[b][ps] = s_ad[bc * a.nblk + ibc[ps]];
+    }
   }
   const uint8_t* wrow = a.w + row0 * a.row_bytes;  // wave-uniform
   int loff[P];                                     // the lane's block offset in a row
@@ -552,14 +561,17 @@ __global__ __launch_bounds__(kLmNT) void lm_int1_kernel(Int1Args a) {
 #pragma unroll
     for (int d = 0; d < kRing; ++d) {
       const int rr = rr0 + d / P, ps = d % P;
-      int si, sm;
-      F::partial(ring[d], act[ps], p, si, sm);
-      if (F::LPB == 8) {
-        si = group8_sum(si);
-        if (F::HAS_MIN) sm = group8_sum(sm);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        int si, sm;
+        F::partial(ring[d], act[b][ps], p, si, sm);
+        if (F::LPB == 8) {
+          si = group8_sum(si);
+          if (F::HAS_MIN) sm = group8_sum(sm);
+        }
+        if (b < nb && rr < nrow && ib[ps] < a.nblk && p == F::LPB - 1)
+          term[(b * a.rw + rr) * a.nblk + ib[ps]] = F::term(ring[d], si, sm, ad[b][ps]);
       }
-      if (rr < nrow && ib[ps] < a.nblk && p == F::LPB - 1)
-        term[rr * a.nblk + ib[ps]] = F::term(ring[d], si, sm, ad[ps]);
       // the slot's next unit, kRing units on: loaded into the registers just
       // freed, so the ring needs no copies between turns
       ring[d] = F::load_w(unit(rr + RPI, ps), p);
@@ -568,11 +580,12 @@ __global__ __launch_bounds__(kLmNT) void lm_int1_kernel(Int1Args a) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane < nrow) {
-    const float* t = term + lane * a.nblk;
+  for (int idx = lane; idx < nb * nrow; idx += 64) {
+    const int b = idx / nrow, rr = idx - b * nrow;
+    const float* t = term + (b * a.rw + rr) * a.nblk;
     float acc = 0.0f;
     for (int j = 0; j < a.nblk; ++j) acc = __fadd_rn(acc, t[j]);
-    a.y[row0 + lane] = acc;
+    a.y[(int64_t)b * a.rows + row0 + rr] = acc;
   }
 }
 
@@ -796,17 +809,22 @@ int device_cus() {
   return n;
 }
 
-template <int T, int P>
+template <int T, int P, int NB>
 hipError_t launch_int1(const LmHeadCall& c, int nblk, hipStream_t s) {
-  Int1Args a{static_cast<const uint8_t*>(c.w), c.rows, c.cols, c.row_bytes, c.x, nblk, 0, c.y};
+  Int1Args a{static_cast<const uint8_t*>(c.w), c.rows, c.cols, c.row_bytes, c.x, c.nb, nblk, 0, c.y};
   // rows per wave: at most what a 4 KiB term buffer holds (and 32)
   int cap = 32;
-  while (cap > 1 && (int64_t)cap * nblk * 4 > 4096) cap >>= 1;
-  const size_t lds = (size_t)c.cols + 4 * (size_t)((nblk + 3) & ~3) + (size_t)(kLmNT / 64) * cap * nblk * 4;
-  static int occ = 0;  // resident workgroups per CU at this LDS size
-  if (occ == 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, lm_int1_kernel<T, P>, kLmNT, lds) !=
-                       hipSuccess || occ <= 0))
-    occ = 4;
+  while (cap > 1 && (int64_t)cap * NB * nblk * 4 > 4096) cap >>= 1;
+  const size_t lds = (size_t)c.nb * c.cols + 4 * (size_t)((c.nb * nblk + 3) & ~3) +
+                     (size_t)(kLmNT / 64) * c.nb * cap * nblk * 4;
+  static int occ = 0;  // resident workgroups per CU at the largest LDS size of this instance
+  if (occ == 0) {
+    const size_t lds_max = (size_t)NB * c.cols + 4 * (size_t)((NB * nblk + 3) & ~3) +
+                           (size_t)(kLmNT / 64) * NB * cap * nblk * 4;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, lm_int1_kernel<T, P, NB>, kLmNT, lds_max) !=
+            hipSuccess || occ <= 0)
+      occ = 4;
+  }
   // one resident round of workgroups with the rows split evenly over their
   // waves, unless that gives a wave more rows than the term buffer holds
   const int64_t waves_min = (c.rows + cap - 1) / cap;
@@ -814,7 +832,7 @@ hipError_t launch_int1(const LmHeadCall& c, int nblk, hipStream_t s) {
   waves = std::min<int64_t>(waves, c.rows);
   const int64_t grid = (waves + kLmNT / 64 - 1) / (kLmNT / 64);
   a.rw = (int)((c.rows + grid * (kLmNT / 64) - 1) / (grid * (kLmNT / 64)));
-  hipLaunchKernelGGL((lm_int1_kernel<T, P>), dim3((unsigned)grid), dim3(kLmNT), lds, s, a);
+  hipLaunchKernelGGL((lm_int1_kernel<T, P, NB>), dim3((unsigned)grid), dim3(kLmNT), lds, s, a);
   return hipGetLastError();
 }
 
@@ -823,11 +841,15 @@ hipError_t launch_int(const LmHeadCall& c, hipStream_t s) {
   using F = Fmt<T>;
   const int nblk = (int)(c.cols / F::BL);
   const int passes = (int)((c.cols / 32 + 63) / 64);
+  // up to four hidden states with each weight slice loaded once for all;
+  // activation slices held in registers for nb x passes <= 4
   if (c.nb == 1 && passes <= 4) {
-    if (passes == 1) return launch_int1<T, 1>(c, nblk, s);
-    if (passes == 2) return launch_int1<T, 2>(c, nblk, s);
-    return launch_int1<T, 4>(c, nblk, s);
+    if (passes == 1) return launch_int1<T, 1, 1>(c, nblk, s);
+    if (passes == 2) return launch_int1<T, 2, 1>(c, nblk, s);
+    return launch_int1<T, 4, 1>(c, nblk, s);
   }
+  if (c.nb == 2 && passes <= 2) return passes == 1 ? launch_int1<T, 1, 2>(c, nblk, s) : launch_int1<T, 2, 2>(c, nblk, s);
+  if (c.nb <= 4 && passes == 1) return launch_int1<T, 1, 4>(c, nblk, s);
   const int64_t n = (int64_t)c.nb * c.cols;
   const int64_t qgrid = (n / 4 + kLmNT - 1) / kLmNT;
   hipLaunchKernelGGL(quant_act_kernel<F::BL>, dim3((unsigned)qgrid), dim3(kLmNT), 0, s, c.x, n, c.act_qs, c.act_d);

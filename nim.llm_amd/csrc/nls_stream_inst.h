@@ -47,8 +47,20 @@ hipError_t set_stream_attributes() {
 
 }  // namespace nls
 
+#ifdef NLS_PHASE_STAMPS
+// this unit's copy of the phase stamps (the phases build only)
+#define NLS_STREAM_STAMP_READER(NT, VEC)                                                            \
+  extern "C" int nls_stream_stamps_##NT##_##VEC(uint64_t* out) {                                    \
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(nls::nls_phase_stamp),                               \
+                               sizeof(uint64_t) * nls::kStampRows * 16) == hipSuccess ? 0 : 3;      \
+  }
+#else
+#define NLS_STREAM_STAMP_READER(NT, VEC)
+#endif
+
 #define NLS_INSTANTIATE_STREAM(NT, VEC)                                                             \
   namespace nls {                                                                                  \
   template hipError_t launch_stream_variant<NT, VEC>(const StreamArgs&, const LaunchPlan&, hipStream_t); \
   template hipError_t set_stream_attributes<NT, VEC>();                                            \
-  }
+  }                                                                                                \
+  NLS_STREAM_STAMP_READER(NT, VEC)

@@ -71,7 +71,7 @@ def test_int8_path_parity(pkg, name):
     bs = O.block_size(t)
     cols_list = [256, 2048, 3072] if bs == 256 else [896, 2048, 2080]
     for ci, cols in enumerate(cols_list):
-        for nb in (1, 2, 4):
+        for nb in (1, 2, 3, 4):
             print(f"lm_head int8 {name} rows=1000 cols={cols} nb={nb}", flush=True)
             run_case(pkg, t, 1000, cols, nb, seed=10 * ci + nb)
     # one hidden state over 3 or 4 passes of 2048 weights (rows streamed in a ring)
