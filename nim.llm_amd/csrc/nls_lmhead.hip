@@ -53,18 +53,9 @@ __device__ __forceinline__ uint4 ld_16(const void* p) {
   __builtin_memcpy(&v, p, 16);
   return v;
 }
-// 8 or 32 bytes at a 2-byte aligned address, read as 4-byte aligned words
-// and funnel-shifted (the words past the field are read only when the
+// 4-byte aligned words covering NW * 4 bytes at a 2-byte aligned address,
+// funnel-shifted into place (the word past the field is read only when the
 // address is not 4-byte aligned, and never past the field's last word).
-__device__ __forceinline__ uint2 ld_8a(const uint8_t* p) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint32_t sh = (uint32_t)(a & 3) * 8;
-  const uint32_t* q = reinterpret_cast<const uint32_t*>(p - (a & 3));
-  uint2 w;
-  __builtin_memcpy(&w, q, 8);
-  const uint32_t w2 = sh ? q[2] : 0u;
-  return make_uint2(__builtin_amdgcn_alignbit(w.y, w.x, sh), __builtin_amdgcn_alignbit(w2, w.y, sh));
-}
 template <int NW>
 __device__ __forceinline__ void ld_words_a(const uint8_t* p, uint32_t (&out)[NW]) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(p);
@@ -724,26 +715,98 @@ struct FloatArgs {
   float* y;
 };
 
+// Eight consecutive weights e0 .. e0 + 7 of a dequantised row (e0 a multiple
+// of 8; past `cols` they read 0 without touching memory).
+template <int T>
+__device__ __forceinline__ void deq8(const uint8_t* __restrict__ rp, int64_t e0, int64_t cols, float (&w)[8]) {
+  if (e0 + 8 <= cols) {
+    if constexpr (T == 0) {  // F32: two 16-byte loads
+      const uint4 a = ld_16(rp + 4 * e0), b = ld_16(rp + 4 * e0 + 16);
+      const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = __uint_as_float(u[j]);
+    } else if constexpr (T == 1 || T == 30) {  // F16, BF16: one 16-byte load
+      const uint4 a = ld_16(rp + 2 * e0);
+      const uint32_t u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (T == 1) {
+          w[2 * j] = half_f(u[j] & 0xFFFF);
+          w[2 * j + 1] = half_f(u[j] >> 16);
+        } else {
+          w[2 * j] = __uint_as_float(u[j] << 16);
+          w[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = deq1<T>(rp, e0 + j);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[j] = e0 + j < cols ? deq1<T>(rp, e0 + j) : 0.0f;
+  }
+}
+
 // dotF32 (quant.nim:362-374) of each dequantised row with each x row: lane
 // k of an aligned group of 8 runs chain k (weights k, k + 8, ...), lane 0
-// takes the cols % 8 tail, and the chains combine as the reference adds them.  32 rows per
-// workgroup; up to kLmNBC activation rows per pass over the row.
-template <int T>
+// takes the cols % 8 tail, and the chains combine as the reference adds them.
+// The row is read in 16-byte pieces: the 8 lanes of a row dequantise 64
+// consecutive weights (8 each) and pass them through LDS so that lane k holds
+// chain k's 8 of them.  32 rows per workgroup; up to kLmNBC activation rows
+// per pass over the row.
+template <int T, bool XLDS>
 __global__ __launch_bounds__(kLmNT) void lm_float_kernel(FloatArgs a) {
-  const int k = threadIdx.x & 7;
-  const int64_t r = (int64_t)blockIdx.x * (kLmNT / 8) + (threadIdx.x >> 3);
-  if (r >= a.rows) return;  // whole groups of 8 leave together
-  const uint8_t* rp = a.w + r * a.row_bytes;
+  __shared__ float s_t[kLmNT / 8][8][9];  // per row group: [lane][its 8 weights], padded
+  // XLDS: the activations of the pass, chain-major: xt[bb][k][j] = x[bb][8 j + k]
+  extern __shared__ __align__(16) float xt[];
+  const int k = threadIdx.x & 7, grp = threadIdx.x >> 3;
+  const int64_t r = (int64_t)blockIdx.x * (kLmNT / 8) + grp;
+  const bool live = r < a.rows;  // (groups past the last row still take part in the exchanges)
+  const uint8_t* rp = a.w + min(r, a.rows - 1) * a.row_bytes;
   const int64_t c8 = a.cols & ~(int64_t)7;
+  const int s8 = (int)(c8 / 8);  // steps of a chain
   for (int b0 = 0; b0 < a.nb; b0 += kLmNBC) {
     const int nbc = min(kLmNBC, a.nb - b0);
     float acc[kLmNBC] = {0.0f, 0.0f, 0.0f, 0.0f};
     const float* xb = a.x + (int64_t)b0 * a.cols;
-    for (int64_t e = k; e < c8; e += 8) {
-      const float w = deq1<T>(rp, e);
+    if constexpr (XLDS) {
+      __syncthreads();  // the previous pass is done with xt
+      for (int i = threadIdx.x; i < nbc * (int)c8; i += kLmNT) {
+        const int bb = i / (int)c8, e = i - bb * (int)c8;
+        xt[(bb * 8 + (e & 7)) * s8 + (e >> 3)] = xb[(int64_t)bb * a.cols + e];
+      }
+      __syncthreads();
+    }
+    for (int64_t seg = 0; seg < c8; seg += 64) {
+      float w[8];
+      deq8<T>(rp, seg + 8 * k, c8, w);
 #pragma unroll
-      for (int bb = 0; bb < kLmNBC; ++bb)
-        if (bb < nbc) acc[bb] = __fadd_rn(acc[bb], __fmul_rn(w, xb[bb * a.cols + e]));
+      for (int j = 0; j < 8; ++j) s_t[grp][k][j] = w[j];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // chain k's weights of this segment: element seg + 8 j + k sits at
+      // lane j's slot k
+      float cw[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cw[j] = s_t[grp][j][k];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int j0 = (int)(seg >> 3);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t e = seg + 8 * j + k;
+        if (e < c8) {
+#pragma unroll
+          for (int bb = 0; bb < kLmNBC; ++bb)
+            if (bb < nbc) {
+              const float xv = XLDS ? xt[(bb * 8 + k) * s8 + j0 + j] : xb[bb * a.cols + e];
+              acc[bb] = __fadd_rn(acc[bb], __fmul_rn(cw[j], xv));
+            }
+        }
+      }
     }
     if (k == 0) {
       for (int64_t e = c8; e < a.cols; ++e) {
@@ -756,7 +819,7 @@ __global__ __launch_bounds__(kLmNT) void lm_float_kernel(FloatArgs a) {
 #pragma unroll
     for (int bb = 0; bb < kLmNBC; ++bb) {
       const float t = group8_dotf32_combine(acc[bb]);
-      if (bb < nbc && k == 6) a.y[(int64_t)(b0 + bb) * a.rows + r] = t;
+      if (live && bb < nbc && k == 6) a.y[(int64_t)(b0 + bb) * a.rows + r] = t;
     }
   }
 }
@@ -881,7 +944,12 @@ template <int T>
 hipError_t launch_float(const LmHeadCall& c, hipStream_t s) {
   FloatArgs a{static_cast<const uint8_t*>(c.w), c.rows, c.cols, c.row_bytes, c.x, c.nb, c.y};
   const int64_t grid = (c.rows + kLmNT / 8 - 1) / (kLmNT / 8);
-  hipLaunchKernelGGL(lm_float_kernel<T>, dim3((unsigned)grid), dim3(kLmNT), 0, s, a);
+  // the activations of a pass in LDS when they fit in 32 KiB
+  const size_t xbytes = (size_t)std::min(c.nb, kLmNBC) * (size_t)(c.cols & ~(int64_t)7) * 4;
+  if (xbytes <= 32768)
+    hipLaunchKernelGGL((lm_float_kernel<T, true>), dim3((unsigned)grid), dim3(kLmNT), xbytes, s, a);
+  else
+    hipLaunchKernelGGL((lm_float_kernel<T, false>), dim3((unsigned)grid), dim3(kLmNT), 0, s, a);
   return hipGetLastError();
 }
 
