@@ -67,6 +67,7 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
   __shared__ float s_part[NW];
   __shared__ int s_cnt;
   __shared__ SeqSumShared sh;
+  __shared__ double s_pow2[kExpfPow2Count];  // the exponential's table
   const int row = (int)blockIdx.x;
   const int tid = (int)threadIdx.x;
   const int lane = lane_id();
@@ -131,6 +132,8 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
   {
     float a[kTopPer], b[kTopPer];
     load(0, a);
+    // (after the first chunk's requests; the barrier after this pass orders it)
+    if (tid < kExpfPow2Count) s_pow2[tid] = kExpfPow2J64[tid];
     for (int c0 = 0; c0 < nV; c0 += kTopCh) {
       const bool more = c0 + kTopCh < nV;
       if (more) load(c0 + kTopCh, b);
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
       for (int q = 0; q < kTopPer; ++q) {
         const int e = elem(c0, q);
         if (e < nV) {
-          ebuf[e - c0] = expf_cr(v[q] - mx);
+          ebuf[e - c0] = expf_cr_t(v[q] - mx, s_pow2);
           const uint32_t k = f2key(v[q]);
           if (m <= NT && k >= t0) {
             const int slot = atomicAdd(&s_cnt, 1);
@@ -189,7 +192,7 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
   }
   const int nl = s_cnt;
   // probs[i] /= s (:57)
-  auto prob_of = [&](float l) -> float { return expf_cr(l - mx) / s; };
+  auto prob_of = [&](float l) -> float { return expf_cr_t(l - mx, s_pow2) / s; };
   auto pkey = [&](float l) -> uint32_t { return f2key(prob_of(l)); };
 
   uint64_t* mem = reinterpret_cast<uint64_t*>(ebuf);
@@ -454,9 +457,19 @@ __global__ void generate_step_kernel(const int32_t* __restrict__ out, int B, int
   hist_len[b] = len + 1;
 }
 
+// Both device evaluations of the exponential: y[i] = exp(x[i]) when they
+// agree, else a NaN with the payload 0xdead (so a checksum over every input
+// covers both).
 __global__ void expf_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+  __shared__ double pow2[kExpfPow2Count];
+  if (threadIdx.x < kExpfPow2Count) pow2[threadIdx.x] = kExpfPow2J64[threadIdx.x];
+  __syncthreads();
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = expf_cr(x[i]);
+  if (i < n) {
+    const float a = expf_cr(x[i]);
+    const float b = expf_cr_t(x[i], pow2);
+    y[i] = __float_as_uint(a) == __float_as_uint(b) ? a : __uint_as_float(0x7fc0deadu);
+  }
 }
 
 // ---------------------------------------------------------------------------

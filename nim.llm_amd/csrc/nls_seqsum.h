@@ -37,6 +37,10 @@ namespace nls {
 
 constexpr int kSeqSat = 1 << 26;  // increments saturate here (no binade holds 2^24 steps of u)
 constexpr int kSeqMaxJ = 16;      // terms per thread in one window
+// The first terms of a sum are added one at a time by one lane: while the sum
+// is a few terms large it changes binade every few terms, and each change
+// would end a window of the workgroup scan.
+constexpr int kSeqSerial = 1024;
 
 // A parity map, packed: a = (d0 << 1) | p0 and c = (d1 << 1) | p1, where d_p
 // is the increment of S for incoming parity p (saturating at kSeqSat) and p_p
@@ -245,8 +249,9 @@ __device__ __forceinline__ SeqMap seq_thread_map(const float* e, int b, int end,
 // writes).  J (in/out, 1 .. kSeqMaxJ) is the window's terms per thread and w
 // (in/out) the window count, both carried from one call to the next over the
 // chunks of a row (start them at 1 and 0, after seq_sum_init and a barrier);
-// `done` is the number of terms summed before e[0].  Two barriers per
-// window; the call ends with one.
+// `done` is the number of terms summed before e[0]; a call with done == 0 and
+// w == 0 (the first of a row) adds the first kSeqSerial terms on one lane
+// first.  Two barriers per window; the call ends with one.
 template <int NT>
 __device__ float seq_sum_block(const float* e, int len, float s, int& J, int& w, int done,
                                SeqSumShared& sh) {
@@ -256,6 +261,28 @@ __device__ float seq_sum_block(const float* e, int len, float s, int& J, int& w,
   const int lane = lane_id();
   const int wv = tid >> 6;
   int pos = 0;
+  if (done == 0 && w == 0 && len > 0) {
+    const int n0 = min(len, kSeqSerial);
+    if (tid == 0) {
+      float t = s;
+      int i = 0;
+      for (; i + 8 <= n0; i += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = e[i + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t = t + v[j];
+      }
+      for (; i < n0; ++i) t = t + e[i];
+      sh.s[1] = t;
+    }
+    __syncthreads();
+    // (the first window writes sh.s[0] only; the second writes sh.s[1] after
+    // its first barrier, which every thread reaches after this read)
+    s = sh.s[1];
+    pos = n0;
+    J = seq_next_j(n0);
+  }
   while (pos < len) {  // uniform
     if (!(s <= 3.4028234663852886e38f)) {
       // NaN or +inf: plain adds

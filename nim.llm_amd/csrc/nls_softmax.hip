@@ -4,11 +4,12 @@
 // One 1024-thread workgroup per row, three steps:
 //   1. mx, the row's float32 maximum (Nim's max(mx, v) keeps mx for a NaN v,
 //      as fmaxf does; the sign of a zero maximum changes no l - mx).
-//   2. s, the fp32 sum of exp(l - mx) (correctly rounded, nls_expf.h) in
-//      index order: chunks of 12288 exponentials go to LDS -- the next
-//      chunk's logits are requested before the current chunk is summed --
-//      and the workgroup adds each chunk exactly as one-at-a-time fp32 adds
-//      would, with the parity-map scan of nls_seqsum.h.
+//   2. s, the fp32 sum of exp(l - mx) (correctly rounded: nls_expf.h's table
+//      form, its table in LDS) in index order: chunks of 12288 exponentials
+//      go to LDS -- the next chunk's logits are requested before the current
+//      chunk is summed -- and the workgroup adds each chunk exactly as
+//      one-at-a-time fp32 adds would, with the parity-map scan of
+//      nls_seqsum.h.
 //   3. softmax: out[i] = exp(l_i - mx) / s for the whole row (out may be the
 //      logits themselves: each element is read before it is written, by the
 //      same thread); logProb: p = exp(l_t - mx) / s for the row's target t,
@@ -37,6 +38,7 @@ __global__ __launch_bounds__(kSmxNT) void softmax_kernel(const float* logits, in
   __shared__ __align__(16) float ebuf[kSmxChunk];
   __shared__ SeqSumShared sh;
   __shared__ float s_part[NW];
+  __shared__ double s_pow2[kExpfPow2Count];  // the exponential's table
   const int row = (int)blockIdx.x;
   const int tid = (int)threadIdx.x;
   const int lane = lane_id();
@@ -77,6 +79,8 @@ __global__ __launch_bounds__(kSmxNT) void softmax_kernel(const float* logits, in
   {
     float a[kSmxPer], b[kSmxPer];
     load(0, a);
+    // (after the first chunk's requests; the barrier after this pass orders it)
+    if (tid < kExpfPow2Count) s_pow2[tid] = kExpfPow2J64[tid];
     for (int c0 = 0; c0 < n; c0 += kSmxChunk) {
       const bool more = c0 + kSmxChunk < n;
       if (more) load(c0 + kSmxChunk, b);
@@ -107,7 +111,7 @@ __global__ __launch_bounds__(kSmxNT) void softmax_kernel(const float* logits, in
 #pragma unroll
       for (int q = 0; q < kSmxPer; ++q) {
         const int e = elem(c0, q);
-        if (e < n) ebuf[e - c0] = expf_cr(v[q] - mx);
+        if (e < n) ebuf[e - c0] = expf_cr_t(v[q] - mx, s_pow2);
       }
       __syncthreads();
       if (c0 + kSmxChunk < n) load(c0 + kSmxChunk, v);
@@ -120,7 +124,7 @@ __global__ __launch_bounds__(kSmxNT) void softmax_kernel(const float* logits, in
     if (tid == 0) {
       const int t = targets[row];
       float p = __builtin_nanf("");
-      if (t >= 0 && t < n) p = expf_cr(x[t] - mx) / s;
+      if (t >= 0 && t < n) p = expf_cr_t(x[t] - mx, s_pow2) / s;
       prob[row] = p;
       logp[row] = log((double)p);
     }
@@ -139,10 +143,10 @@ __global__ __launch_bounds__(kSmxNT) void softmax_kernel(const float* logits, in
           const int e0 = c0 + 4 * (tid + g * NT);
           if (e0 < n) {
             f32x4 r;
-            r.x = expf_cr(a[4 * g] - mx) / s;
-            r.y = expf_cr(a[4 * g + 1] - mx) / s;
-            r.z = expf_cr(a[4 * g + 2] - mx) / s;
-            r.w = expf_cr(a[4 * g + 3] - mx) / s;
+            r.x = expf_cr_t(a[4 * g] - mx, s_pow2) / s;
+            r.y = expf_cr_t(a[4 * g + 1] - mx, s_pow2) / s;
+            r.z = expf_cr_t(a[4 * g + 2] - mx, s_pow2) / s;
+            r.w = expf_cr_t(a[4 * g + 3] - mx, s_pow2) / s;
             *reinterpret_cast<f32x4*>(o + e0) = r;
           }
         }
@@ -150,7 +154,7 @@ __global__ __launch_bounds__(kSmxNT) void softmax_kernel(const float* logits, in
 #pragma unroll
         for (int q = 0; q < kSmxPer; ++q) {
           const int e = elem(c0, q);
-          if (e < n) o[e] = expf_cr(a[q] - mx) / s;
+          if (e < n) o[e] = expf_cr_t(a[q] - mx, s_pow2) / s;
         }
       }
       if (more) {

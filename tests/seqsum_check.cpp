@@ -29,9 +29,16 @@ static float plain_sum(const std::vector<float>& e, float s) {
 static long g_windows = 0;
 static long g_terms = 0;  // terms composed, over all windows
 
-static float block_sum_chunk(const float* e, int len, float s, int& J, int done) {
+static float block_sum_chunk(const float* e, int len, float s, int& J, int done, int serial) {
   const int NT = 1024, W = 64, NW = NT / W;
   int pos = 0;
+  if (done == 0 && serial > 0 && len > 0) {
+    // the first terms one at a time (kSeqSerial on the device)
+    const int n0 = std::min(len, serial);
+    for (int i = 0; i < n0; ++i) s = s + e[i];
+    pos = n0;
+    J = seq_next_j(n0);
+  }
   while (pos < len) {
     ++g_windows;
     if (!(s <= 3.4028234663852886e38f)) {
@@ -147,30 +154,38 @@ static float block_sum_chunk(const float* e, int len, float s, int& J, int done)
 }
 
 // the sum over chunks of 12288 terms, the window width carried across them,
-// as the softmax kernels call it
-static float block_sum(const std::vector<float>& e, float s) {
+// as the softmax kernels call it; `serial` first terms added one at a time
+// (the device adds kSeqSerial; 0 runs every term through the windows)
+static float block_sum(const std::vector<float>& e, float s, int serial) {
   const int CH = 12288;
   int J = 1;
   for (size_t c0 = 0; c0 < e.size(); c0 += CH)
-    s = block_sum_chunk(e.data() + c0, (int)std::min<size_t>(CH, e.size() - c0), s, J, (int)c0);
+    s = block_sum_chunk(e.data() + c0, (int)std::min<size_t>(CH, e.size() - c0), s, J, (int)c0, serial);
   return s;
 }
 
 static int g_fail = 0;
 
-static void check(const char* name, const std::vector<float>& e, float s0 = 0.0f) {
+static void check_one(const char* name, const std::vector<float>& e, float s0, int serial) {
   const long w0 = g_windows, t0 = g_terms;
-  const float a = plain_sum(e, s0), b = block_sum(e, s0);
+  const float a = plain_sum(e, s0), b = block_sum(e, s0, serial);
   uint32_t ba, bb;
   memcpy(&ba, &a, 4);
   memcpy(&bb, &b, 4);
   const bool ok = ba == bb || (a != a && b != b);
-  printf("%-44s n=%7zu sum=%-14.8g %s (windows %ld, terms composed %.2f n)\n", name, e.size(), (double)a,
-         ok ? "ok" : "MISMATCH", g_windows - w0, (double)(g_terms - t0) / std::max<size_t>(e.size(), 1));
+  printf("%-44s n=%7zu serial=%4d sum=%-14.8g %s (windows %ld, terms composed %.2f n)\n", name, e.size(), serial,
+         (double)a, ok ? "ok" : "MISMATCH", g_windows - w0,
+         (double)(g_terms - t0) / std::max<size_t>(e.size(), 1));
   if (!ok) {
     printf("   plain %a  block %a\n", (double)a, (double)b);
     g_fail = 1;
   }
+}
+
+// every case with all terms through the windows, and as the device runs it
+static void check(const char* name, const std::vector<float>& e, float s0 = 0.0f) {
+  check_one(name, e, s0, 0);
+  check_one(name, e, s0, kSeqSerial);
 }
 
 int main() {
