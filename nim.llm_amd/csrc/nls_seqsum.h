@@ -169,6 +169,7 @@ struct SeqSumShared {
   SeqMap wtot[2][16];  // per window parity, per wave: the map of its terms
   int stop[2];         // the window's term that leaves the binade (kSeqNoStop: none)
   float s[2];          // the sum after that term
+  float s_plain;       // the sum finished with plain adds (NaN or +inf)
 };
 
 // Call once (by every thread) before the first seq_sum_block on `sh`, followed
@@ -208,22 +209,33 @@ __device__ __forceinline__ SeqMap sm_row_scan(SeqMap m) {
   return m;
 }
 
+// Inclusive integer scan over lanes 0..15 (one row).
+__device__ __forceinline__ int seq_row_scan_int(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);  // row_shr:8
+  return x;
+}
+
 __device__ __forceinline__ SeqMap sm_readlane(SeqMap m, int l) {
   return SeqMap{__builtin_amdgcn_readlane(m.a, l), __builtin_amdgcn_readlane(m.c, l)};
 }
 
-// The map of this thread's JB-term run at b (terms at or past `end` count as
-// zeros), with every term read before any is used.  Ties are rare (a term
-// whose bits below u are exactly 100...0), so the run is first summed as if
-// it held none -- the increments are then e/u rounded to nearest -- and a
-// wave where some lane met a tie or a term too large redoes its runs with
-// the parity bookkeeping.
+// This thread's JB-term run at b (terms at or past `end` count as zeros),
+// with every term read before any is used.  Ties are rare (a term whose bits
+// below u are exactly 100...0), so the run is first summed as if it held
+// none -- the increments are then e/u rounded to nearest and do not depend
+// on S -- into A (clamped at 2^24: any run that large leaves the binade).
+// When some lane of the wave met a tie or a term too large, `wodd` is set
+// and m is the run's parity map, with the bookkeeping redone.
 template <int JB>
-__device__ __forceinline__ SeqMap seq_thread_map(const float* e, int b, int end, int len, int E) {
+__device__ __forceinline__ void seq_thread_run(const float* e, int b, int end, int len, int E, int& A,
+                                               bool& wodd, SeqMap& m) {
   float v[JB];
 #pragma unroll
   for (int j = 0; j < JB; ++j) v[j] = b + j < end ? e[min(b + j, len - 1)] : 0.0f;
-  int A = 0;
+  int a = 0;
   bool odd = false;
 #pragma unroll
   for (int j = 0; j < JB; ++j) {
@@ -231,14 +243,22 @@ __device__ __forceinline__ SeqMap seq_thread_map(const float* e, int b, int end,
     const bool ok = q < 16777216.0f;
     const float qc = ok ? q : 0.0f;
     const float fr = seq_fract(qc);
-    A += (int)qc + (fr > 0.5f ? 1 : 0);
+    a += (int)qc + (fr > 0.5f ? 1 : 0);
     odd = odd || !ok || fr == 0.5f;
   }
-  if (__ballot(odd) == 0ull) return sm_make(A, A & 1, A, (A + 1) & 1);  // wave-uniform
-  SeqRun run;
+  A = min(a, 1 << 24);
+  wodd = __ballot(odd) != 0ull;  // wave-uniform
+  if (wodd) {
+    SeqRun run;
 #pragma unroll
-  for (int j = 0; j < JB; ++j) run.add(v[j], E);
-  return run.map();
+    for (int j = 0; j < JB; ++j) run.add(v[j], E);
+    m = run.map();
+  }
+}
+
+// A map that adds the same amount for either parity (a run without ties).
+__device__ __forceinline__ bool sm_is_plain(SeqMap m) {
+  return (m.a >> 1) == (m.c >> 1) && ((m.a ^ m.c) & 1) != 0;
 }
 
 // s + e[0] + ... + e[len - 1], added one at a time in fp32 as above.  Every
@@ -251,7 +271,9 @@ __device__ __forceinline__ SeqMap seq_thread_map(const float* e, int b, int end,
 // chunks of a row (start them at 1 and 0, after seq_sum_init and a barrier);
 // `done` is the number of terms summed before e[0]; a call with done == 0 and
 // w == 0 (the first of a row) adds the first kSeqSerial terms on one lane
-// first.  Two barriers per window; the call ends with one.
+// first.  A window scans integer increments in waves without ties (the
+// general parity maps in the others) and takes one barrier, or two when a
+// term of it leaves the binade; the call ends with a barrier.
 template <int NT>
 __device__ float seq_sum_block(const float* e, int len, float s, int& J, int& w, int done,
                                SeqSumShared& sh) {
@@ -288,10 +310,10 @@ __device__ float seq_sum_block(const float* e, int len, float s, int& J, int& w,
       // NaN or +inf: plain adds
       if (tid == 0) {
         for (int i = pos; i < len; ++i) s = s + e[i];
-        sh.s[0] = s;
+        sh.s_plain = s;
       }
       __syncthreads();
-      s = sh.s[0];
+      s = sh.s_plain;
       __syncthreads();
       return s;
     }
@@ -301,34 +323,68 @@ __device__ float seq_sum_block(const float* e, int len, float s, int& J, int& w,
     const int jn = min(J, (len - pos + NT - 1) / NT);
     const int b = pos + tid * jn;
     const int end = min(b + jn, len);
-    SeqMap m;
+    int A = 0;
+    bool wodd = false;
+    SeqMap m = sm_identity();
     if (jn <= 1)
-      m = seq_thread_map<1>(e, b, end, len, E);
+      seq_thread_run<1>(e, b, end, len, E, A, wodd, m);
     else if (jn <= 2)
-      m = seq_thread_map<2>(e, b, end, len, E);
+      seq_thread_run<2>(e, b, end, len, E, A, wodd, m);
     else if (jn <= 4)
-      m = seq_thread_map<4>(e, b, end, len, E);
+      seq_thread_run<4>(e, b, end, len, E, A, wodd, m);
     else if (jn <= 8)
-      m = seq_thread_map<8>(e, b, end, len, E);
+      seq_thread_run<8>(e, b, end, len, E, A, wodd, m);
     else if (jn <= 12)
-      m = seq_thread_map<12>(e, b, end, len, E);
+      seq_thread_run<12>(e, b, end, len, E, A, wodd, m);
     else
-      m = seq_thread_map<16>(e, b, end, len, E);
-    const SeqMap inc = sm_wave_scan(m);
-    if (lane == kWave - 1) sh.wtot[bw][wv] = inc;
+      seq_thread_run<16>(e, b, end, len, E, A, wodd, m);
+    // in-wave inclusive scan: integers (<= 2^30) without ties, else maps
+    int incA = 0;
+    SeqMap incM = sm_identity();
+    if (!wodd)
+      incA = wave_incl_scan(A);
+    else
+      incM = sm_wave_scan(m);
+    if (lane == kWave - 1) sh.wtot[bw][wv] = wodd ? incM : sm_make(incA, incA & 1, incA, (incA + 1) & 1);
     __syncthreads();
     // (the other buffer's readers finished before the barrier above)
     if (tid == 0) sh.stop[bw ^ 1] = kSeqNoStop;
-    // the waves' maps, scanned by every wave's first row of lanes
+    // the waves' maps, scanned by every wave's first row of lanes: integers
+    // when no wave met a tie (increments saturate at 2^26: the sum stays
+    // below 2^31), else maps
     SeqMap wt = lane < NW ? sh.wtot[bw][lane] : sm_identity();
-    wt = sm_row_scan(wt);
-    SeqMap pre = wv > 0 ? sm_readlane(wt, wv - 1) : sm_identity();
-    pre = sm_then(pre, sm_dpp<0x138, 0xf>(inc));  // wave_shr:1 -- lanes below, in this wave
+    const bool plain = __ballot(!sm_is_plain(wt)) == 0ull;  // uniform over the workgroup
+    SeqMap pre;  // the waves below this one
+    int Send;    // S after the window's last term (at least 2^24 when one leaves the binade)
+    if (plain) {
+      const int d = seq_row_scan_int(lane < NW ? (wt.a >> 1) : 0);
+      const int p = wv > 0 ? __builtin_amdgcn_readlane(d, wv - 1) : 0;
+      pre = sm_make(p, p & 1, p, (p + 1) & 1);
+      Send = S0 + __builtin_amdgcn_readlane(d, NW - 1);
+    } else {
+      wt = sm_row_scan(wt);
+      pre = wv > 0 ? sm_readlane(wt, wv - 1) : sm_identity();
+      Send = S0 + sm_inc(sm_readlane(wt, NW - 1), S0);
+    }
+    ++w;
+    if (Send < (1 << 24)) {
+      // no term of the window leaves the binade (uniform)
+      s = seq_ldexp((float)Send, E - 23);
+      pos = min(pos + NT * jn, len);
+      J = min(J * 2, kSeqMaxJ);
+      continue;
+    }
     // this thread's incoming and outgoing S; the one thread where S reaches
     // 2^24 (or meets a term that leaves the binade by itself) has its terms
     // replayed by the first row of its wave, one term per lane
-    const int Sin = S0 + sm_inc(pre, S0);
-    const int Sout = Sin < (1 << 24) ? Sin + sm_inc(m, Sin) : Sin;
+    int Sin, Sout;
+    if (!wodd) {
+      Sin = S0 + sm_inc(pre, S0) + (incA - A);
+      Sout = Sin + A;
+    } else {
+      Sin = S0 + sm_inc(sm_then(pre, sm_dpp<0x138, 0xf>(incM)), S0);  // wave_shr:1 -- lanes below
+      Sout = Sin < (1 << 24) ? Sin + sm_inc(m, Sin) : Sin;
+    }
     const uint64_t cross = __ballot(Sin < (1 << 24) && Sout >= (1 << 24));
     if (cross) {  // wave-uniform
       const int L = __ffsll((unsigned long long)cross) - 1;
@@ -350,13 +406,10 @@ __device__ float seq_sum_block(const float* e, int len, float s, int& J, int& w,
     }
     __syncthreads();
     const int k = sh.stop[bw];
-    ++w;
     if (k == kSeqNoStop) {
-      // no term of the window leaves the binade
-      const SeqMap tot = sm_readlane(wt, NW - 1);
-      s = seq_ldexp((float)(S0 + sm_inc(tot, S0)), E - 23);
+      // (not reached: a window whose sum reaches 2^24 has a thread where it does)
+      s = seq_ldexp((float)Send, E - 23);
       pos = min(pos + NT * jn, len);
-      J = min(J * 2, kSeqMaxJ);
     } else {
       s = sh.s[bw];
       J = seq_next_j(done + k);

@@ -3,9 +3,11 @@
 //
 // The device routine seq_sum_block runs the parity-map scan over a workgroup
 // of 1024 threads; this program runs the same steps (the same per-term codes,
-// packed maps, window sizes, the zero codes past a thread's terms, replays
-// and binade changes; the scans run Hillis-Steele over each wave and over the
-// waves' totals, a grouping of the same associative composition) with the threads as loops,
+// clamped integer increments of waves without ties and packed maps of the
+// others, window sizes, the zero codes past a thread's terms, the integer
+// scan of plain wave totals, replays and binade changes; the scans run
+// Hillis-Steele over each wave and over the waves' totals, a grouping of the
+// same associative composition) with the threads as loops,
 // on term arrays chosen to break a wrong rounding rule: softmax exponentials
 // of many spreads, exact ties at every scale, subnormals and zeros, a dynamic
 // range of 2^160, runs that park the sum at 2^24, and NaN / +inf terms.
@@ -49,15 +51,17 @@ static float block_sum_chunk(const float* e, int len, float s, int& J, int done,
     const int S0 = (int)seq_ldexp(s, 23 - E);
     const int jn = std::min(J, (len - pos + NT - 1) / NT);
     g_terms += std::min(NT * jn, len - pos);
-    std::vector<SeqMap> m(NT), inc(NT);
+    std::vector<SeqMap> m(NT, sm_identity()), inc(NT, sm_identity());
+    std::vector<int> A(NT), incA(NT);
     std::vector<bool> wodd(NW, false);
     for (int t = 0; t < NT; ++t) {
       const int b = pos + t * jn, end = std::min(b + jn, len);
       // the device's template width: 1, 2, 4, 8, 12 or 16 terms; the run
-      // summed as if tie-free, with the parity bookkeeping redone for every
-      // lane of a wave where one lane met a tie or a term too large
+      // summed as if tie-free (clamped at 2^24), with the parity maps
+      // formed for every lane of a wave where one lane met a tie or a term
+      // too large
       const int jb = jn <= 1 ? 1 : jn <= 2 ? 2 : jn <= 4 ? 4 : jn <= 8 ? 8 : jn <= 12 ? 12 : 16;
-      int A = 0;
+      int a = 0;
       bool odd = false;
       for (int j = 0; j < jb; ++j) {
         const float v = b + j < end ? e[std::min(b + j, len - 1)] : 0.0f;
@@ -65,10 +69,10 @@ static float block_sum_chunk(const float* e, int len, float s, int& J, int done,
         const bool ok = q < 16777216.0f;
         const float qc = ok ? q : 0.0f;
         const float fr = seq_fract(qc);
-        A += (int)qc + (fr > 0.5f ? 1 : 0);
+        a += (int)qc + (fr > 0.5f ? 1 : 0);
         odd = odd || !ok || fr == 0.5f;
       }
-      m[t] = sm_make(A, A & 1, A, (A + 1) & 1);
+      A[t] = std::min(a, 1 << 24);
       wodd[t / W] = wodd[t / W] || odd;
     }
     for (int t = 0; t < NT; ++t) {
@@ -79,31 +83,74 @@ static float block_sum_chunk(const float* e, int len, float s, int& J, int done,
       for (int j = 0; j < jb; ++j) run.add(b + j < end ? e[std::min(b + j, len - 1)] : 0.0f, E);
       m[t] = run.map();
     }
-    // wave-level inclusive scans (Hillis-Steele, as the shuffles do)
+    // wave-level inclusive scans (Hillis-Steele, as the shuffles do): maps in
+    // waves with a tie, integers in the others
     inc = m;
+    incA = A;
     for (int o = 1; o < W; o <<= 1) {
       std::vector<SeqMap> nx = inc;
+      std::vector<int> nxA = incA;
       for (int t = 0; t < NT; ++t)
-        if (t % W >= o) nx[t] = sm_then(inc[t - o], inc[t]);
+        if (t % W >= o) {
+          nx[t] = sm_then(inc[t - o], inc[t]);
+          nxA[t] = incA[t - o] + incA[t];
+        }
       inc = nx;
+      incA = nxA;
     }
-    // the waves' maps, scanned the same way over NW lanes
+    // the waves' maps; scanned as integers when every one is plain
     std::vector<SeqMap> wt(NW);
-    for (int w = 0; w < NW; ++w) wt[w] = inc[w * W + W - 1];
-    for (int o = 1; o < NW; o <<= 1) {
-      std::vector<SeqMap> nx = wt;
-      for (int l = o; l < NW; ++l) nx[l] = sm_then(wt[l - o], wt[l]);
-      wt = nx;
+    bool plain = true;
+    for (int w = 0; w < NW; ++w) {
+      const int l = w * W + W - 1;
+      wt[w] = wodd[w] ? inc[l] : sm_make(incA[l], incA[l] & 1, incA[l], (incA[l] + 1) & 1);
+      const bool pl = (wt[w].a >> 1) == (wt[w].c >> 1) && ((wt[w].a ^ wt[w].c) & 1) != 0;
+      if (wodd[w] && pl) {
+        printf("   a wave with a tie has a plain map\n");
+        return NAN;
+      }
+      plain = plain && pl;
+    }
+    std::vector<SeqMap> wpre(NW, sm_identity());
+    int Send;
+    if (plain) {
+      int d = 0;
+      for (int w = 0; w < NW; ++w) {
+        wpre[w] = sm_make(d, d & 1, d, (d + 1) & 1);
+        d += wt[w].a >> 1;
+      }
+      Send = S0 + d;
+    } else {
+      for (int o = 1; o < NW; o <<= 1) {
+        std::vector<SeqMap> nx = wt;
+        for (int l = o; l < NW; ++l) nx[l] = sm_then(wt[l - o], wt[l]);
+        wt = nx;
+      }
+      for (int w = 1; w < NW; ++w) wpre[w] = wt[w - 1];
+      Send = S0 + sm_inc(wt[NW - 1], S0);
+    }
+    if (Send < (1 << 24)) {
+      // no term of the window leaves the binade
+      s = seq_ldexp((float)Send, E - 23);
+      pos = std::min(pos + NT * jn, len);
+      J = std::min(J * 2, kSeqMaxJ);
+      continue;
     }
     int kstop = -1;
     float sstop = 0.0f;
     int replays = 0;
     for (int t = 0; t < NT; ++t) {
       const int wv = t / W, lane = t % W;
-      SeqMap pre = wv > 0 ? wt[wv - 1] : sm_identity();
-      if (lane > 0) pre = sm_then(pre, inc[t - 1]);
-      const int Sin = S0 + sm_inc(pre, S0);
-      const int Sout = Sin < (1 << 24) ? Sin + sm_inc(m[t], Sin) : Sin;
+      int Sin, Sout;
+      if (!wodd[wv]) {
+        Sin = S0 + sm_inc(wpre[wv], S0) + (incA[t] - A[t]);
+        Sout = Sin + A[t];
+      } else {
+        SeqMap pre = wpre[wv];
+        if (lane > 0) pre = sm_then(pre, inc[t - 1]);
+        Sin = S0 + sm_inc(pre, S0);
+        Sout = Sin < (1 << 24) ? Sin + sm_inc(m[t], Sin) : Sin;
+      }
       if (Sin < (1 << 24) && Sout >= (1 << 24)) {
         // the replay: one term per lane of a row, their maps scanned in order
         ++replays;
@@ -139,16 +186,12 @@ static float block_sum_chunk(const float* e, int len, float s, int& J, int done,
       return NAN;
     }
     if (kstop < 0) {
-      const SeqMap tot = wt[NW - 1];
-      const int S1 = S0 + sm_inc(tot, S0);
-      s = seq_ldexp((float)S1, E - 23);
-      pos = std::min(pos + NT * jn, len);
-      J = std::min(J * 2, kSeqMaxJ);
-    } else {
-      s = sstop;
-      J = seq_next_j(done + kstop);
-      pos = kstop + 1;
+      printf("   a window reached 2^24 without a thread where it does\n");
+      return NAN;
     }
+    s = sstop;
+    J = seq_next_j(done + kstop);
+    pos = kstop + 1;
   }
   return s;
 }
