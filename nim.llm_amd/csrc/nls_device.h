@@ -2313,64 +2313,87 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     }
     return m;
   };
-  // The row is counted in rounds of 4 * NW blocks, in index order, and the
-  // walk stops at the round holding the t-th member (on average half the row
-  // is read).  The patched members go in first.
+  // The row is counted in rounds of 4 * NW blocks and the walk stops at the
+  // round holding the t-th member: in index order when t lies in the lower
+  // half of the group's c members, else from the row's end for the
+  // (c - 1 - t)-th member from the top (on average a quarter of the row is
+  // read).  The patched members go in first.
+  const int64_t cg = (int64_t)(uint32_t)L.gsort[s_g];
+  const bool rev = 2 * t >= cg;  // uniform
   for (int i = tid; i < nblk; i += NT) bcnt[i] = 0u;
   __syncthreads();
   for (int sl = tid; sl < np; sl += NT)
     if (L.pfin[sl] == vg) atomicAdd(&bcnt[L.pid[sl] / (kWave * W)], 1u);
   if (tid == 0) {
-    s_left = t;
+    s_left = rev ? cg - 1 - t : t;
     s_found = 0;
   }
   __syncthreads();
-  constexpr int RB = 4 * NW;
-  for (int r0 = 0; r0 < nblk; r0 += RB) {
-    int m[4];
+  // (one instance per direction: the index order's loop stays as plain as
+  // when it was the only one)
+  auto search = [&](auto rev_c) __attribute__((always_inline)) {
+    constexpr bool REV = decltype(rev_c)::value;
+    auto phys = [&](int lb) { return REV ? nblk - 1 - lb : lb; };  // logical block -> block
+    constexpr int RB = 4 * NW;
+    for (int r0 = 0; r0 < nblk; r0 += RB) {
+      int m[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int bk = r0 + wv + u * NW;
-      m[u] = bk < nblk ? lane_count(bk) : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int bk = r0 + wv + u * NW;
-      const int c = wave_sum_i(m[u]);
-      if (lane == 0 && bk < nblk) bcnt[bk] += (uint32_t)c;
-    }
-    __syncthreads();
-    if (wv == 0) {
-      int64_t left = s_left;
-      const int rend = min(r0 + RB, nblk);
-      for (int base = r0; base < rend; base += kWave) {
-        const int c = (base + lane < rend) ? (int)bcnt[base + lane] : 0;
-        const int incl = wave_incl_scan(c);
-        const int sum = __shfl(incl, kWave - 1, kWave);
-        if (left < sum) {
-          // the block: the first lane whose inclusive count passes `left`
-          const uint64_t past = __ballot((int64_t)incl > left);
-          const int bl = __ffsll((unsigned long long)past) - 1;
-          const int bk = base + bl;
-          const int64_t within = left - (__shfl(incl, bl, kWave) - __shfl(c, bl, kWave));
-          const uint32_t mb = lane_members(bk);
-          const int mc = __popc(mb);
-          const int mi = wave_incl_scan(mc);
-          if ((int64_t)(mi - mc) <= within && within < (int64_t)mi) {
-            uint32_t mm = mb;
-            for (int r = (int)(within - (mi - mc)); r > 0; --r) mm &= mm - 1u;
-            s_id = (bk * kWave + lane) * W + (__ffs(mm) - 1);
-          }
-          if (lane == 0) s_found = 1;
-          break;
-        }
-        left -= sum;
+      for (int u = 0; u < 4; ++u) {
+        const int lb = r0 + wv + u * NW;
+        m[u] = lb < nblk ? lane_count(phys(lb)) : 0;
       }
-      if (lane == 0) s_left = left;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int lb = r0 + wv + u * NW;
+        const int c = wave_sum_i(m[u]);
+        if (lane == 0 && lb < nblk) bcnt[phys(lb)] += (uint32_t)c;
+      }
+      __syncthreads();
+      if (wv == 0) {
+        int64_t left = s_left;
+        const int rend = min(r0 + RB, nblk);
+        for (int base = r0; base < rend; base += kWave) {
+          const int c = (base + lane < rend) ? (int)bcnt[phys(base + lane)] : 0;
+          const int incl = wave_incl_scan(c);
+          const int sum = __shfl(incl, kWave - 1, kWave);
+          if (left < sum) {
+            // the block: the first lane whose inclusive count passes `left`
+            const uint64_t past = __ballot((int64_t)incl > left);
+            const int bl = __ffsll((unsigned long long)past) - 1;
+            const int bk = phys(base + bl);
+            const int64_t within = left - (__shfl(incl, bl, kWave) - __shfl(c, bl, kWave));
+            const uint32_t mb = lane_members(bk);
+            const int mc = __popc(mb);
+            const int mi = wave_incl_scan(mc);
+            // members before this lane's, in the walk's order
+            const int64_t before = REV ? (int64_t)(__shfl(mi, kWave - 1, kWave) - mi) : (int64_t)(mi - mc);
+            if (before <= within && within < before + mc) {
+              uint32_t mm = mb;
+              int e;
+              if (REV) {
+                for (int r = (int)(within - before); r > 0; --r) mm &= ~(1u << (31 - __clz(mm)));
+                e = 31 - __clz(mm);
+              } else {
+                for (int r = (int)(within - before); r > 0; --r) mm &= mm - 1u;
+                e = __ffs(mm) - 1;
+              }
+              s_id = (bk * kWave + lane) * W + e;
+            }
+            if (lane == 0) s_found = 1;
+            break;
+          }
+          left -= sum;
+        }
+        if (lane == 0) s_left = left;
+      }
+      __syncthreads();
+      if (s_found) break;
     }
-    __syncthreads();
-    if (s_found) break;
-  }
+  };
+  if (rev)
+    search(std::true_type{});
+  else
+    search(std::false_type{});
   NLS_GSTAMP(row, 7);
   if (s_id < 0) return res;
   res.ok = 1;

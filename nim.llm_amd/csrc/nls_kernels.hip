@@ -196,7 +196,7 @@ __global__ __launch_bounds__(NT) void top_tokens_kernel(const float* __restrict_
   auto pkey = [&](float l) -> uint32_t { return f2key(prob_of(l)); };
 
   uint64_t* mem = reinterpret_cast<uint64_t*>(ebuf);
-  constexpr int kCand = (int)(sizeof(ebuf) / sizeof(uint64_t));
+  constexpr int kCand = (int)(sizeof(ebuf) / (sizeof(uint64_t)));
   auto emit = [&](int cnt) {  // mem[0..cnt): key << 32 | ~index; the first m, sorted, out
     const int np = next_pow2(cnt);
     for (int i = cnt + tid; i < np; i += NT) mem[i] = 0ull;  // below every real key
