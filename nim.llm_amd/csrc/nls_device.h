@@ -1868,9 +1868,16 @@ struct GroupLds {
   float* pfin;       //   their final values
   uint32_t* hkey;    // [kGrpHashCap] f2key of a distinct value (kGrpEmpty: free)
   uint32_t* hcnt;    //   its multiplicity
-  uint64_t* gsort;   // [kGrpHashCap] (~f2key(value) << 32) | multiplicity, ascending
+  uint64_t* gsort;   // [kGrpHashCap] (~f2key(value) << 32) | multiplicity (or kGrpOne | index), ascending
 };
 constexpr uint32_t kGrpEmpty = 0xffffffffu;  // f2key of a NaN, which never enters
+// A group's multiplicity in the low word of its sort record; a value that
+// occurs once carries its element's index instead (V < 2^31), flagged.
+constexpr uint32_t kGrpOne = 0x80000000u;
+__device__ __forceinline__ uint32_t group_count(uint64_t rec) {
+  const uint32_t lo = (uint32_t)rec;
+  return (lo & kGrpOne) ? 1u : lo;
+}
 
 __device__ __forceinline__ GroupLds group_lds(unsigned char* base, int nw) {
   GroupLds L;
@@ -1885,9 +1892,18 @@ __device__ __forceinline__ GroupLds group_lds(unsigned char* base, int nw) {
   L.gsort = reinterpret_cast<uint64_t*>(L.hcnt + kGrpHashCap);  // byte offset 8*nw + 16*caps
   return L;
 }
+// Per hash slot: the index of the occurrence that inserted it (the sort
+// array's first half, until the groups are collected; addressed from the
+// count array, which it follows, so no other base stays live).
+__device__ __forceinline__ int32_t* group_first(const GroupLds& L) {
+  return reinterpret_cast<int32_t*>(L.hcnt + kGrpHashCap);
+}
 
-// Count one more occurrence of key; false when the table is full.
-__device__ __forceinline__ bool group_insert(const GroupLds& L, uint32_t key, int* distinct) {
+// Count one more occurrence of key, the element at index `idx`; false when
+// the table is full.  The inserting occurrence's index is kept per slot (in
+// the sort array, unused until the groups are collected): for a value that
+// occurs once it is the value's only member.
+__device__ __forceinline__ bool group_insert(const GroupLds& L, uint32_t key, int* distinct, int idx) {
   uint32_t h = (key * 0x9E3779B1u) >> (32 - kGrpHashBits);
   for (int probe = 0; probe < kGrpHashCap; ++probe) {
     uint32_t cur = L.hkey[h];
@@ -1895,6 +1911,7 @@ __device__ __forceinline__ bool group_insert(const GroupLds& L, uint32_t key, in
       cur = atomicCAS(&L.hkey[h], kGrpEmpty, key);
       if (cur == kGrpEmpty) {
         cur = key;
+        group_first(L)[h] = idx;
         if (atomicAdd(distinct, 1) >= kGrpHashLimit) return false;
       }
     }
@@ -2042,7 +2059,7 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   // slot is counted with one atomic add, and only the others (first
   // occurrences, collisions) probe.
   bool bad = false;
-  auto count8 = [&](const float* vv, uint32_t want) __attribute__((always_inline)) {
+  auto count8 = [&](const float* vv, uint32_t want, auto&& ix) __attribute__((always_inline)) {
     uint32_t hs[8], cur[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) hs[q] = (f2key(vv[q]) * 0x9E3779B1u) >> (32 - kGrpHashBits);
@@ -2055,18 +2072,26 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
       if (cur[q] == key)
         atomicAdd(&L.hcnt[hs[q]], 1u);
       else
-        bad |= !group_insert(L, key, &s_distinct);
+        bad |= !group_insert(L, key, &s_distinct, ix(q));
     }
   };
-  auto count16 = [&](const float (&vv)[16], uint32_t want) __attribute__((always_inline)) {
-    count8(vv, want & 0xffu);
-    count8(vv + 8, want >> 8);
+  // (ix(q): the row index of vv[q])
+  auto count16 = [&](const float (&vv)[16], uint32_t want, auto&& ix) __attribute__((always_inline)) {
+    count8(vv, want & 0xffu, ix);
+    count8(vv + 8, want >> 8, [&](int q) { return ix(q + 8); });
   };
-  // the row's final values 16 per thread at a time: fn(vv, in) with in's bit
-  // q set where vv[q] is an unpatched value of the row.  The loops run the
-  // same number of times on every lane of a wave (fn reduces over the wave)
-  // and stop when a lane has filled the table.
-  const int wbase = tid - lane;
+  // the row's final values 16 per thread at a time: fn(vv, in, ix) with in's
+  // bit q set where vv[q] is an unpatched value of the row, whose index is
+  // ix(q).  The loops run the same number of times on every lane of a wave
+  // (fn reduces over the wave) and stop when a lane has filled the table.
+  const int wbase = __builtin_amdgcn_readfirstlane(tid - lane);  // (uniform over the wave)
+  // the lane's index, computed where it is used (the compiler cannot move it
+  // earlier and keep it in a register)
+  auto lane_here = []() __attribute__((always_inline)) {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+  };
   auto for_each16 = [&](auto&& fn) __attribute__((always_inline)) {
     if (vec) {
       for (int w4 = wbase; w4 < V4; w4 += 4 * NT) {
@@ -2086,7 +2111,9 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
           vv[4 * u + 3] = x[u].w * invT;
           in |= ((~pb) & 15u) << (4 * u);
         }
-        fn(vv, in);
+        // (the index is formed where a value is inserted, from the wave's
+        // scalar base and the lane read there: nothing is held for it)
+        fn(vv, in, [&](int q) { return 4 * (w4 + lane_here() + (q >> 2) * NT) + (q & 3); });
         if (__ballot(bad)) break;
       }
     } else {
@@ -2100,7 +2127,7 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
           vv[q] = i < V ? src[i] * invT : 0.0f;
           if (i < V && !((L.bitmap[i >> 5] >> (i & 31)) & 1u)) in |= 1u << q;
         }
-        fn(vv, in);
+        fn(vv, in, [&](int q) { return w0 + lane_here() + q * NT; });
         if (__ballot(bad)) break;
       }
     }
@@ -2118,7 +2145,7 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   if (rmx > -__builtin_inff()) atomicMax(&s_rkey, f2key(rmx));
   __syncthreads();
   rmx = key2f(s_rkey);
-  for_each16([&](const float (&vv)[16], uint32_t in) {
+  for_each16([&](const float (&vv)[16], uint32_t in, auto&& ix) {
 #pragma unroll
     for (int q = 0; q < 16; ++q)
       if ((in >> q) & 1u) {
@@ -2133,11 +2160,11 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
 #pragma unroll
     for (int q = 0; q < 16; ++q)
       if (((in >> q) & 1u) && vv[q] - rmx >= kGroupFloor) want |= 1u << q;
-    count16(vv, want);
+    count16(vv, want, ix);
   });
   for (int sl = tid; sl < np && !bad; sl += NT) {
     const float v = L.pfin[sl];
-    if (v - rmx >= kGroupFloor) bad |= !group_insert(L, f2key(v), &s_distinct);
+    if (v - rmx >= kGroupFloor) bad |= !group_insert(L, f2key(v), &s_distinct, L.pid[sl]);
   }
   // the row maximum: every thread's running maximum (NaN never taken)
   const uint64_t nb = __ballot(nan);
@@ -2167,22 +2194,27 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     if (tid == 0) s_distinct = 0;
     bad = false;
     __syncthreads();
-    for_each16([&](const float (&vv)[16], uint32_t in) {
+    for_each16([&](const float (&vv)[16], uint32_t in, auto&& ix) {
       uint32_t want = 0u;
 #pragma unroll
       for (int q = 0; q < 16; ++q)
         if (((in >> q) & 1u) && vv[q] - mx >= kGroupFloor) want |= 1u << q;
-      count16(vv, want);
+      count16(vv, want, ix);
     });
     for (int sl = tid; sl < np && !bad; sl += NT) {
       const float v = L.pfin[sl];
-      if (v - mx >= kGroupFloor) bad |= !group_insert(L, f2key(v), &s_distinct);
+      if (v - mx >= kGroupFloor) bad |= !group_insert(L, f2key(v), &s_distinct, L.pid[sl]);
     }
     if (bad) s_fail = 1;
   }
   __syncthreads();
   NLS_GSTAMP(row, 3);
   if (s_fail) return res;
+  // a value that occurs once: its index replaces the count (read before any
+  // record is written over the inserting indices)
+  for (int h = tid; h < kGrpHashCap; h += NT)
+    if (L.hcnt[h] == 1u) L.hcnt[h] = kGrpOne | (uint32_t)group_first(L)[h];
+  __syncthreads();
   for (int h = tid; h < kGrpHashCap; h += NT) {
     const uint32_t k = L.hkey[h];
     // (values counted against a running maximum that fall below the floor of
@@ -2205,9 +2237,9 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   for (int g = tid; g < G; g += NT) {
     const uint64_t e = L.gsort[g];
     const float v = key2f(~(uint32_t)(e >> 32));
-    gc[g] = (uint32_t)e;
+    gc[g] = group_count(e);
     ge[g] = expf_cr(v - mx);
-    atomicAdd(&s_held, (unsigned long long)(uint32_t)e);
+    atomicAdd(&s_held, (unsigned long long)group_count(e));
   }
   __syncthreads();
   // wave 0 walks the groups (its lanes look ahead 64 groups at a time)
@@ -2313,87 +2345,95 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     }
     return m;
   };
-  // The row is counted in rounds of 4 * NW blocks and the walk stops at the
-  // round holding the t-th member: in index order when t lies in the lower
-  // half of the group's c members, else from the row's end for the
-  // (c - 1 - t)-th member from the top (on average a quarter of the row is
-  // read).  The patched members go in first.
-  const int64_t cg = (int64_t)(uint32_t)L.gsort[s_g];
-  const bool rev = 2 * t >= cg;  // uniform
-  for (int i = tid; i < nblk; i += NT) bcnt[i] = 0u;
-  __syncthreads();
-  for (int sl = tid; sl < np; sl += NT)
-    if (L.pfin[sl] == vg) atomicAdd(&bcnt[L.pid[sl] / (kWave * W)], 1u);
-  if (tid == 0) {
-    s_left = rev ? cg - 1 - t : t;
-    s_found = 0;
-  }
-  __syncthreads();
-  // (one instance per direction: the index order's loop stays as plain as
-  // when it was the only one)
-  auto search = [&](auto rev_c) __attribute__((always_inline)) {
-    constexpr bool REV = decltype(rev_c)::value;
-    auto phys = [&](int lb) { return REV ? nblk - 1 - lb : lb; };  // logical block -> block
-    constexpr int RB = 4 * NW;
-    for (int r0 = 0; r0 < nblk; r0 += RB) {
-      int m[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int lb = r0 + wv + u * NW;
-        m[u] = lb < nblk ? lane_count(phys(lb)) : 0;
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int lb = r0 + wv + u * NW;
-        const int c = wave_sum_i(m[u]);
-        if (lane == 0 && lb < nblk) bcnt[phys(lb)] += (uint32_t)c;
-      }
-      __syncthreads();
-      if (wv == 0) {
-        int64_t left = s_left;
-        const int rend = min(r0 + RB, nblk);
-        for (int base = r0; base < rend; base += kWave) {
-          const int c = (base + lane < rend) ? (int)bcnt[phys(base + lane)] : 0;
-          const int incl = wave_incl_scan(c);
-          const int sum = __shfl(incl, kWave - 1, kWave);
-          if (left < sum) {
-            // the block: the first lane whose inclusive count passes `left`
-            const uint64_t past = __ballot((int64_t)incl > left);
-            const int bl = __ffsll((unsigned long long)past) - 1;
-            const int bk = phys(base + bl);
-            const int64_t within = left - (__shfl(incl, bl, kWave) - __shfl(c, bl, kWave));
-            const uint32_t mb = lane_members(bk);
-            const int mc = __popc(mb);
-            const int mi = wave_incl_scan(mc);
-            // members before this lane's, in the walk's order
-            const int64_t before = REV ? (int64_t)(__shfl(mi, kWave - 1, kWave) - mi) : (int64_t)(mi - mc);
-            if (before <= within && within < before + mc) {
-              uint32_t mm = mb;
-              int e;
-              if (REV) {
-                for (int r = (int)(within - before); r > 0; --r) mm &= ~(1u << (31 - __clz(mm)));
-                e = 31 - __clz(mm);
-              } else {
-                for (int r = (int)(within - before); r > 0; --r) mm &= mm - 1u;
-                e = __ffs(mm) - 1;
-              }
-              s_id = (bk * kWave + lane) * W + e;
-            }
-            if (lane == 0) s_found = 1;
-            break;
-          }
-          left -= sum;
-        }
-        if (lane == 0) s_left = left;
-      }
-      __syncthreads();
-      if (s_found) break;
+  // A value that occurs once needs no search.  Otherwise the row is counted
+  // in rounds of 4 * NW blocks and the walk stops at the round holding the
+  // t-th member: in index order when t lies in the lower half of the group's
+  // c members, else from the row's end for the (c - 1 - t)-th member from the
+  // top (on average a quarter of the row is read).  The patched members go
+  // in first.
+  const uint64_t grec = L.gsort[s_g];
+  if ((uint32_t)grec & kGrpOne) {
+    // a value that occurs once: its member was kept when it was counted
+    if (tid == 0) s_id = (int)((uint32_t)grec & ~kGrpOne);
+    __syncthreads();
+  } else {
+    const int64_t cg = (int64_t)group_count(grec);
+    const bool rev = 2 * t >= cg;  // uniform
+    for (int i = tid; i < nblk; i += NT) bcnt[i] = 0u;
+    __syncthreads();
+    for (int sl = tid; sl < np; sl += NT)
+      if (L.pfin[sl] == vg) atomicAdd(&bcnt[L.pid[sl] / (kWave * W)], 1u);
+    if (tid == 0) {
+      s_left = rev ? cg - 1 - t : t;
+      s_found = 0;
     }
-  };
-  if (rev)
-    search(std::true_type{});
-  else
-    search(std::false_type{});
+    __syncthreads();
+    // (one instance per direction: the index order's loop stays as plain as
+    // when it was the only one)
+    auto search = [&](auto rev_c) __attribute__((always_inline)) {
+      constexpr bool REV = decltype(rev_c)::value;
+      auto phys = [&](int lb) { return REV ? nblk - 1 - lb : lb; };  // logical block -> block
+      constexpr int RB = 4 * NW;
+      for (int r0 = 0; r0 < nblk; r0 += RB) {
+        int m[4];
+  #pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int lb = r0 + wv + u * NW;
+          m[u] = lb < nblk ? lane_count(phys(lb)) : 0;
+        }
+  #pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int lb = r0 + wv + u * NW;
+          const int c = wave_sum_i(m[u]);
+          if (lane == 0 && lb < nblk) bcnt[phys(lb)] += (uint32_t)c;
+        }
+        __syncthreads();
+        if (wv == 0) {
+          int64_t left = s_left;
+          const int rend = min(r0 + RB, nblk);
+          for (int base = r0; base < rend; base += kWave) {
+            const int c = (base + lane < rend) ? (int)bcnt[phys(base + lane)] : 0;
+            const int incl = wave_incl_scan(c);
+            const int sum = __shfl(incl, kWave - 1, kWave);
+            if (left < sum) {
+              // the block: the first lane whose inclusive count passes `left`
+              const uint64_t past = __ballot((int64_t)incl > left);
+              const int bl = __ffsll((unsigned long long)past) - 1;
+              const int bk = phys(base + bl);
+              const int64_t within = left - (__shfl(incl, bl, kWave) - __shfl(c, bl, kWave));
+              const uint32_t mb = lane_members(bk);
+              const int mc = __popc(mb);
+              const int mi = wave_incl_scan(mc);
+              // members before this lane's, in the walk's order
+              const int64_t before = REV ? (int64_t)(__shfl(mi, kWave - 1, kWave) - mi) : (int64_t)(mi - mc);
+              if (before <= within && within < before + mc) {
+                uint32_t mm = mb;
+                int e;
+                if (REV) {
+                  for (int r = (int)(within - before); r > 0; --r) mm &= ~(1u << (31 - __clz(mm)));
+                  e = 31 - __clz(mm);
+                } else {
+                  for (int r = (int)(within - before); r > 0; --r) mm &= mm - 1u;
+                  e = __ffs(mm) - 1;
+                }
+                s_id = (bk * kWave + lane) * W + e;
+              }
+              if (lane == 0) s_found = 1;
+              break;
+            }
+            left -= sum;
+          }
+          if (lane == 0) s_left = left;
+        }
+        __syncthreads();
+        if (s_found) break;
+      }
+    };
+    if (rev)
+      search(std::true_type{});
+    else
+      search(std::false_type{});
+  }
   NLS_GSTAMP(row, 7);
   if (s_id < 0) return res;
   res.ok = 1;
