@@ -2075,15 +2075,14 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
         bad |= !group_insert(L, key, &s_distinct, ix(q));
     }
   };
-  // (ix(q): the row index of vv[q])
-  auto count16 = [&](const float (&vv)[16], uint32_t want, auto&& ix) __attribute__((always_inline)) {
-    count8(vv, want & 0xffu, ix);
-    count8(vv + 8, want >> 8, [&](int q) { return ix(q + 8); });
-  };
-  // the row's final values 16 per thread at a time: fn(vv, in, ix) with in's
+  // the row's final values 8 per thread at a time: fn(vv, in, ix) with in's
   // bit q set where vv[q] is an unpatched value of the row, whose index is
-  // ix(q).  The loops run the same number of times on every lane of a wave
-  // (fn reduces over the wave) and stop when a lane has filled the table.
+  // ix(q).  With 16-byte loads the next 8 are requested before these are
+  // counted, so the counting runs while they are in flight (16 values in
+  // registers, as many as a CU's request queue keeps in flight for the
+  // workgroup).  The loops run the same number of times on every lane of a
+  // wave (fn reduces over the wave) and stop when a lane has filled the
+  // table.
   const int wbase = __builtin_amdgcn_readfirstlane(tid - lane);  // (uniform over the wave)
   // the lane's index, computed where it is used (the compiler cannot move it
   // earlier and keep it in a register)
@@ -2092,18 +2091,22 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
     return l;
   };
-  auto for_each16 = [&](auto&& fn) __attribute__((always_inline)) {
+  auto for_each8 = [&](auto&& fn) __attribute__((always_inline)) {
     if (vec) {
-      for (int w4 = wbase; w4 < V4; w4 += 4 * NT) {
-        const int b4 = w4 + lane;
-        float4 x[4];
+      float4 nx[2];
+      auto request = [&](int w4) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) x[u] = src4[min(b4 + u * NT, V4 - 1)];
-        float vv[16];
+        for (int u = 0; u < 2; ++u) nx[u] = src4[min(w4 + lane + u * NT, V4 - 1)];
+      };
+      if (wbase < V4) request(wbase);
+      for (int w4 = wbase; w4 < V4; w4 += 2 * NT) {
+        const float4 x[2] = {nx[0], nx[1]};
+        if (w4 + 2 * NT < V4) request(w4 + 2 * NT);  // (uniform)
+        float vv[8];
         uint32_t in = 0u;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i4 = b4 + u * NT;
+        for (int u = 0; u < 2; ++u) {
+          const int i4 = w4 + lane + u * NT;
           const uint32_t pb = i4 < V4 ? (L.bitmap[i4 >> 3] >> ((i4 & 7) * 4)) & 15u : 15u;
           vv[4 * u + 0] = x[u].x * invT;
           vv[4 * u + 1] = x[u].y * invT;
@@ -2117,12 +2120,12 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
         if (__ballot(bad)) break;
       }
     } else {
-      for (int w0 = wbase; w0 < V; w0 += 16 * NT) {
+      for (int w0 = wbase; w0 < V; w0 += 8 * NT) {
         const int b = w0 + lane;
-        float vv[16];
+        float vv[8];
         uint32_t in = 0u;
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
+        for (int q = 0; q < 8; ++q) {
           const int i = b + q * NT;
           vv[q] = i < V ? src[i] * invT : 0.0f;
           if (i < V && !((L.bitmap[i >> 5] >> (i & 31)) & 1u)) in |= 1u << q;
@@ -2145,9 +2148,9 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   if (rmx > -__builtin_inff()) atomicMax(&s_rkey, f2key(rmx));
   __syncthreads();
   rmx = key2f(s_rkey);
-  for_each16([&](const float (&vv)[16], uint32_t in, auto&& ix) {
+  for_each8([&](const float (&vv)[8], uint32_t in, auto&& ix) {
 #pragma unroll
-    for (int q = 0; q < 16; ++q)
+    for (int q = 0; q < 8; ++q)
       if ((in >> q) & 1u) {
         nan |= (vv[q] != vv[q]);
         rmx = __builtin_fmaxf(rmx, vv[q]);
@@ -2158,9 +2161,9 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     rmx = __builtin_fmaxf(rmx, key2f(s_rkey));
     uint32_t want = 0u;
 #pragma unroll
-    for (int q = 0; q < 16; ++q)
+    for (int q = 0; q < 8; ++q)
       if (((in >> q) & 1u) && vv[q] - rmx >= kGroupFloor) want |= 1u << q;
-    count16(vv, want, ix);
+    count8(vv, want, ix);
   });
   for (int sl = tid; sl < np && !bad; sl += NT) {
     const float v = L.pfin[sl];
@@ -2194,12 +2197,12 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     if (tid == 0) s_distinct = 0;
     bad = false;
     __syncthreads();
-    for_each16([&](const float (&vv)[16], uint32_t in, auto&& ix) {
+    for_each8([&](const float (&vv)[8], uint32_t in, auto&& ix) {
       uint32_t want = 0u;
 #pragma unroll
-      for (int q = 0; q < 16; ++q)
+      for (int q = 0; q < 8; ++q)
         if (((in >> q) & 1u) && vv[q] - mx >= kGroupFloor) want |= 1u << q;
-      count16(vv, want, ix);
+      count8(vv, want, ix);
     });
     for (int sl = tid; sl < np && !bad; sl += NT) {
       const float v = L.pfin[sl];
