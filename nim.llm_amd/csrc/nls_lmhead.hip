@@ -748,12 +748,52 @@ __device__ __forceinline__ void deq8(const uint8_t* __restrict__ rp, int64_t e0,
   }
 }
 
+// The 2- and 4-byte types' eight weights as loaded (F32: both pieces; F16,
+// BF16: `a`), so that a segment's load can go out one segment ahead.
+struct Raw8 {
+  uint4 a, b;
+};
+template <int T>
+__device__ __forceinline__ Raw8 raw8(const uint8_t* __restrict__ rp, int64_t e0, int64_t cols) {
+  Raw8 r{make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+  if (e0 + 8 <= cols) {
+    if constexpr (T == 0) {
+      r.a = ld_16(rp + 4 * e0);
+      r.b = ld_16(rp + 4 * e0 + 16);
+    } else {
+      r.a = ld_16(rp + 2 * e0);
+    }
+  }
+  return r;
+}
+template <int T>
+__device__ __forceinline__ void cvt8(const Raw8& r, float (&w)[8]) {
+  if constexpr (T == 0) {
+    const uint32_t u[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[j] = __uint_as_float(u[j]);
+  } else {
+    const uint32_t u[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (T == 1) {
+        w[2 * j] = half_f(u[j] & 0xFFFF);
+        w[2 * j + 1] = half_f(u[j] >> 16);
+      } else {
+        w[2 * j] = __uint_as_float(u[j] << 16);
+        w[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
+      }
+    }
+  }
+}
+
 // dotF32 (quant.nim:362-374) of each dequantised row with each x row: lane
 // k of an aligned group of 8 runs chain k (weights k, k + 8, ...), lane 0
 // takes the cols % 8 tail, and the chains combine as the reference adds them.
 // The row is read in 16-byte pieces: the 8 lanes of a row dequantise 64
 // consecutive weights (8 each) and pass them through LDS so that lane k holds
-// chain k's 8 of them.  32 rows per workgroup; up to kLmNBC activation rows
+// chain k's 8 of them; for the 2- and 4-byte types the next 64 are requested
+// before these are used.  32 rows per workgroup; up to kLmNBC activation rows
 // per pass over the row.
 template <int T, bool XLDS>
 __global__ __launch_bounds__(kLmNT) void lm_float_kernel(FloatArgs a) {
@@ -778,9 +818,20 @@ __global__ __launch_bounds__(kLmNT) void lm_float_kernel(FloatArgs a) {
       }
       __syncthreads();
     }
+    // F32, F16, BF16: the next segment's 16-byte pieces are requested before
+    // this segment is used
+    constexpr bool kPre = T == 0 || T == 1 || T == 30;
+    Raw8 nxt{};
+    if constexpr (kPre) nxt = raw8<T>(rp, 8 * k, c8);
     for (int64_t seg = 0; seg < c8; seg += 64) {
       float w[8];
-      deq8<T>(rp, seg + 8 * k, c8, w);
+      if constexpr (kPre) {
+        const Raw8 cur = nxt;
+        if (seg + 64 < c8) nxt = raw8<T>(rp, seg + 64 + 8 * k, c8);
+        cvt8<T>(cur, w);
+      } else {
+        deq8<T>(rp, seg + 8 * k, c8, w);
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) s_t[grp][k][j] = w[j];
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
