@@ -2060,6 +2060,7 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   // occurrences, collisions) probe.
   bool bad = false;
   auto count8 = [&](const float* vv, uint32_t want, auto&& ix) __attribute__((always_inline)) {
+    if (__ballot(want != 0u) == 0ull) return;  // (uniform) nothing of the wave's within the floor
     uint32_t hs[8], cur[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) hs[q] = (f2key(vv[q]) * 0x9E3779B1u) >> (32 - kGrpHashBits);
