@@ -98,6 +98,38 @@ __device__ __forceinline__ int group8_sum(int v) {
   return v;
 }
 template <int CTRL, bool BOUND>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, BOUND);
+}
+// NB per-state block sums of an aligned group of 8 lanes (lane p = 0..7 of
+// the group), reduced at once: lanes exchange the halves of their states
+// they do not keep (quad_perm 1,0,3,2, then 2,3,0,1), so each lane of a quad
+// holds one state's quad sum, and row_shr:4 adds the other quad.  Lanes 4..7
+// get the totals of states group8_state<NB>(p) (NB = 4: 0, 2, 1, 3; NB = 2:
+// 0, 1, 0, 1): 4 DPP moves for four states instead of 12.
+template <int NB>
+__device__ __forceinline__ int group8_state(int p) {
+  return NB == 4 ? (((p & 1) << 1) | ((p >> 1) & 1)) : (p & 1);
+}
+template <int NB>
+__device__ __forceinline__ int group8_sum_states(const int (&v)[NB], int p) {
+  static_assert(NB == 2 || NB == 4, "two or four states");
+  const bool odd = p & 1;
+  int t;
+  if constexpr (NB == 2) {
+    const int keep = odd ? v[1] : v[0], send = odd ? v[0] : v[1];
+    t = keep + dpp_i<0xB1, false>(send);
+    t += dpp_i<0x4E, false>(t);
+  } else {
+    const int k0 = odd ? v[2] : v[0], k1 = odd ? v[3] : v[1];
+    const int x0 = odd ? v[0] : v[2], x1 = odd ? v[1] : v[3];
+    const int r0 = k0 + dpp_i<0xB1, false>(x0), r1 = k1 + dpp_i<0xB1, false>(x1);
+    const bool hi = (p & 2) != 0;
+    t = (hi ? r1 : r0) + dpp_i<0x4E, false>(hi ? r0 : r1);
+  }
+  return t + dpp_i<0x114, true>(t);  // row_shr:4
+}
+template <int CTRL, bool BOUND>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, BOUND));
 }
@@ -552,16 +584,31 @@ __global__ __launch_bounds__(kLmNT) void lm_int1_kernel(Int1Args a) {
 #pragma unroll
     for (int d = 0; d < kRing; ++d) {
       const int rr = rr0 + d / P, ps = d % P;
+      if constexpr (F::LPB == 8 && NB == 4) {  // (two states: measured faster one at a time)
+        // the states' sums reduced together; lane p >= 4 writes state st's term
+        int si[NB], sm[NB];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        int si, sm;
-        F::partial(ring[d], act[b][ps], p, si, sm);
-        if (F::LPB == 8) {
-          si = group8_sum(si);
-          if (F::HAS_MIN) sm = group8_sum(sm);
+        for (int b = 0; b < NB; ++b) F::partial(ring[d], act[b][ps], p, si[b], sm[b]);
+        const int ti = group8_sum_states<NB>(si, p);
+        const int tm = F::HAS_MIN ? group8_sum_states<NB>(sm, p) : 0;
+        const int st = group8_state<NB>(p);
+        float adv = ad[0][ps];
+#pragma unroll
+        for (int b = 1; b < NB; ++b) adv = st == b ? ad[b][ps] : adv;
+        if (p >= 4 && st < nb && rr < nrow && ib[ps] < a.nblk)
+          term[(st * a.rw + rr) * a.nblk + ib[ps]] = F::term(ring[d], ti, tm, adv);
+      } else {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          int si, sm;
+          F::partial(ring[d], act[b][ps], p, si, sm);
+          if (F::LPB == 8) {
+            si = group8_sum(si);
+            if (F::HAS_MIN) sm = group8_sum(sm);
+          }
+          if (b < nb && rr < nrow && ib[ps] < a.nblk && p == F::LPB - 1)
+            term[(b * a.rw + rr) * a.nblk + ib[ps]] = F::term(ring[d], si, sm, ad[b][ps]);
         }
-        if (b < nb && rr < nrow && ib[ps] < a.nblk && p == F::LPB - 1)
-          term[(b * a.rw + rr) * a.nblk + ib[ps]] = F::term(ring[d], si, sm, ad[b][ps]);
       }
       // the slot's next unit, kRing units on: loaded into the registers just
       // freed, so the ring needs no copies between turns
