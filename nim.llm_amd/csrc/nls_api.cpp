@@ -539,6 +539,7 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   // Greedy and top-k <= 64 rows streamed whole by 1024-thread workgroups run
   // k64_kernel, its patch hash table as large as the LDS allows.
   s->plan.k64 = false;
+  s->plan.k64_rows = kK64RowsAny;
   s->hbits = 0;
   if (stream_ok && g.wave && g.nt == 1024 && g.S == 1 && env_int("NLS_K64", 1)) {
     int hb = 0;
@@ -548,6 +549,14 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
       s->plan.k64 = true;
       s->hbits = hb;
       s->plan.lds = k64_lds_bytes(vocab, hb);
+      // the instance for the kinds of streamed rows present
+      bool any_greedy = false, any_topk = false;
+      for (int b = 0; b < B; ++b) {
+        if (!s->h_rp[b].fast) continue;
+        any_greedy |= s->h_rp[b].mode == kModeGreedy;
+        any_topk |= s->h_rp[b].mode == kModeTopK;
+      }
+      if (any_greedy != any_topk) s->plan.k64_rows = any_greedy ? kK64RowsGreedy : kK64RowsTopK;
     }
   }
   // Without full-sort rows the whole-row kernel only serves the rare row the

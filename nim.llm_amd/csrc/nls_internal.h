@@ -172,9 +172,15 @@ struct StreamArgs {
 };
 
 
+// k64_kernel instances by the streamed rows they serve
+constexpr int kK64RowsAny = 0;     // greedy and top-k rows
+constexpr int kK64RowsTopK = 1;    // top-k rows only
+constexpr int kK64RowsGreedy = 2;  // greedy rows only
+
 struct LaunchPlan {
   int nt;        // streaming workgroup size: 256, 512 (k > 64, two per CU) or 1024
   bool k64;      // k64_kernel instead of stream_kernel (wave path, one workgroup per row)
+  int k64_rows;  // the kinds of streamed rows: kK64RowsAny, kK64RowsTopK or kK64RowsGreedy
   bool wave;     // every top-k row has k <= kWaveTopK: per-wave candidate buffers
   int q;         // per-thread top-Q of the threshold refresh: 1, 2, 4 or 8
   bool vec4;     // 16-byte loads (V % 4 == 0 and aligned logits)

@@ -245,7 +245,11 @@ __device__ __forceinline__ void k64_tail(uint64_t x, int k, const RowParams& P, 
   }
 }
 
-template <bool VEC>
+// RK: the kinds of streamed rows the instance serves (kK64RowsAny: greedy and
+// top-k, kK64RowsTopK, kK64RowsGreedy).  An instance for one kind compiles
+// only that kind's code, so neither kind's registers and branches weigh on
+// the other's.
+template <bool VEC, int RK>
 __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k64_kernel(const StreamArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ int smem[kNW + 4];
@@ -347,12 +351,16 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
       st0 = load_const(a.rng + 2 * row);
       st1 = load_const(a.rng + 2 * row + 1);
     }
-    if (P.mode == kModeFull || !P.fast) {
+    // (a streamed row of a kind the instance does not serve cannot occur: the
+    // host picks the instance from the rows' modes; the whole-row path would
+    // take it)
+    const bool served = RK == kK64RowsAny || (RK == kK64RowsGreedy) == (P.mode == kModeGreedy);
+    if (P.mode == kModeFull || !P.fast || !served) {
       if (tid == 0) pushed = push_generic(a.generic_list, a.generic_count, row);
       return;
     }
     if (wv == 0) NLS_STAMP(row, 1);
-    const bool greedy = P.mode == kModeGreedy;
+    const bool greedy = RK == kK64RowsAny ? P.mode == kModeGreedy : RK == kK64RowsGreedy;
     const int k = P.k;
 
     // ---- 2. patched ids: bitmap and hash table ----
@@ -564,22 +572,59 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
         return full || (VEC ? o < len : o + (q & 3) < len);
       };
       if (greedy) {
-        // argmax (:45-49): only a lane whose chunk maximum beats its running
-        // best walks the chunk in index order (strict >: the first index wins)
-        float tmx = -__builtin_inff();
-#pragma unroll
-        for (int q = 0; q < kNE; ++q)
-          if (valid(q) && v[q] > tmx) tmx = v[q];
+        // argmax (:45-49): one pass over the lane's values in index order
+        // keeps the first of the largest unpatched ones (strict >), which is
+        // then merged into the lane's running best.  Every lane of a wave
+        // runs it on every chunk: with 64 lanes some lane nearly always
+        // improves, so a per-lane gate would save nothing.  (A NaN is never
+        // taken; -inf only when nothing larger is met, as index 0's rule
+        // below and argmax_merge arrange.)
         if (first && tid == 0) s_x0 = v[0];
-        if (tmx > bv || (tmx == bv && bi == 0x7fffffff)) {
+        uint32_t pm = 0u;  // bit q: value q is patched (one bitmap word per float4 group)
+        if (has_patch) {
 #pragma unroll
-          for (int q = 0; q < kNE; ++q)
-            if (valid(q)) {
-              if (patched(loc_of(q)))
-                capture(loc_of(q), v[q]);
-              else
-                argmax_merge(bv, bi, v[q], loc_of(q));
-            }
+          for (int j = 0; j < kNV4; ++j) {
+            const int o = obase + j * kGS;
+            pm |= ((bitmap[min(o, len - 1) >> 5] >> (o & 31)) & 15u) << (4 * j);
+          }
+        }
+        const float b0 = bv;  // the lane's best before this chunk
+        const bool none = bi == 0x7fffffff;  // (no best yet: b0 is -inf and stands for no element)
+        float cv = -__builtin_inff();
+        int cq = -1;
+#pragma unroll
+        for (int q = 0; q < kNE; ++q) {
+          const bool ok = valid(q) && !((pm >> q) & 1u);
+          if (ok && v[q] > cv) {
+            cv = v[q];
+            cq = q;
+          }
+        }
+        if (cq < 0) {
+          // nothing above -inf: the first unpatched -inf, if any
+#pragma unroll
+          for (int q = kNE - 1; q >= 0; --q)
+            if (valid(q) && !((pm >> q) & 1u) && v[q] == cv) cq = q;
+        }
+        if (cq >= 0) argmax_merge(bv, bi, cv, obase + (cq >> 2) * kGS + (cq & 3));
+        // A patched id's original logit is captured when it beats the
+        // earlier best (or equals -inf with none yet).  The others cannot
+        // win: a non-riser's final value is at most its original logit
+        // (risers are listed already), and that best's index is smaller,
+        // since a lane meets its elements in index order.  (A NaN cannot
+        // win either.)
+        if (pm) {
+          auto want = [&](int q) -> bool {
+            return ((pm >> q) & 1u) && valid(q) && (v[q] > b0 || (none && v[q] == b0));
+          };
+          bool cap = false;
+#pragma unroll
+          for (int q = 0; q < kNE; ++q) cap |= want(q);
+          if (cap) {
+#pragma unroll
+            for (int q = 0; q < kNE; ++q)
+              if (want(q)) capture(loc_of(q), v[q]);
+          }
         }
         return;
       }
@@ -1054,20 +1099,42 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
   }
 }
 
+template <bool VEC>
+static void launch_k64_rows(const StreamArgs& a, const LaunchPlan& p, hipStream_t s) {
+  switch (p.k64_rows) {
+    case kK64RowsTopK:
+      hipLaunchKernelGGL((k64_kernel<VEC, kK64RowsTopK>), dim3(a.B), dim3(kNT), p.lds, s, a);
+      break;
+    case kK64RowsGreedy:
+      hipLaunchKernelGGL((k64_kernel<VEC, kK64RowsGreedy>), dim3(a.B), dim3(kNT), p.lds, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((k64_kernel<VEC, kK64RowsAny>), dim3(a.B), dim3(kNT), p.lds, s, a);
+  }
+}
+
 hipError_t launch_k64(const StreamArgs& a, const LaunchPlan& p, hipStream_t s) {
   if (p.vec4)
-    hipLaunchKernelGGL(k64_kernel<true>, dim3(a.B), dim3(kNT), p.lds, s, a);
+    launch_k64_rows<true>(a, p, s);
   else
-    hipLaunchKernelGGL(k64_kernel<false>, dim3(a.B), dim3(kNT), p.lds, s, a);
+    launch_k64_rows<false>(a, p, s);
   return hipGetLastError();
 }
 
-hipError_t set_k64_attributes() {
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k64_kernel<true>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kK64MaxDynLds);
-  if (e != hipSuccess) return e;
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(&k64_kernel<false>),
+template <bool VEC, int RK>
+static hipError_t set_k64_attr() {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(&k64_kernel<VEC, RK>),
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kK64MaxDynLds);
+}
+
+hipError_t set_k64_attributes() {
+  hipError_t e;
+  if ((e = set_k64_attr<true, kK64RowsAny>()) != hipSuccess) return e;
+  if ((e = set_k64_attr<true, kK64RowsTopK>()) != hipSuccess) return e;
+  if ((e = set_k64_attr<true, kK64RowsGreedy>()) != hipSuccess) return e;
+  if ((e = set_k64_attr<false, kK64RowsAny>()) != hipSuccess) return e;
+  if ((e = set_k64_attr<false, kK64RowsTopK>()) != hipSuccess) return e;
+  return set_k64_attr<false, kK64RowsGreedy>();
 }
 
 }  // namespace nls

@@ -191,6 +191,51 @@ def test_patched_ids_that_fall_or_rise(pkg, torch, B, V):
     compare_rows(x, plist, hists, biases, u, ids, dbg, f"B={B} V={V}")
 
 
+@pytest.mark.parametrize("B", [12, 264])
+def test_greedy_rows_resting_on_patched_ids_or_neg_inf(pkg, torch, B):
+    """Greedy rows (sampler.nim:45-49, :77-78) whose argmax rests on -inf or
+    on a patched id: rows of -inf with index 0 penalised or banned (answer
+    0), a biased id tying the maximum at a smaller index than an unpatched
+    one in the same lane, the same tie at a larger index (a later chunk of
+    the same lane), and an all -inf row but for its last id.  (B = 12 splits
+    rows over the CUs; B = 264 gives every row a workgroup.)"""
+    V = 70000
+    base = dict(temperature=0.0, topK=0, topP=1.0, minP=0.0, repeatPenalty=1.0, repeatLastN=0,
+                presencePenalty=0.0, frequencyPenalty=0.0, seed=5)
+    x = np.full((B, V), -1.0, dtype=np.float32)
+    plist, hists, biases = [], [], []
+    for b in range(B):
+        d, h, bias = dict(base), [], {}
+        kind = b % 6
+        if kind == 0:    # all -inf, index 0 penalised
+            x[b] = -np.inf; d.update(repeatPenalty=1.5); h = [0, 0, 17]
+        elif kind == 1:  # all -inf, index 0 banned
+            x[b] = -np.inf; bias = {0: -math.inf, 9: -2.0}
+        elif kind == 2:  # the biased (unchanged) id at 5 ties the unpatched 7 and 16389
+            x[b, [5, 7, 16389]] = 2.0; bias = {5: 0.0}
+        elif kind == 3:  # an unchanged id at 16389 ties 7, met later in the same lane
+            x[b, [7, 16389, 40000]] = 2.0; bias = {16389: 0.0}
+        elif kind == 4:  # all -inf but the last id, penalised to 0.0
+            x[b] = -np.inf; x[b, V - 1] = 0.0; d.update(repeatPenalty=2.0); h = [V - 1]
+        else:            # all -inf, penalised ids around index 0
+            x[b] = -np.inf; d.update(presencePenalty=1.0); h = [3, 0]
+        if (b // 6) % 2:  # the same rows with a top id that its presence penalty takes to -950
+            x[b, 60000] = 50.0; h = h + [60000]; d.update(presencePenalty=1000.0)
+        plist.append(d)
+        hists.append([int(i) for i in h])
+        biases.append(bias)
+    say(f"[greedy_edge_rows] B={B} V={V}")
+    u = np.zeros(B)
+    H = max(len(h) for h in hists)
+    hist = np.full((B, H), -1, dtype=np.int64)
+    for b, h in enumerate(hists):
+        hist[b, :len(h)] = h
+    params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
+    ids, dbg = run_gpu(pkg, torch, x, params, hist, u, debug_cap=64,
+                       accept_rows=[len(h) for h in hists])
+    compare_rows(x, plist, hists, biases, u, ids, dbg, f"B={B} V={V}")
+
+
 @pytest.mark.parametrize("B", [8, 300, 600])
 def test_topk_rows_in_sorted_order(pkg, torch, B):
     """Top-k rows (64 < k <= 2048) whose first tile is not typical of the row:
