@@ -163,6 +163,11 @@ struct nls_sampler {
   int32_t* generic_list = nullptr;
   int32_t* generic_count = nullptr;  // [2]
   int32_t* all_rows = nullptr;       // no streaming rows: 0 .. B-1, then B (the count), then a spare
+  // k64_kernel with full-sort rows in the batch: the streamed rows (its
+  // grid) and the others (the whole-row kernel's fixed list)
+  int32_t* k64_list = nullptr;
+  int32_t* full_list = nullptr;
+  int n_k64_list = 0, n_full_list = 0;
   uint32_t* done = nullptr;          // workgroups finished (whole-row rows served inline)
   int gen_inline = 0;
   uint32_t* gen_scratch = nullptr;
@@ -192,6 +197,8 @@ struct nls_sampler {
     dfree(generic_list);
     dfree(generic_count);
     dfree(all_rows);
+    dfree(k64_list);
+    dfree(full_list);
     dfree(done);
     dfree(gen_scratch);
     dfree(stage_ids);
@@ -619,6 +626,21 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
     const hipError_t e0 = hipMemcpy(s->all_rows, rows.data(), rows.size() * 4, hipMemcpyHostToDevice);
     if (e0 != hipSuccess) return fail(hip_fail(e0, "upload row list"));
   }
+  if (s->plan.k64 && any_full && any_fast) {
+    // Rows that are not streamed would only hand themselves on from a
+    // workgroup of their own; with random kinds that leaves some CUs many
+    // more streamed rows than others.  The grid takes the streamed rows
+    // alone, and the whole-row kernel the others from a fixed list.
+    std::vector<int32_t> fast, full;
+    for (int b = 0; b < B; ++b) (s->h_rp[b].fast ? fast : full).push_back(b);
+    if ((rc = dalloc(&s->k64_list, fast.size()))) return fail(rc);
+    if ((rc = dalloc(&s->full_list, full.size()))) return fail(rc);
+    hipError_t e0 = hipMemcpy(s->k64_list, fast.data(), fast.size() * 4, hipMemcpyHostToDevice);
+    if (e0 == hipSuccess) e0 = hipMemcpy(s->full_list, full.data(), full.size() * 4, hipMemcpyHostToDevice);
+    if (e0 != hipSuccess) return fail(hip_fail(e0, "upload row lists"));
+    s->n_k64_list = (int)fast.size();
+    s->n_full_list = (int)full.size();
+  }
   if ((rc = dalloc(&s->done, 1))) return fail(rc);
   int64_t vpad = 1;
   while (vpad < vocab) vpad <<= 1;
@@ -846,6 +868,12 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
     ga.generic_count = s->all_rows + s->B;
     ga.next_count = s->all_rows + s->B + 1;
     a.gen_inline = 0;
+  }
+  if (s->k64_list && !lp.no_stream) {
+    a.row_list = s->k64_list;
+    a.n_list = s->n_k64_list;
+    ga.fixed_list = s->full_list;
+    ga.n_fixed = s->n_full_list;
   }
   a.ga = ga;
   lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);

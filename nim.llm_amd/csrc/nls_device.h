@@ -2533,8 +2533,9 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
   uint32_t* kB = iA + a.vpad;
   uint32_t* iB = kB + a.vpad;
   float* work = reinterpret_cast<float*>(iB + a.vpad);
-  for (int li = w0; li < count; li += nw) {
-    const int row = load_agent(&a.generic_list[li]);
+  const int nfx = a.fixed_list ? a.n_fixed : 0;
+  for (int li = w0; li < nfx + count; li += nw) {
+    const int row = li < nfx ? a.fixed_list[li] : load_agent(&a.generic_list[li - nfx]);
     if (a.row_done && a.row_done[row] != 0) {  // a finished row of a batched loop
       if (tid == 0) a.out[row] = -1;
       continue;

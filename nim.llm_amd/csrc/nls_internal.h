@@ -127,6 +127,10 @@ struct GenericArgs {
   DebugPtrs dbg;
   int grouped;  // 1: the launch carries group_lds_bytes(V) of dynamic LDS
   const int32_t* row_done;  // [B] or null: a nonzero row samples nothing (out = -1)
+  // rows known to need this path when the sampler was made (full sorts),
+  // served before the listed ones; null: none
+  const int32_t* fixed_list;
+  int n_fixed;
 };
 
 struct StreamArgs {
@@ -168,6 +172,11 @@ struct StreamArgs {
   uint32_t* done;
   int hbits;    // k64_kernel: log2 of the patch hash table's slots
   const int32_t* row_done;  // [B] or null: a nonzero row samples nothing (out = -1)
+  // k64_kernel: the streamed rows, one per workgroup (a batch whose other
+  // rows go to the whole-row kernel from its fixed list); null: workgroup b
+  // takes row b
+  const int32_t* row_list;
+  int n_list;
   GenericArgs ga;
 };
 

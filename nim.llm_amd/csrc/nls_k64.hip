@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wv = tid >> 6;
-  const int row = (int)blockIdx.x;
+  const int row = a.row_list ? a.row_list[blockIdx.x] : (int)blockIdx.x;
   const int len = (int)a.V;
   const int hcap = 1 << a.hbits;
 
@@ -1101,15 +1101,16 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
 
 template <bool VEC>
 static void launch_k64_rows(const StreamArgs& a, const LaunchPlan& p, hipStream_t s) {
+  const dim3 grid(a.row_list ? a.n_list : a.B);
   switch (p.k64_rows) {
     case kK64RowsTopK:
-      hipLaunchKernelGGL((k64_kernel<VEC, kK64RowsTopK>), dim3(a.B), dim3(kNT), p.lds, s, a);
+      hipLaunchKernelGGL((k64_kernel<VEC, kK64RowsTopK>), grid, dim3(kNT), p.lds, s, a);
       break;
     case kK64RowsGreedy:
-      hipLaunchKernelGGL((k64_kernel<VEC, kK64RowsGreedy>), dim3(a.B), dim3(kNT), p.lds, s, a);
+      hipLaunchKernelGGL((k64_kernel<VEC, kK64RowsGreedy>), grid, dim3(kNT), p.lds, s, a);
       break;
     default:
-      hipLaunchKernelGGL((k64_kernel<VEC, kK64RowsAny>), dim3(a.B), dim3(kNT), p.lds, s, a);
+      hipLaunchKernelGGL((k64_kernel<VEC, kK64RowsAny>), grid, dim3(kNT), p.lds, s, a);
   }
 }
 
