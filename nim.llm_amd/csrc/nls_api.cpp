@@ -161,7 +161,7 @@ struct nls_sampler {
   uint32_t* arrive = nullptr;
   uint64_t* rng = nullptr;
   int32_t* generic_list = nullptr;
-  int32_t* generic_count = nullptr;  // [2]
+  int32_t* generic_count = nullptr;  // [4]
   int32_t* all_rows = nullptr;       // no streaming rows: 0 .. B-1, then B (the count), then a spare
   // k64_kernel with full-sort rows in the batch: the streamed rows (its
   // grid) and the others (the whole-row kernel's fixed list)
@@ -616,7 +616,7 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   if ((rc = dalloc(&s->arrive, B))) return fail(rc);
   if ((rc = dalloc(&s->rng, (size_t)2 * B))) return fail(rc);
   if ((rc = dalloc(&s->generic_list, B))) return fail(rc);
-  if ((rc = dalloc(&s->generic_count, 2))) return fail(rc);
+  if ((rc = dalloc(&s->generic_count, 4))) return fail(rc);  // counts, then claim counters (by call parity)
   if (s->plan.no_stream) {
     std::vector<int32_t> rows((size_t)B + 2);
     for (int b = 0; b < B; ++b) rows[b] = b;
@@ -671,7 +671,7 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
     return fail(hip_fail(e, "clear counters"));
   if ((e = hipMemsetAsync(s->done, 0, sizeof(uint32_t), st)) != hipSuccess)
     return fail(hip_fail(e, "clear counters"));
-  if ((e = hipMemsetAsync(s->generic_count, 0, sizeof(int32_t) * 2, st)) != hipSuccess)
+  if ((e = hipMemsetAsync(s->generic_count, 0, sizeof(int32_t) * 4, st)) != hipSuccess)
     return fail(hip_fail(e, "clear counters"));
   if ((e = hipStreamSynchronize(st)) != hipSuccess) return fail(hip_fail(e, "sync"));
   *out = s;
@@ -831,6 +831,12 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   ga.generic_list = s->generic_list;
   ga.generic_count = cnt_now;
   ga.next_count = cnt_next;
+  if (!s->gen_inline && !s->plan.no_stream) {
+    // every call of this sampler launches the whole-row kernel, which zeroes
+    // the next call's claim counter
+    ga.claim = s->generic_count + 2 + s->parity;
+    ga.next_claim = s->generic_count + 2 + (s->parity ^ 1);
+  }
   ga.scratch = s->gen_scratch;
   ga.vpad = s->gen_vpad;
   ga.d_u = d_u;

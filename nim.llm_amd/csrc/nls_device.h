@@ -511,7 +511,7 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
   }
 }
 
-template <int NT, bool GROUPED = false>
+template <int NT, bool GROUPED = false, bool CLAIM = false>
 __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int nw, int count, uint32_t* wcnt,
                                              uint32_t* dbase, uint32_t* drun, int* smem, double* s_u_p,
                                              int* s_i, float* s_rv, int* s_ri,
@@ -2521,7 +2521,7 @@ __device__ __forceinline__ bool window_topk(const GenericArgs& a, int row, const
 // Rows of the list from index w0 on, every nw-th: the whole-row path.  LDS
 // scratch is passed in (wcnt: NW * 256 words, dbase and drun: 256 each), so
 // that the streaming kernel's last workgroup can run it too.
-template <int NT, bool GROUPED>
+template <int NT, bool GROUPED, bool CLAIM>
 __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int nw, int count, uint32_t* wcnt,
                                              uint32_t* dbase, uint32_t* drun, int* smem, double* s_u_p,
                                              int* s_i, float* s_rv, int* s_ri, unsigned char* glds) {
@@ -2534,7 +2534,21 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
   uint32_t* iB = kB + a.vpad;
   float* work = reinterpret_cast<float*>(iB + a.vpad);
   const int nfx = a.fixed_list ? a.n_fixed : 0;
-  for (int li = w0; li < nfx + count; li += nw) {
+  // With a claim counter every workgroup takes the next unclaimed row when it
+  // is done with one, so rows of uneven cost spread evenly; the barriers keep
+  // the broadcast slot from being overwritten before every thread has read it.
+  // (only the whole-row kernel's claiming instance: the others keep their
+  // code, and the streaming kernels' last workgroup serves its rows alone)
+  __shared__ int s_claim;
+  auto next_row = [&](int li_static) -> int {
+    if constexpr (!CLAIM) return li_static;
+    if (!a.claim) return li_static;
+    __syncthreads();
+    if (tid == 0) s_claim = atomicAdd(a.claim, 1);
+    __syncthreads();
+    return s_claim;
+  };
+  for (int li = next_row(w0); li < nfx + count; li = next_row(li + nw)) {
     const int row = li < nfx ? a.fixed_list[li] : load_agent(&a.generic_list[li - nfx]);
     if (a.row_done && a.row_done[row] != 0) {  // a finished row of a batched loop
       if (tid == 0) a.out[row] = -1;
@@ -2733,7 +2747,9 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
   }
 }
 
-template <int NT>
+// CLAIM: workgroups claim rows one at a time (a.claim); otherwise workgroup w
+// takes list positions w, w + gridDim.x, ...
+template <int NT, bool CLAIM>
 __global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
   constexpr int NW = NT / kWave;
   __shared__ uint32_t wcnt[NW * 256];
@@ -2745,9 +2761,12 @@ __global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
   __shared__ float s_rv[NW];
   __shared__ int s_ri[NW];
   extern __shared__ __align__(16) unsigned char glds[];  // group_lds_bytes(V) when a.grouped
-  if (blockIdx.x == 0 && threadIdx.x == 0) *a.next_count = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *a.next_count = 0;
+    if (a.next_claim) *a.next_claim = 0;
+  }
   const int count = *a.generic_count;
-  generic_rows<NT, true>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri,
+  generic_rows<NT, true, CLAIM>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri,
                          glds);
 }
 

@@ -6,13 +6,20 @@
 namespace nls {
 
 hipError_t launch_generic(const GenericArgs& ga, const LaunchPlan& lp, hipStream_t s) {
-  hipLaunchKernelGGL(generic_kernel<kGenericThreads>, dim3(lp.gen_blocks), dim3(kGenericThreads),
-                     ga.grouped ? lp.gen_lds : 0, s, ga);
+  if (ga.claim)
+    hipLaunchKernelGGL((generic_kernel<kGenericThreads, true>), dim3(lp.gen_blocks), dim3(kGenericThreads),
+                       ga.grouped ? lp.gen_lds : 0, s, ga);
+  else
+    hipLaunchKernelGGL((generic_kernel<kGenericThreads, false>), dim3(lp.gen_blocks), dim3(kGenericThreads),
+                       ga.grouped ? lp.gen_lds : 0, s, ga);
   return hipGetLastError();
 }
 
 hipError_t set_generic_attributes() {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(&generic_kernel<kGenericThreads>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&generic_kernel<kGenericThreads, true>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)group_lds_bytes(kGrpMaxV));
+  if (e != hipSuccess) return e;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(&generic_kernel<kGenericThreads, false>),
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)group_lds_bytes(kGrpMaxV));
 }
 

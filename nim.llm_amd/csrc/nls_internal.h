@@ -119,6 +119,11 @@ struct GenericArgs {
   const int32_t* generic_list;
   const int32_t* generic_count;  // this call's counter
   int32_t* next_count;           // the next call's counter, zeroed here
+  // the next unclaimed list position (workgroups claim rows one at a time;
+  // null: workgroup w takes positions w, w + n, ...) and the next call's
+  // claim counter, zeroed here
+  int32_t* claim;
+  int32_t* next_claim;
   uint32_t* scratch;             // per workgroup: 5 x vpad uint32
   int64_t vpad;
   const double* d_u;
