@@ -191,6 +191,52 @@ def test_patched_ids_that_fall_or_rise(pkg, torch, B, V):
     compare_rows(x, plist, hists, biases, u, ids, dbg, f"B={B} V={V}")
 
 
+def test_mixed_batch_consecutive_calls(pkg, torch):
+    """One sampler over a batch mixing greedy, top-k and full-sort rows
+    (sampler.nim:77-97), called three times in a row on fresh logits and
+    uniforms: every row of every call against the oracle.  Such a batch runs
+    the streamed rows alone in the streaming grid and the full-sort rows from
+    a fixed list, with the whole-row kernel's workgroups claiming rows from a
+    counter that each call resets for the next."""
+    B, V = 320, 30000
+    rng = np.random.default_rng(77)
+    plist, hists, biases = [], [], []
+    for b in range(B):
+        kind = b % 5
+        d = dict(temperature=1.0, topK=0, topP=1.0, minP=0.0, repeatPenalty=1.0, repeatLastN=0,
+                 presencePenalty=0.0, frequencyPenalty=0.0, seed=2)
+        if kind == 0:
+            d.update(temperature=0.0)
+        elif kind == 1:
+            d.update(topK=20)
+        elif kind == 2:
+            d.update(minP=0.1)
+        elif kind == 3:
+            d.update(topP=0.8)
+        else:
+            d.update(topK=50, presencePenalty=0.5, repeatLastN=16)
+        plist.append(d)
+        hists.append([int(i) for i in rng.integers(0, V, 24)])
+        biases.append({int(rng.integers(0, V)): 1.5} if b % 7 == 0 else {})
+    params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
+    s = pkg.BatchSampler(params, V)
+    try:
+        plan, streamed = s.plan()
+        say(f"[mixed_batch_calls] B={B} V={V} k64={plan.k64} streamed={sum(streamed)}")
+        assert plan.k64 and 0 < sum(streamed) < B
+        s.accept(np.array(hists, dtype=np.int64))
+        for call in range(3):
+            x = (np.round(rng.standard_normal((B, V)) * 8.0) / 4.0).astype(np.float32)
+            u = rng.random(B)
+            d = torch.from_numpy(x).cuda()
+            du = torch.from_numpy(u).cuda()
+            ids = s.sample(d, du).cpu().numpy()
+            torch.cuda.synchronize()
+            compare_rows(x, plist, hists, biases, u, ids, None, f"call {call}")
+    finally:
+        s.close()
+
+
 @pytest.mark.parametrize("B", [12, 264])
 def test_greedy_rows_resting_on_patched_ids_or_neg_inf(pkg, torch, B):
     """Greedy rows (sampler.nim:45-49, :77-78) whose argmax rests on -inf or
