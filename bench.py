@@ -807,9 +807,13 @@ def main():
     ap.add_argument("--lm-cols", type=int, default=2048)
     ap.add_argument("--lm-nb", type=int, default=1)
     ap.add_argument("--lm-exact", action="store_true", help="exactMatmul: the float path")
+    ap.add_argument("--lib", default="",
+                    help="time this build of the library instead of nim.llm_amd/libnimllm_sampler.so")
     ap.add_argument("--phase-stamps", action="store_true",
                     help="per-phase times of the k64 kernel from the phases build of the library")
     args = ap.parse_args()
+    if args.lib:
+        load_pkg().LIB_PATH = os.path.abspath(args.lib)
     if args.traffic_summary:
         return traffic_summary(args)
     if args.phase_stamps:
