@@ -820,7 +820,7 @@ def main():
         return phase_stamps(args)
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (rows shard across GPUs with no "
-              "collective; see DESIGN.md); --gpus must be 1", file=sys.stderr)
+              "collective: each GPU samples its own rows); --gpus must be 1", file=sys.stderr)
         sys.exit(2)
 
     if args.top_tokens:

@@ -79,7 +79,19 @@ enum {
   NLS_PATH_GREEDY = 1,     /* argmax                                          */
   NLS_PATH_TOPK = 2,       /* chunked top-k candidates + exact merge          */
   NLS_PATH_FULL = 3,       /* full-vocabulary (sort) path, fast prefix kernel */
-  NLS_PATH_GENERIC = 4     /* whole-row sort; rows the fast kernels hand off  */
+  NLS_PATH_GENERIC = 4,    /* whole-row sort; rows the fast kernels hand off  */
+  NLS_PATH_WINDOW = 5,     /* whole-row kernel, top-k members without a sort  */
+  /* Flag OR-ed into the path of a sampling row with a NaN among its
+   * candidates.  The reference's heap and merge-sort comparisons
+   * (sampler.nim:88-97) make the result of a row with any NaN final logit
+   * depend on element order, so such a row is outside the parity claim.
+   * Here a NaN with the sign bit clear (the NaN the GPU's arithmetic makes)
+   * orders above +inf and is always a candidate, so its row is always
+   * flagged; one with the sign bit set orders below -inf and is flagged when
+   * it is a candidate (full-sort rows, or k above the row's other values).
+   * Greedy rows follow argmax (sampler.nim:45-49) exactly, NaN included, and
+   * are never flagged. */
+  NLS_PATH_NAN = 0x100
 };
 
 /* Presets: defaultSampling (sampler.nim:28-31) and greedySampling (:33-35). */

@@ -167,6 +167,7 @@ struct TailOut {
   int id;
   int n;
   float total;
+  int nan_cand;  // kPathNaN when a candidate value is NaN, else 0
 };
 
 // Wave-level fp32 chain over x[0..cnt) in index order: acc = acc OP x[0] OP
@@ -288,6 +289,9 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
   t.n = s_n;
   t.total = s_total;
   t.id = ids[s_pos];
+  // (NaN keys sort to the ends of the candidate order)
+  const float last = val[ncand - 1];
+  t.nan_cand = (mx != mx || last != last) ? kPathNaN : 0;
   return t;
 }
 
@@ -498,12 +502,13 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
   const uint64_t hit = __ballot(lane < n && rl <= 0.0f);
   const int pos = hit ? __ffsll((unsigned long long)hit) - 1 : n - 1;
   const int tok = __builtin_amdgcn_readlane(id, pos);
+  const bool nan_c = dbg.path && __ballot(valid && v != v) != 0ull;  // a NaN candidate
   if (lane == 0) {
     out[row] = tok;
     if (dbg.n) dbg.n[row] = n;
     if (dbg.ncand) dbg.ncand[row] = k;
     if (dbg.total) dbg.total[row] = total;
-    if (dbg.path) dbg.path[row] = path;
+    if (dbg.path) dbg.path[row] = path | (nan_c ? kPathNaN : 0);
   }
   if (lane < min(n, dbg.cap)) {
     if (dbg.cand_ids) dbg.cand_ids[(int64_t)row * dbg.cap + lane] = id;
@@ -1701,7 +1706,7 @@ void stream_kernel(const StreamArgs a) {
     const TailOut to = softmax_cutoff_draw<NT>(vals, ids, ebuf, k, P, s_u, smem);
     if (wv == 0) NLS_STAMP(row, 6);
     if (tid == 0) a.out[row] = to.id;
-    write_debug<NT>(a.dbg, row, 2, to.n, k, to.total, ids, ebuf);
+    write_debug<NT>(a.dbg, row, 2 | to.nan_cand, to.n, k, to.total, ids, ebuf);
   };
   run();
   if (a.gen_inline) {
@@ -2513,7 +2518,7 @@ __device__ __forceinline__ bool window_topk(const GenericArgs& a, int row, const
   __syncthreads();
   const TailOut to = softmax_cutoff_draw<NT>(vals, ids, ebuf, k, P, *s_u_p, smem);
   if (tid == 0) a.out[row] = to.id;
-  write_debug<NT>(a.dbg, row, 5, to.n, k, to.total, ids, ebuf);
+  write_debug<NT>(a.dbg, row, 5 | to.nan_cand, to.n, k, to.total, ids, ebuf);
   __syncthreads();
   return true;
 }
@@ -2674,7 +2679,7 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
       const TailOut t = softmax_cutoff_draw<NT>(work, iA, reinterpret_cast<float*>(kB), n, P, *s_u_p,
                                                 smem);
       if (tid == 0) a.out[row] = t.id;
-      write_debug<NT>(a.dbg, row, 4, t.n, n, t.total, iA, reinterpret_cast<float*>(kB));
+      write_debug<NT>(a.dbg, row, 4 | t.nan_cand, t.n, n, t.total, iA, reinterpret_cast<float*>(kB));
       if (gout.ok && tid == 0) {
         a.out[row] = gout.id;
         if (a.dbg.n) a.dbg.n[row] = gout.n;
@@ -2741,7 +2746,7 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
     const TailOut t = softmax_cutoff_draw<NT>(work, reinterpret_cast<int32_t*>(kB),
                                               reinterpret_cast<float*>(iB), k, P, *s_u_p, smem);
     if (tid == 0) a.out[row] = t.id;
-    write_debug<NT>(a.dbg, row, 4, t.n, k, t.total, reinterpret_cast<int32_t*>(kB),
+    write_debug<NT>(a.dbg, row, 4 | t.nan_cand, t.n, k, t.total, reinterpret_cast<int32_t*>(kB),
                     reinterpret_cast<float*>(iB));
     __syncthreads();
   }

@@ -92,6 +92,13 @@ struct DebugPtrs {
   int32_t cap;
 };
 
+// OR-ed into a sampling row's debug path code when a NaN is among the row's
+// candidates.  The key map orders a NaN with the sign bit clear above +inf
+// (always a candidate) and one with it set below -inf; the reference's heap
+// and sort comparisons (src/nimllm/sampler.nim:88-97) leave a row with any
+// NaN order-dependent, so such a row's result is this sampler's own.
+constexpr int32_t kPathNaN = 0x100;
+
 // Grouped sort path of the whole-row kernel (full-sort rows replayed over
 // their distinct values): LDS for the row's patch table, a hash table of the
 // distinct values and their sorted list.  Rows that need more take the

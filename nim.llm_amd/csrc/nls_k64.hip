@@ -232,12 +232,13 @@ __device__ __forceinline__ void k64_tail(uint64_t x, int k, const RowParams& P, 
   const uint64_t hit = __ballot(lane < n && rl <= 0.0f);
   const int pos = hit ? __ffsll((unsigned long long)hit) - 1 : n - 1;
   const int tok = __builtin_amdgcn_readlane(id, pos);
+  const bool nan_c = dbg.path && __ballot(valid && v != v) != 0ull;  // a NaN candidate
   if (lane == 0) {
     out[row] = tok;
     if (dbg.n) dbg.n[row] = n;
     if (dbg.ncand) dbg.ncand[row] = k;
     if (dbg.total) dbg.total[row] = total;
-    if (dbg.path) dbg.path[row] = 2;
+    if (dbg.path) dbg.path[row] = 2 | (nan_c ? kPathNaN : 0);
   }
   if (lane < min(n, dbg.cap)) {
     if (dbg.cand_ids) dbg.cand_ids[(int64_t)row * dbg.cap + lane] = id;

@@ -478,19 +478,35 @@ typedef struct {
   int expf_mode;
   int64_t* out;
   nlo_result* res;
+  int64_t cap;         /* candidates kept per row in cand_ids / cand_probs */
+  int64_t* cand_ids;   /* [B, cap] or NULL */
+  float* cand_probs;   /* [B, cap] or NULL */
   int64_t r0, r1;
 } batch_job;
 
 static void* batch_worker(void* arg) {
   batch_job* j = (batch_job*)arg;
+  const int want = j->cap > 0 && j->cand_ids && j->cand_probs;
+  int64_t* ci = want ? (int64_t*)malloc((size_t)j->V * sizeof(int64_t)) : NULL;
+  float* cp = want ? (float*)malloc((size_t)j->V * sizeof(float)) : NULL;
   for (int64_t r = j->r0; r < j->r1; ++r) {
+    nlo_result rr;
     j->out[r] = nlo_sample(&j->p[r], j->logits + r * j->V, j->V,
                            j->hist ? j->hist + r * j->H : NULL, j->hlen ? j->hlen[r] : 0,
                            j->bias_ids ? j->bias_ids + r * j->NB : NULL,
                            j->bias_vals ? j->bias_vals + r * j->NB : NULL,
-                           j->nb ? j->nb[r] : 0, j->u[r], j->expf_mode,
-                           j->res ? &j->res[r] : NULL, NULL, NULL, NULL);
+                           j->nb ? j->nb[r] : 0, j->u[r], j->expf_mode, &rr, ci, cp, NULL);
+    if (j->res) j->res[r] = rr;
+    if (want) {
+      const int64_t m = rr.ncand < j->cap ? rr.ncand : j->cap;
+      for (int64_t i = 0; i < j->cap; ++i) {
+        j->cand_ids[r * j->cap + i] = i < m ? ci[i] : -1;
+        j->cand_probs[r * j->cap + i] = i < m ? cp[i] : 0.0f;
+      }
+    }
   }
+  free(ci);
+  free(cp);
   return NULL;
 }
 
@@ -508,6 +524,16 @@ void nlo_sample_batch_res(const nlo_params* p, const float* logits, int64_t B, i
                           const int64_t* bias_ids, const double* bias_vals, int64_t NB,
                           const int64_t* nb, const double* u, int expf_mode,
                           int64_t* out_ids, nlo_result* res, int nthreads) {
+  nlo_sample_batch_cand(p, logits, B, V, hist, H, hlen, bias_ids, bias_vals, NB, nb, u, expf_mode,
+                        out_ids, res, 0, NULL, NULL, nthreads);
+}
+
+void nlo_sample_batch_cand(const nlo_params* p, const float* logits, int64_t B, int64_t V,
+                           const int64_t* hist, int64_t H, const int64_t* hlen,
+                           const int64_t* bias_ids, const double* bias_vals, int64_t NB,
+                           const int64_t* nb, const double* u, int expf_mode,
+                           int64_t* out_ids, nlo_result* res, int64_t cap, int64_t* cand_ids,
+                           float* cand_probs, int nthreads) {
   if (nthreads < 1) nthreads = 1;
   if (nthreads > B) nthreads = (int)(B > 0 ? B : 1);
   batch_job* jobs = (batch_job*)calloc((size_t)nthreads, sizeof(batch_job));
@@ -528,6 +554,9 @@ void nlo_sample_batch_res(const nlo_params* p, const float* logits, int64_t B, i
     j->expf_mode = expf_mode;
     j->out = out_ids;
     j->res = res;
+    j->cap = cap;
+    j->cand_ids = cand_ids;
+    j->cand_probs = cand_probs;
     j->r0 = B * t / nthreads;
     j->r1 = B * (t + 1) / nthreads;
   }

@@ -108,6 +108,16 @@ void nlo_sample_batch_res(const nlo_params* p, const float* logits, int64_t B, i
                           const int64_t* nb, const double* u, int expf_mode,
                           int64_t* out_ids, nlo_result* res, int nthreads);
 
+/* nlo_sample_batch_res that also writes the first cap candidates of every
+ * row (ids and probabilities, as nlo_sample's cand / probs give them) into
+ * cand_ids[B, cap] and cand_probs[B, cap]; entries past ncand hold -1 / 0. */
+void nlo_sample_batch_cand(const nlo_params* p, const float* logits, int64_t B, int64_t V,
+                           const int64_t* hist, int64_t H, const int64_t* hlen,
+                           const int64_t* bias_ids, const double* bias_vals, int64_t NB,
+                           const int64_t* nb, const double* u, int expf_mode,
+                           int64_t* out_ids, nlo_result* res, int64_t cap, int64_t* cand_ids,
+                           float* cand_probs, int nthreads);
+
 /* argmax (sampler.nim:45-49): first index of the greatest value. */
 int64_t nlo_argmax(const float* x, int64_t n);
 /* softmaxInPlace (sampler.nim:51-57). */

@@ -99,6 +99,8 @@ def lib():
             P(ctypes.c_double), ctypes.c_int, P(ctypes.c_int64), ctypes.c_int,
         ]
         L.nlo_sample_batch_res.argtypes = L.nlo_sample_batch.argtypes[:-1] + [P(Result), ctypes.c_int]
+        L.nlo_sample_batch_cand.argtypes = L.nlo_sample_batch.argtypes[:-1] + [
+            P(Result), ctypes.c_int64, P(ctypes.c_int64), P(ctypes.c_float), ctypes.c_int]
         L.nlo_argmax.argtypes = [P(ctypes.c_float), ctypes.c_int64]
         L.nlo_argmax.restype = ctypes.c_int64
         L.nlo_softmax_inplace.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int]
@@ -189,9 +191,12 @@ def sample(params: Params, logits, history=(), bias=None, u=0.5,
 
 
 def sample_batch(params_list, logits, hist=None, hlen=None, bias_ids=None, bias_vals=None,
-                 nb=None, u=None, expf_mode=EXPF_LIBM, nthreads=1, want_res=False):
+                 nb=None, u=None, expf_mode=EXPF_LIBM, nthreads=1, want_res=False, cand_cap=0):
     """Rows [B, V] through the restated sampler on `nthreads` threads.  Returns
-    the ids, or (ids, list of Result) with want_res."""
+    the ids, or (ids, list of Result) with want_res, or with cand_cap > 0
+    (ids, list of Result, cand_ids [B, cand_cap], cand_probs [B, cand_cap]):
+    each row's first cand_cap candidates in the order sampler.nim:85-100
+    leaves them (-1 / 0 past the row's candidate count)."""
     L = lib()
     x = np.ascontiguousarray(logits, dtype=np.float32)
     B, V = x.shape
@@ -214,6 +219,12 @@ def sample_batch(params_list, logits, hist=None, hlen=None, bias_ids=None, bias_
         L.nlo_sample_batch(*args, nthreads)
         return out
     res = (Result * max(B, 1))()
+    if cand_cap > 0:
+        ci = np.zeros((B, cand_cap), dtype=np.int64)
+        cp = np.zeros((B, cand_cap), dtype=np.float32)
+        L.nlo_sample_batch_cand(*args, res, cand_cap, _ptr(ci, ctypes.c_int64),
+                                _ptr(cp, ctypes.c_float), nthreads)
+        return out, [res[i] for i in range(B)], ci, cp
     L.nlo_sample_batch_res(*args, res, nthreads)
     return out, [res[i] for i in range(B)]
 

@@ -1,6 +1,6 @@
 /*
  * nim_binding_check.c -- makes exactly the C-ABI calls of the Nim binding
- * described in INTEGRATION.md (a `Sampler` whose sample/accept forward to a
+ * a Nim maintainer adds to src/nimllm/sampler.nim (a `Sampler` whose sample/accept forward to a
  * one-row handle) and checks every sampled id against the oracle.
  *
  * The reference loop it follows: src/nimllm/chat.nim:204-208 (sample, stop on

@@ -191,6 +191,75 @@ def test_patched_ids_that_fall_or_rise(pkg, torch, B, V):
     compare_rows(x, plist, hists, biases, u, ids, dbg, f"B={B} V={V}")
 
 
+NAN_POS = np.uint32(0x7FC00000).view(np.float32)  # sign bit clear: orders above +inf
+NAN_NEG = np.uint32(0xFFC00000).view(np.float32)  # sign bit set: orders below -inf
+
+
+@pytest.mark.parametrize("case", ["k64_topk40", "k64_small_topk50", "split_topk40", "full_sort",
+                                  "topk300"])
+def test_nan_rows_flagged_others_bit_exact(pkg, torch, case):
+    """Sampling rows with a NaN final logit are outside the parity claim (the
+    reference's heap and sort comparisons, sampler.nim:88-97, make them
+    order-dependent).  The debug path code carries NLS_PATH_NAN (0x100) on
+    every row whose candidates hold a NaN: always for a NaN with the sign bit
+    clear (above +inf in the key order), and for one with it set (below
+    -inf) on full-sort rows.  The batch's other rows stay bit-exact against
+    the oracle and unflagged, and a greedy row with a NaN logit follows
+    argmax (sampler.nim:45-49)."""
+    V, k, B, seed = {"k64_topk40": (128256, 40, 256, 1), "k64_small_topk50": (32000, 50, 8, 2),
+                     "split_topk40": (128256, 40, 12, 3), "full_sort": (50000, 0, 8, 4),
+                     "topk300": (100000, 300, 8, 5)}[case]
+    rng = np.random.default_rng(seed)
+    say(f"[nan_rows] {case} B={B} V={V} k={k}")
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    base = dict(temperature=0.9, topK=k, topP=0.95, minP=0.0, repeatPenalty=1.0, repeatLastN=0,
+                presencePenalty=0.0, frequencyPenalty=0.0, seed=3)
+    plist = [dict(base) for _ in range(B)]
+    biases = [{} for _ in range(B)]
+    expect = {}  # row -> flagged?
+    x[1, int(rng.integers(0, V))] = NAN_POS
+    expect[1] = True
+    x[2, rng.choice(V, 3 * max(k, 64), replace=False)] = NAN_POS  # more NaNs than candidates
+    expect[2] = True
+    biases[3] = {int(rng.integers(0, V)): math.nan}  # a NaN bias makes the final logit NaN
+    expect[3] = True
+    x[4, int(rng.integers(0, V))] = NAN_NEG
+    expect[4] = k == 0  # a candidate only on a full-sort row
+    x[5, 7] = NAN_POS  # greedy: argmax skips it
+    plist[5]["temperature"] = 0.0
+    clean = [b for b in range(B) if b not in expect and b != 5]
+    params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
+    u = rng.random(B)
+    s = pkg.BatchSampler(params, V)
+    try:
+        plan, streamed = s.plan()
+        say(f"[nan_rows] {case}: k64={plan.k64} streamed={sum(streamed)}")
+        if case.startswith("k64"):
+            assert plan.k64 and all(streamed)
+        if case == "split_topk40":  # rows split over several workgroups
+            assert not plan.k64 and all(streamed)
+        d = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+        du = torch.from_numpy(u).cuda()
+        ids, dbg = s.sample(d, du, debug_cap=64)
+        torch.cuda.synchronize()
+        ids = ids.cpu().numpy()
+        dbg = {kk: vv.cpu().numpy() for kk, vv in dbg.items()}
+    finally:
+        s.close()
+    assert ids.min() >= 0 and ids.max() < V
+    path = dbg["path"]
+    for b, flagged in expect.items():
+        assert bool(path[b] & 0x100) == flagged, (case, b, hex(int(path[b])))
+    assert not (path[5] & 0x100) and path[5] == 1
+    res = O.sample(O.make_params(**plist[5]), x[5], (), {}, 0.5, O.EXPF_CR, want_cand=False)[0]
+    assert ids[5] == res.id == int(np.argmax(np.where(np.isnan(x[5]), -np.inf, x[5])))
+    for b in clean:
+        assert not (path[b] & 0x100), (case, b, hex(int(path[b])))
+    cd = {kk: vv[clean] for kk, vv in dbg.items()}
+    compare_rows(x[clean], [plist[b] for b in clean], [()] * len(clean), [biases[b] for b in clean],
+                 u[clean], ids[clean], cd, f"nan_rows {case}")
+
+
 def test_mixed_batch_consecutive_calls(pkg, torch):
     """One sampler over a batch mixing greedy, top-k and full-sort rows
     (sampler.nim:77-97), called three times in a row on fresh logits and
@@ -454,7 +523,7 @@ def test_golden_fixtures(pkg, torch):
 
 WORKLOAD_NAMES = ["single_32k", "zipf_minp_128k", "headline", "penalties_152k", "flat_topk1000",
                   "mixed_ties_152k"]
-# The north star's window: a row may differ from the reference (the oracle
+# The parity window: a row may differ from the reference (the oracle
 # with the C library's expf) only when one of its draws or cutoffs lies within
 # 1e-6 of a boundary: the draw (margin_draw, in units of the CDF), the top-p
 # running sum (margin_topp, absolute) or the min-p threshold (margin_minp,
@@ -463,7 +532,8 @@ EXC_WINDOW = 1e-6
 
 
 def exception_classes(res):
-    """SURVEY-style exception classes a row falls in, from an oracle Result."""
+    """The exception classes (draw, top-p, min-p boundary) a row falls in, from
+    an oracle Result."""
     out = []
     if res.greedy:
         return out
@@ -490,10 +560,11 @@ def write_report(name, record):
 @pytest.mark.parametrize("name", WORKLOAD_NAMES)
 def test_workload_parity(pkg, torch, name):
     """Every row of the workload at full size against the oracle, in both exp
-    modes.  Against the correctly rounded exp (the device's) ids, n and the
-    total are bit-exact on every row.  Against the C library's expf (what the
-    reference's exp(float32) calls) a row may differ only inside the north
-    star's 1e-6 window, which the libm oracle's own margins must show."""
+    modes.  Against the correctly rounded exp (the device's) ids, n, the
+    total and the first min(n, 64) kept candidates (ids and probabilities)
+    are bit-exact on every sampling row.  Against the C library's expf (what the
+    reference's exp(float32) calls) a row may differ only inside the 1e-6
+    window of a draw or cutoff boundary, which the libm oracle's own margins must show."""
     from nimllm_amd import workloads
 
     w = workloads.make(name, seed=7)
@@ -506,20 +577,28 @@ def test_workload_parity(pkg, torch, name):
     H = w.hist.shape[1]
     hist = w.hist if H else None
     hl = np.full(w.B, H)
-    oc, rc = O.sample_batch(plist, w.logits, hist, hl, bid, bval, bcnt, w.u, O.EXPF_CR,
-                            nthreads=8, want_res=True)
+    cap = dbg["cand_ids"].shape[1]
+    oc, rc, oci, ocp = O.sample_batch(plist, w.logits, hist, hl, bid, bval, bcnt, w.u, O.EXPF_CR,
+                                      nthreads=8, want_res=True, cand_cap=cap)
     ol, rl = O.sample_batch(plist, w.logits, hist, hl, bid, bval, bcnt, w.u, O.EXPF_LIBM,
                             nthreads=8, want_res=True)
     say(f"[workload_parity] {name}: oracle done for {w.B} rows in both exp modes")
-    # (1) correctly rounded exp: every row bit-exact (id, n, total)
+    # (1) correctly rounded exp: every row bit-exact (id, n, total, and the
+    # first min(n, 64) kept candidates' ids and probabilities)
     bad = np.nonzero(ids != oc)[0]
     assert bad.size == 0, (name, bad[:10].tolist())
+    cand_rows = 0
     for b in range(w.B):
         r = rc[b]
         if r.greedy:
             continue
         assert int(dbg["n"][b]) == r.n, (name, b, int(dbg["n"][b]), r.n)
         assert dbg["total"][b].view(np.uint32) == np.float32(r.total).view(np.uint32), (name, b)
+        m = min(int(r.n), cap)
+        assert np.array_equal(dbg["cand_ids"][b, :m].astype(np.int64), oci[b, :m]), (name, b)
+        assert np.array_equal(dbg["cand_probs"][b, :m].view(np.uint32), ocp[b, :m].view(np.uint32)), (
+            name, b)
+        cand_rows += 1
     # (2) the C library's expf: differing rows lie in the 1e-6 window
     counts = {"E1_draw": 0, "E2_topp": 0, "E3_minp": 0}
     for b in range(w.B):
@@ -533,6 +612,7 @@ def test_workload_parity(pkg, torch, name):
     oracle_flips = int(np.sum(oc != ol))
     paths = np.bincount(dbg["path"], minlength=5).tolist()
     record = {"rows": int(w.B), "rows_bit_exact_cr_exp": int(w.B - bad.size),
+              "rows_candidates_compared": cand_rows,
               "rows_differing_from_libm_exp": int(differ.size),
               "rows_where_oracle_cr_and_libm_differ_E4": oracle_flips,
               "rows_in_window": counts, "paths_greedy_topk_full_generic": paths[1:]}
@@ -722,8 +802,8 @@ def test_generate_step_batched_contexts(pkg, torch):
 
 
 def test_nim_binding_call_sequence(pkg, torch):
-    """tests/nim_binding_check.c makes exactly the calls of the Nim binding in
-    INTEGRATION.md (create, set the RNG state from the Nim Rand, replay the
+    """tests/nim_binding_check.c makes exactly the calls of the Nim binding of the
+    sampler (create, set the RNG state from the Nim Rand, replay the
     history, then sample_host / accept per step, skipping accept on an
     end-of-generation id) and checks every id against the oracle."""
     import os

@@ -228,6 +228,38 @@ def test_invariants():
         assert res.id == int(np.argmax(x))
 
 
+def test_batch_candidates_match_single_rows():
+    """The threaded batch call's first-cap candidates, results and ids equal
+    one nlo_sample call per row (greedy, top-k and full-sort rows, penalties,
+    bias, rows with fewer candidates than the cap)."""
+    rng = np.random.default_rng(12)
+    B, V, H, NB, cap = 24, 700, 16, 3, 64
+    x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    x[3, :] = 0.5  # one flat row: every candidate tied
+    plist, rows = [], []
+    for b in range(B):
+        kw = dict(temperature=[0.0, 0.8, 1.2][b % 3], topK=[0, 5, 40, 1000, V][b % 5],
+                  topP=[1.0, 0.9][b % 2], minP=[0.0, 0.05][(b // 2) % 2], repeatPenalty=1.1,
+                  repeatLastN=8, presencePenalty=0.2, frequencyPenalty=0.1, seed=b)
+        plist.append(O.make_params(**kw))
+        rows.append(kw)
+    hist = rng.integers(0, V, (B, H)).astype(np.int64)
+    hl = np.full(B, H, dtype=np.int64)
+    bid = np.stack([rng.choice(V, NB, replace=False) for _ in range(B)]).astype(np.int64)
+    bval = rng.standard_normal((B, NB))
+    nb = np.full(B, NB, dtype=np.int64)
+    u = rng.random(B)
+    ids, res, ci, cp = O.sample_batch(plist, x, hist, hl, bid, bval, nb, u, O.EXPF_CR,
+                                      nthreads=4, want_res=True, cand_cap=cap)
+    for b in range(B):
+        bias = {int(i): float(v) for i, v in zip(bid[b], bval[b])}
+        r1, cand, probs, _ = O.sample(plist[b], x[b], hist[b], bias, u[b], O.EXPF_CR)
+        assert ids[b] == r1.id and res[b].id == r1.id and res[b].n == r1.n
+        m = min(len(cand), cap)
+        assert np.array_equal(ci[b, :m], cand[:m]) and np.all(ci[b, m:] == -1)
+        assert np.array_equal(cp[b, :m].view(np.uint32), probs[:m].view(np.uint32))
+
+
 def test_penalty_identity_and_brute_force():
     rng = np.random.default_rng(4)
     V = 50
