@@ -53,6 +53,11 @@ typedef struct nls_lora {
   float scale;
 } nls_lora;
 
+/* rowBytes(type, cols) (quant.nim:65-70): the bytes of one weight row, or -1
+ * for a type the reference cannot read or a cols that is not whole blocks
+ * (where rowBytes raises).  d_weight must hold rows times this. */
+int64_t nls_lm_head_row_bytes(int32_t ggml_type, int64_t cols);
+
 /* Bytes of device workspace nls_lm_head needs for these sizes (0 when the
  * call needs none).  `exact` is the reference's exactMatmul switch
  * (model.nim:173-175).  Returns 0 for an unsupported type as well. */

@@ -192,6 +192,14 @@ int nls_set_rng_state(nls_sampler* s, int32_t row, uint64_t a0, uint64_t a1);
 int nls_top_tokens(const float* d_logits, int32_t rows, int64_t vocab, int32_t n, int32_t* d_ids,
                    float* d_probs, void* stream);
 
+/* argmax (src/nimllm/sampler.nim:45-49) of each of `rows` rows of d_logits
+ * [rows x vocab] (device, row-major): d_out[r] = the first index of the
+ * row's greatest value.  As in the reference, a NaN is never taken, a NaN at
+ * index 0 answers 0, and vocab == 0 answers 0 for every row.  Bit-exact (an
+ * index).  Asynchronous on `stream`; vocab >= 2^29 is
+ * NLS_ERR_INVALID_ARGUMENT. */
+int nls_argmax(const float* d_logits, int32_t rows, int64_t vocab, int32_t* d_out, void* stream);
+
 /* perplexity's per-position term (src/nimllm/model.nim:578-583): for each of
  * `rows` rows of d_logits [rows x vocab] (device, row-major) and its target id
  * d_targets[r] in [0, vocab), d_out[r] = -(float64(l[t] - mx) - ln(s)), with mx

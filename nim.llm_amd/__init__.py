@@ -38,7 +38,7 @@ EXPORTED = (
     "nls_top_tokens", "nls_row_nll", "nls_softmax_rows", "nls_log_prob", "nls_expf_device",
     "nls_profile_next",
     "nls_profile_next_generic", "nls_get_plan", "nls_status_string", "nls_last_error",
-    "nls_lm_head_workspace", "nls_lm_head",
+    "nls_lm_head_workspace", "nls_lm_head", "nls_lm_head_row_bytes", "nls_argmax",
 )
 
 
@@ -141,6 +141,9 @@ def lib():
         L.nls_lm_head_workspace.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                             ctypes.c_int32]
         L.nls_lm_head_workspace.restype = ctypes.c_size_t
+        L.nls_lm_head_row_bytes.argtypes = [ctypes.c_int32, ctypes.c_int64]
+        L.nls_lm_head_row_bytes.restype = ctypes.c_int64
+        L.nls_argmax.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, vp, vp]
         L.nls_lm_head.argtypes = [vp, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, vp, ctypes.c_int32, vp,
                                   ctypes.c_int32, P(NlsLora), vp, ctypes.c_size_t, vp]
         L.nls_lm_head.restype = ctypes.c_int32
@@ -448,6 +451,33 @@ def topTokens(logits, n: int = 5):
     return [(int(i), float(p)) for i, p in zip(ids[0].tolist(), probs[0].tolist())]
 
 
+def argmax_device(logits):
+    """argmax (sampler.nim:45-49) of every row of a [rows, V] (or [V])
+    float32 device tensor: int32 [rows], the first index of each row's
+    greatest value (a NaN never taken; a NaN at index 0 answers 0)."""
+    import torch
+
+    x = logits if logits.dim() == 2 else logits.reshape(1, -1)
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    rows, V = x.shape
+    out = torch.empty(rows, dtype=torch.int32, device=x.device)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    check(lib().nls_argmax(ctypes.c_void_p(x.data_ptr()) if V else None, rows, V,
+                           ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream)), "nls_argmax")
+    return out
+
+
+def argmax(logits) -> int:
+    """argmax (sampler.nim:45-49) of one row of logits (any float32 sequence
+    or tensor), computed on the device."""
+    import numpy as np
+    import torch
+
+    x = logits if torch.is_tensor(logits) else torch.from_numpy(np.ascontiguousarray(logits, dtype=np.float32))
+    x = x.reshape(1, -1).to(device="cuda", dtype=torch.float32).contiguous()
+    return int(argmax_device(x)[0].item())
+
+
 def row_nll_device(logits, targets):
     """perplexity's per-position term (src/nimllm/model.nim:578-583) for a
     [rows, V] float32 device tensor and int32 target ids [rows]: float64
@@ -561,7 +591,14 @@ def lm_head(weight, ggml_type: int, rows: int, cols: int, x, exact: bool = False
 
     x2 = x if x.dim() == 2 else x.reshape(1, -1)
     assert x2.is_cuda and x2.dtype == torch.float32 and x2.is_contiguous() and x2.shape[1] == cols
-    assert weight.is_cuda and weight.is_contiguous()
+    rb = int(lib().nls_lm_head_row_bytes(ggml_type, cols))
+    if rb < 0:
+        raise SamplerError(f"lm_head: type {ggml_type} with cols={cols} is not a readable GGUF row "
+                           "(rowBytes raises)")
+    assert weight.is_cuda and weight.is_contiguous() and weight.dtype == torch.uint8
+    assert weight.device == x2.device, "lm_head: weight and x on different devices"
+    assert weight.numel() >= rows * rb, (
+        f"lm_head: weight holds {weight.numel()} bytes, rows x rowBytes = {rows * rb}")
     nb = x2.shape[0]
     if out is None:
         out = torch.empty((nb, rows), dtype=torch.float32, device=x2.device)
@@ -571,7 +608,11 @@ def lm_head(weight, ggml_type: int, rows: int, cols: int, x, exact: bool = False
     if lora is not None:
         a, b, scale = lora
         assert a.is_contiguous() and b.is_contiguous() and a.dtype == torch.float32 and b.dtype == torch.float32
+        assert a.is_cuda and b.is_cuda and a.device == x2.device and b.device == x2.device
+        assert a.dim() == 2 and b.dim() == 2
         rank = a.shape[0]
+        assert tuple(a.shape) == (rank, cols) and tuple(b.shape) == (rows, rank), (
+            f"lm_head: LoRA a {tuple(a.shape)} must be ({rank}, {cols}), b {tuple(b.shape)} ({rows}, {rank})")
         lo = NlsLora(a.data_ptr(), b.data_ptr(), rank, float(scale))
     need = lm_head_workspace(ggml_type, cols, nb, rank, exact)
     if work is None or work.numel() < need:

@@ -149,6 +149,9 @@ struct nls_sampler {
   int S = 1, L = 0, xcd_map = 0;
   int ccap = 0, nwords = 0, pcap = 0, mcap = 0, kcap = 0, offA = 0, pc = 0;
   int parity = 0;  // which generic counter this call uses
+  // set when a call failed after some of its kernels may have run: the
+  // counters it would have handed on are cleared before the next call
+  bool counters_dirty = false;
   int hbits = 0;   // k64_kernel's hash table: 2^hbits slots
 
   RowParams* rp = nullptr;
@@ -785,6 +788,11 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
     dp.path = dbg->path;
     dp.cap = dbg->cap;
   }
+  if (s->counters_dirty) {
+    NLS_HIP(launch_clear_counters(s->arrive, s->B, s->done, s->generic_count, s->stream));
+    s->parity = 0;
+    s->counters_dirty = false;
+  }
   int32_t* cnt_now = s->generic_count + s->parity;
   int32_t* cnt_next = s->generic_count + (s->parity ^ 1);
   StreamArgs a;
@@ -885,7 +893,12 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
   hipEvent_t e0 = s->prof_start, e1 = s->prof_stop, g0 = s->prof_gstart, g1 = s->prof_gstop;
   s->prof_start = s->prof_stop = s->prof_gstart = s->prof_gstop = nullptr;
-  NLS_HIP(launch_sample(a, ga, lp, s->stream, e0, e1, g0, g1));
+  const hipError_t le = launch_sample(a, ga, lp, s->stream, e0, e1, g0, g1);
+  if (le != hipSuccess) {
+    // a kernel of this call may have run and left its counters for the next
+    s->counters_dirty = true;
+    return hip_fail(le, "launch_sample");
+  }
   s->parity ^= 1;
   return NLS_OK;
 }
@@ -980,13 +993,15 @@ int nls_sample_host_noalloc(nls_sampler* s, const float* h_logits, int64_t* h_ou
   NLS_HIP(hipMemcpyAsync(d_logits, h_logits, n * 4, hipMemcpyHostToDevice, s->stream));
   const int rc = sample_impl(s, d_logits, nullptr, d_out, nullptr, false);
   if (rc) return rc;
-  // the int32 ids land in the first half of h_out and are widened in place,
-  // from the last one down (no host buffer either)
-  int32_t* narrow = reinterpret_cast<int32_t*>(h_out);
-  NLS_HIP(hipMemcpyAsync(narrow, d_out, (size_t)s->B * 4, hipMemcpyDeviceToHost, s->stream));
+  // the int32 ids land in the first half of h_out's bytes and are widened in
+  // place, from the last one down (no host buffer either; each narrow id is
+  // read as bytes before its slot's wide store can overlap it)
+  unsigned char* bytes = reinterpret_cast<unsigned char*>(h_out);
+  NLS_HIP(hipMemcpyAsync(bytes, d_out, (size_t)s->B * 4, hipMemcpyDeviceToHost, s->stream));
   NLS_HIP(hipStreamSynchronize(s->stream));
   for (int b = s->B - 1; b >= 0; --b) {
-    const int32_t v = narrow[b];
+    int32_t v;
+    std::memcpy(&v, bytes + (size_t)4 * b, sizeof v);
     h_out[b] = v;
   }
   return NLS_OK;
@@ -1036,6 +1051,15 @@ int nls_row_nll(const float* d_logits, int32_t rows, int64_t vocab, const int32_
   if (vocab == 0) return NLS_ERR_EMPTY_VOCAB;
   if (!d_logits || !d_targets || !d_out) return NLS_ERR_INVALID_ARGUMENT;
   NLS_HIP(launch_row_nll(d_logits, rows, vocab, d_targets, d_out, reinterpret_cast<hipStream_t>(stream)));
+  return NLS_OK;
+}
+
+int nls_argmax(const float* d_logits, int32_t rows, int64_t vocab, int32_t* d_out, void* stream) {
+  // (the kernel addresses a row in bytes with 32-bit offsets)
+  if (rows < 0 || vocab < 0 || vocab >= (int64_t{1} << 29)) return NLS_ERR_INVALID_ARGUMENT;
+  if (rows == 0) return NLS_OK;
+  if (!d_out || (vocab > 0 && !d_logits)) return NLS_ERR_INVALID_ARGUMENT;
+  NLS_HIP(launch_argmax(d_logits, rows, vocab, d_out, reinterpret_cast<hipStream_t>(stream)));
   return NLS_OK;
 }
 
@@ -1125,6 +1149,11 @@ LmLayout lm_layout(int type, int64_t cols, int nb, int rank, bool exact) {
 }  // namespace
 
 extern "C" {
+
+int64_t nls_lm_head_row_bytes(int32_t type, int64_t cols) {
+  if (!lm_type_supported(type) || cols <= 0 || cols % lm_block_size(type) != 0) return -1;
+  return cols / lm_block_size(type) * lm_type_bytes(type);
+}
 
 size_t nls_lm_head_workspace(int32_t type, int64_t cols, int32_t nb, int32_t lora_rank, int32_t exact) {
   if (!lm_type_supported(type) || cols <= 0 || nb < 0 || lora_rank < 0) return 0;

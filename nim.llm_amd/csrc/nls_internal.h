@@ -218,6 +218,7 @@ hipError_t launch_accept_host(const int32_t* d_ids, const int32_t* d_cnt, int B,
                               int32_t* hist, int64_t* hist_len, int hcap, int row_only, hipStream_t s);
 // one batched generation step after the sampling: rows not done finish on an
 // end-of-generation id, else accept theirs
+hipError_t launch_clear_counters(uint32_t* arrive, int B, uint32_t* done, int32_t* gcount, hipStream_t s);
 hipError_t launch_generate_step(const int32_t* d_out, int B, int64_t V, const int32_t* eog, int n_eog,
                                 int32_t* row_done, int32_t* hist, int64_t* hist_len, int hcap, hipStream_t s);
 hipError_t launch_accept_device(const int32_t* d_ids, int B, int64_t V, int32_t* hist,
@@ -226,6 +227,7 @@ hipError_t launch_expf(const float* x, float* y, int64_t n, hipStream_t s);
 // topTokens over `rows` rows of V logits: n results per row (stride n), n <= kTopMaxN or V <= kTopMaxN
 constexpr int kTopThreads = 1024;
 constexpr int kTopMaxN = 2048;   // largest number of results per row (sorted in LDS)
+hipError_t launch_argmax(const float* logits, int rows, int64_t V, int32_t* out, hipStream_t s);
 hipError_t launch_row_nll(const float* logits, int rows, int64_t V, const int32_t* targets, double* out,
                           hipStream_t s);
 hipError_t launch_top_tokens(const float* logits, int rows, int64_t V, int n, int32_t* ids,

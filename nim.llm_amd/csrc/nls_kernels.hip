@@ -404,6 +404,96 @@ __global__ __launch_bounds__(NT) void row_nll_kernel(const float* __restrict__ l
   }
 }
 
+// argmax (src/nimllm/sampler.nim:45-49) of each row (one workgroup per row):
+// `best` moves to i only when l[i] > l[best], so the answer is the first
+// index of the greatest value, a NaN is never taken, a NaN at index 0 keeps
+// the answer 0, and an empty row answers 0.  Each thread keeps the first of
+// its largest values (its elements arrive in index order); the threads'
+// (value, index) pairs then reduce by larger value, then smaller index.
+template <int NT>
+__global__ __launch_bounds__(NT) void argmax_rows_kernel(const float* __restrict__ logits, int64_t V,
+                                                         int32_t* __restrict__ out) {
+  constexpr int NW = NT / kWave;
+  constexpr int kNone = 0x7fffffff;
+  __shared__ float s_v[NW];
+  __shared__ int s_i[NW];
+  const int row = (int)blockIdx.x;
+  const int tid = (int)threadIdx.x;
+  const int lane = lane_id();
+  const int wv = tid >> 6;
+  if (V == 0) {
+    if (tid == 0) out[row] = 0;
+    return;
+  }
+  const float* __restrict__ x = logits + (int64_t)row * V;
+  const __amdgpu_buffer_rsrc_t xr = slice_rsrc(x, (int)V);  // V < 2^29 (checked by the host)
+  float bv = -__builtin_inff();
+  int bi = kNone;
+  auto take = [&](float l, int i, bool in) __attribute__((always_inline)) {
+    if (in && (l > bv || (l == bv && i < bi))) {
+      bv = l;
+      bi = i;
+    }
+  };
+  const bool vec = (V % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+  if (vec) {
+    const int V4 = (int)(V >> 2);
+    for (int b = tid; b < V4; b += NT * 4) {
+      f32x4 q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i4 = b + u * NT;
+        q[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             xr, i4 < V4 ? i4 * 16 : 0x7ffffff0, 0, 0));
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i4 = b + u * NT;
+        const bool in = i4 < V4;
+        take(q[u].x, 4 * i4, in);
+        take(q[u].y, 4 * i4 + 1, in);
+        take(q[u].z, 4 * i4 + 2, in);
+        take(q[u].w, 4 * i4 + 3, in);
+      }
+    }
+  } else {
+    constexpr int U = 8;
+    for (int i0 = 0; i0 < (int)V; i0 += NT * U) {
+      float l[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * NT + tid;
+        l[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             xr, i < (int)V ? i * 4 : 0x7ffffff0, 0, 0));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) take(l[u], i0 + u * NT + tid, i0 + u * NT + tid < (int)V);
+    }
+  }
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    s_v[wv] = bv;
+    s_i[wv] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < NW; ++w)
+      if (s_v[w] > bv || (s_v[w] == bv && s_i[w] < bi)) {
+        bv = s_v[w];
+        bi = s_i[w];
+      }
+    const float x0 = x[0];
+    out[row] = (x0 != x0 || bi == kNone) ? 0 : bi;
+  }
+}
+
 // ids: [rows x count] staged ids (skipped entries already removed), row b
 // appending its first cnt[b] of them.
 __global__ void accept_host_kernel(const int32_t* __restrict__ ids, const int32_t* __restrict__ cnt,
@@ -506,6 +596,21 @@ hipError_t launch_accept_host(const int32_t* d_ids, const int32_t* d_cnt, int B,
   return hipGetLastError();
 }
 
+// Zeroes a handle's per-call counters: the S > 1 arrival counts, the
+// finished-workgroup count and the four handed-on / claim counters.
+__global__ void clear_counters_kernel(uint32_t* arrive, int B, uint32_t* done, int32_t* gcount) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < B) arrive[i] = 0u;
+  if (i == 0) *done = 0u;
+  if (i < 4) gcount[i] = 0;
+}
+
+hipError_t launch_clear_counters(uint32_t* arrive, int B, uint32_t* done, int32_t* gcount, hipStream_t s) {
+  const int n = B > 4 ? B : 4;
+  hipLaunchKernelGGL(clear_counters_kernel, dim3((n + 255) / 256), dim3(256), 0, s, arrive, B, done, gcount);
+  return hipGetLastError();
+}
+
 hipError_t launch_generate_step(const int32_t* d_out, int B, int64_t V, const int32_t* eog, int n_eog,
                                 int32_t* row_done, int32_t* hist, int64_t* hist_len, int hcap, hipStream_t s) {
   hipLaunchKernelGGL(generate_step_kernel, dim3((B + 255) / 256), dim3(256), 0, s, d_out, B, V, eog, n_eog,
@@ -544,6 +649,14 @@ hipError_t launch_top_tokens(const float* logits, int rows, int64_t V, int n, in
 hipError_t launch_row_nll(const float* logits, int rows, int64_t V, const int32_t* targets, double* out,
                           hipStream_t s) {
   hipLaunchKernelGGL(row_nll_kernel<1024>, dim3(rows), dim3(1024), 0, s, logits, V, targets, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* logits, int rows, int64_t V, int32_t* out, hipStream_t s) {
+  if (V < 32768)
+    hipLaunchKernelGGL(argmax_rows_kernel<256>, dim3(rows), dim3(256), 0, s, logits, V, out);
+  else
+    hipLaunchKernelGGL(argmax_rows_kernel<1024>, dim3(rows), dim3(1024), 0, s, logits, V, out);
   return hipGetLastError();
 }
 

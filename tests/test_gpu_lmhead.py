@@ -143,3 +143,34 @@ def test_lm_head_feeds_sampler(pkg):
                       seed=5)
     want = [O.sample(p, want_logits[b], u=u[b], expf_mode=O.EXPF_CR)[0].id for b in range(B)]
     assert list(ids) == want
+
+
+@pytest.mark.gpu
+def test_lm_head_rejects_mismatched_tensors(pkg):
+    """The wrapper refuses, before any launch, a weight of the wrong dtype or
+    fewer than rows x rowBytes bytes, a cols that is not whole blocks, and
+    LoRA tensors of the wrong shape."""
+    import torch
+
+    t, rows, cols = O.GGML["Q6_K"], 64, 512
+    rb = int(pkg.lib().nls_lm_head_row_bytes(t, cols))
+    assert rb == O.row_bytes(t, cols)
+    assert pkg.lib().nls_lm_head_row_bytes(t, cols + 1) == -1
+    assert pkg.lib().nls_lm_head_row_bytes(99, cols) == -1
+    x = torch.zeros((1, cols), dtype=torch.float32, device="cuda")
+    w = torch.zeros(rows * rb, dtype=torch.uint8, device="cuda")
+    with pytest.raises(AssertionError):
+        pkg.lm_head(w[:-1], t, rows, cols, x)
+    with pytest.raises(AssertionError):
+        pkg.lm_head(w.view(torch.int8), t, rows, cols, x)
+    with pytest.raises(pkg.SamplerError):
+        pkg.lm_head(w, t, rows, cols + 1, torch.zeros((1, cols + 1), dtype=torch.float32, device="cuda"))
+    a = torch.zeros((4, cols), dtype=torch.float32, device="cuda")
+    b = torch.zeros((rows, 4), dtype=torch.float32, device="cuda")
+    with pytest.raises(AssertionError):
+        pkg.lm_head(w, t, rows, cols, x, lora=(a, b[:, :3].contiguous(), 1.0))
+    with pytest.raises(AssertionError):
+        pkg.lm_head(w, t, rows, cols, x, lora=(a[:, :-1].contiguous(), b, 1.0))
+    y = pkg.lm_head(w, t, rows, cols, x, lora=(a, b, 1.0))  # the well-formed call runs
+    torch.cuda.synchronize()
+    assert y.shape == (1, rows)

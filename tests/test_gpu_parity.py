@@ -1026,3 +1026,46 @@ def test_row_nll_parity(pkg, torch):
     t = np.array([3, 5000], np.int32)
     got = pkg.row_nll_device(torch.from_numpy(x).cuda(), torch.from_numpy(t)).cpu().numpy()
     assert math.isnan(got[0]) and math.isnan(got[1])
+
+
+def test_argmax_parity(pkg, torch):
+    """argmax (src/nimllm/sampler.nim:45-49) on the device against the
+    oracle's nlo_argmax (pinned to numpy.argmax's first maximum): ties, -0 and
+    +0, -inf, NaN at index 0 and elsewhere, rows of NaN only, one-element and
+    empty rows, rows whose length is not a multiple of 4 (4-byte loads) and
+    rows of the vocabularies the sampler serves (16-byte loads)."""
+    import ctypes
+
+    rng = np.random.default_rng(45)
+    L = O.lib()
+    P = ctypes.POINTER(ctypes.c_float)
+
+    def ref(row):
+        r = np.ascontiguousarray(row, dtype=np.float32)
+        return int(L.nlo_argmax(r.ctypes.data_as(P), len(r))) if len(r) else 0
+
+    for B, V in ((13, 1), (13, 7), (13, 1001), (16, 32000), (64, 128256), (8, 151936), (9, 40003)):
+        say(f"[argmax] B={B} V={V}")
+        x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+        if V >= 7:
+            x[0] = np.round(x[0])                          # ties everywhere
+            x[1, :] = -np.inf                              # all -inf: 0
+            x[2, 0] = np.nan                               # NaN at 0: 0
+            x[3, rng.choice(V, 3, replace=False)] = np.nan  # NaN elsewhere: skipped
+            x[4, :] = np.nan                               # NaN only: 0
+            x[5, :] = 0.0
+            x[5, V // 2] = -0.0                            # +0 and -0 tie: the first
+            x[6, :] = -np.inf
+            x[6, V - 1] = -1e30                            # the last element
+            if B > 8:
+                x[7, rng.choice(V, min(V, 20), replace=False)] = np.float32(50.0)  # equal maxima
+                x[8, :] = np.float32(3.0)
+                x[8, 0] = -np.inf                          # from -inf at 0 up
+        got = pkg.argmax_device(torch.from_numpy(x).cuda()).cpu().numpy()
+        want = np.array([ref(x[b]) for b in range(B)])
+        assert np.array_equal(got, want), (B, V, np.flatnonzero(got != want)[:8])
+    # an empty row answers 0, as the reference's loop never runs
+    got = pkg.argmax_device(torch.zeros((3, 0), dtype=torch.float32, device="cuda")).cpu().numpy()
+    assert got.tolist() == [0, 0, 0]
+    # the host-sequence form
+    assert pkg.argmax([1.0, 3.0, 3.0, -2.0]) == 1

@@ -1,6 +1,8 @@
 """nls_sample_host_noalloc (no counterpart in the reference): the
 allocation-free variant of nls_sample_host, checked through the C ABI against
-nls_sample_host on the same inputs, two calls in a row, the second smaller."""
+nls_sample_host on the same inputs, two calls in a row, the second smaller,
+and with the device's free memory unchanged across its calls (the first call
+after nls_create included)."""
 import ctypes
 import sys
 
@@ -51,16 +53,25 @@ def test_sample_host_noalloc_matches_sample_host(pkg):
         hist = rng.integers(0, V, size=(B, 200))
         h_ref, h_na = _handles(pkg, B, V, 77 + call, hist)
         try:
+            free0 = None
             for step in range(3):
                 x = np.ascontiguousarray(rng.standard_normal((B, V)).astype(np.float32) * 2.5)
                 xp = x.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
                 want = np.zeros(B, dtype=np.int64)
                 got = np.full(B, -7, dtype=np.int64)
+                # (the reference call's first run allocates its own buffers and
+                # loads the kernels, before the free memory is read)
                 pkg.check(L.nls_sample_host(h_ref, xp, want.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))),
                           "nls_sample_host")
+                torch.cuda.synchronize()
+                if free0 is None:
+                    free0 = torch.cuda.mem_get_info()[0]
                 pkg.check(L.nls_sample_host_noalloc(h_na, xp, got.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))),
                           "nls_sample_host_noalloc")
                 assert np.array_equal(got, want), (call, step, got, want)
+            torch.cuda.synchronize()
+            free1 = torch.cuda.mem_get_info()[0]
+            assert free1 == free0, (call, free0, free1)
         finally:
             L.nls_destroy(h_ref)
             L.nls_destroy(h_na)
