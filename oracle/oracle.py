@@ -16,7 +16,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libnls_oracle.so")
+# NLS_ORACLE_LIB names another build of the same sources (the sanitizer build)
+LIB_PATH = os.environ.get("NLS_ORACLE_LIB") or os.path.join(HERE, "libnls_oracle.so")
 
 EXPF_LIBM = 0
 EXPF_CR = 1

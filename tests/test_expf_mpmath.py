@@ -31,6 +31,8 @@ import oracle as O  # noqa: E402
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 FLAGS = ["-O2", "-ffp-contract=off", "-fno-fast-math", "-std=c++17", "-Wall"]
+if os.environ.get("NLS_SANITIZE") == "1":  # the sanitizer run (tests/test_runs_cpu.py)
+    FLAGS = FLAGS + ["-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-g"]
 PREC = 256
 
 

@@ -26,6 +26,12 @@ import oracle as O
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 FLAGS = ["-O2", "-ffp-contract=off", "-fno-fast-math", "-std=c++17", "-Wall"]
+# AddressSanitizer + UndefinedBehaviorSanitizer: every check below also runs
+# built with these (test_sanitized_checks), so an out-of-bounds table index
+# or an undefined shift in the device logic fails the CPU suite
+SANFLAGS = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-fno-omit-frame-pointer", "-g"]
+if os.environ.get("NLS_SANITIZE") == "1":
+    FLAGS = FLAGS + SANFLAGS
 
 
 @pytest.fixture(scope="module")
@@ -121,3 +127,44 @@ def test_group_walk_matches_oracle_sort_path(built):
             done += 1
     # rows whose cutoffs end inside the groups never need the whole row
     assert done >= 100, (done, need_all)
+
+
+def _san_runtime():
+    libs = []
+    for name in ("libasan.so", "libubsan.so"):
+        p = subprocess.run(["gcc", "-print-file-name=" + name], capture_output=True, text=True).stdout.strip()
+        if not os.path.isabs(p) or not os.path.exists(p):
+            pytest.skip(f"no {name} for gcc")
+        libs.append(p)
+    return " ".join(libs)
+
+
+@pytest.mark.skipif(os.environ.get("NLS_SANITIZE") == "1", reason="runs the sanitized build itself")
+def test_sanitized_checks(tmp_path):
+    """runs_check, seqsum_check and exp64_check built with ASan + UBSan and
+    run; then, in a child interpreter with the sanitizer runtime preloaded and
+    the oracle's sanitizer build (oracle/Makefile `asan`), this file's checks
+    (the group walk of grouped_check.cpp among them), the oracle's pins, the
+    LM head oracle's pins and the correctly rounded exp's mpmath check
+    (expf_cr_check.cpp), each C/C++ part built with the same flags."""
+    import sys
+
+    for name, args, want in (("runs_check", ["3000"], "0 failures"),
+                             ("seqsum_check", [], "all sums bit-identical"),
+                             ("exp64_check", [], "0 failures")):
+        exe = str(tmp_path / (name + "_san"))
+        subprocess.run(["g++", *FLAGS, *SANFLAGS, "-o", exe, os.path.join(HERE, name + ".cpp"), "-lm"],
+                       check=True)
+        r = subprocess.run([exe, *args], capture_output=True, text=True, timeout=300)
+        assert r.returncode == 0 and want in r.stdout, (name, r.stdout[-2000:], r.stderr[-4000:])
+    so = str(tmp_path / "libnls_oracle_asan.so")
+    subprocess.run(["make", "-s", "-C", os.path.join(os.path.dirname(HERE), "oracle"), "asan",
+                    "ASAN_OUT=" + so], check=True)
+    env = dict(os.environ, LD_PRELOAD=_san_runtime(), ASAN_OPTIONS="detect_leaks=0",
+               NLS_SANITIZE="1", NLS_ORACLE_LIB=so)
+    files = ["test_runs_cpu.py", "test_oracle.py", "test_lmhead_oracle.py", "test_expf_mpmath.py"]
+    r = subprocess.run([sys.executable, "-m", "pytest", "-q", "-p", "no:cacheprovider", "-m", "not gpu",
+                        *[os.path.join(HERE, f) for f in files]],
+                       capture_output=True, text=True, timeout=900, env=env, cwd=os.path.dirname(HERE))
+    assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-4000:]
+    assert " passed" in r.stdout and " failed" not in r.stdout, r.stdout[-2000:]
