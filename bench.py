@@ -30,6 +30,7 @@ import json
 import math
 import os
 import platform
+import subprocess
 import sys
 import time
 
@@ -637,27 +638,171 @@ def bench_sample_host(args):
            "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": med / 1e3,
            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
            "data": "synthetic (seeded numpy logits in host memory, one blocking call at a time)",
-           "config": {"workload": args.workload, "B": B, "V": V}, "calls": times,
+           "config": {"workload": workloads.describe(args.workload, B, V), "B": B, "V": V}, "calls": times,
            "cpu_baseline": {"value": cpu_us, "unit": "us per call", "cores": 1, "kind": "port",
                             "sample": f"median of the same {B}-row call on one thread; C restatement of "
                                       "src/nimllm/sampler.nim:59-121 (libm expf)"}}
     print(json.dumps(res), flush=True)
 
 
-def phase_stamps(args):
-    """Per-phase wall-clock of the k64 kernel on the workload, from the
-    `phases` build of the library (make -C nim.llm_amd/csrc phases):
-    medians over the rows' workgroups of the time each phase took, for the
-    last of a run of back-to-back calls."""
+def bench_decode_chain(args):
+    """One decode step's tail on the device, per token, at the output shape of
+    --lm-rows x --lm-cols (--lm-type; Llama-3.2-1B's 128256 x 2048 by
+    default): the normalised hidden state from host memory to the device,
+    the output projection (nls_lm_head, model.nim:470), the sampler
+    (nls_sample, chat.nim:205) writing the id into pinned host memory, and one
+    synchronisation -- beside the CPU restatement's matmul + sample of the same
+    step.  Also timed: the same chain with the acceptance on the device
+    (nls_generate_step, chat.nim:205-208) and the id copied back."""
     import ctypes
+
     import numpy as np
     import torch
 
     pkg = load_pkg()
+    from nimllm_amd import workloads
+
+    L = pkg.lib()
+    t = workloads.LM_TYPE_NAMES[args.lm_type]
+    rows, cols = args.lm_rows, args.lm_cols
+    w_np = workloads.make_lm_weights(t, rows, cols, seed=args.seed)
+    xs = workloads.make_lm_hidden(args.steps + args.warmup + 1, cols, seed=args.seed)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    nbuf = max(2, math.ceil(640e6 / w_np.nbytes))
+    base = torch.from_numpy(w_np).to(dev)
+    bufs = [base] + [base.clone() for _ in range(nbuf - 1)]
+    x_pin = torch.empty(cols, dtype=torch.float32).pin_memory()
+    x_dev = torch.empty((1, cols), dtype=torch.float32, device=dev)
+    y = torch.empty((1, rows), dtype=torch.float32, device=dev)
+    work = torch.empty(max(1, pkg.lm_head_workspace(t, cols, 1, 0, False)), dtype=torch.uint8, device=dev)
+    id_pin = torch.zeros(1, dtype=torch.int32).pin_memory()
+    params = pkg.defaultSampling()
+    params.seed = args.seed
+    hist = np.arange(64, dtype=np.int64).reshape(1, 64) * 997 % rows
+    s = pkg.BatchSampler([params], rows, stream=stream)
+    s.accept(hist)
+    d_id = torch.empty(1, dtype=torch.int32, device=dev)
+    eog = torch.tensor([rows + 1], dtype=torch.int32, device=dev)  # no end-of-generation id is drawn
+    done = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step(i, accept):
+        x_pin.numpy()[:] = xs[i]
+        x_dev.copy_(x_pin.reshape(1, cols), non_blocking=True)
+        pkg.lm_head(bufs[i % nbuf], t, rows, cols, x_dev, out=y, work=work)
+        if accept:
+            s.generate_step(y, eog, done, out=d_id)
+            id_pin.copy_(d_id, non_blocking=True)
+            stream.synchronize()
+        else:
+            pkg.check(L.nls_sample(s._h, ctypes.c_void_p(y.data_ptr()), None,
+                                   ctypes.c_void_p(id_pin.data_ptr()), None), "nls_sample")
+            s.synchronize()
+        return int(id_pin.numpy()[0])
+
+    # parity: the first step's id against the oracle's matmul + sample with the
+    # same first uniform of initRand(seed)
+    first = step(0, False)
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    logits = O.matmul(t, w_np, rows, cols, xs[0:1])[0]
+    op = O.make_params(temperature=params.temperature, topK=params.topK, topP=params.topP, minP=params.minP,
+                       repeatPenalty=params.repeatPenalty, repeatLastN=params.repeatLastN,
+                       presencePenalty=params.presencePenalty, frequencyPenalty=params.frequencyPenalty,
+                       seed=params.seed)
+    res, _, _, _ = O.sample(op, logits, hist[0], {}, float(O.uniforms(args.seed, 1)[0]), O.EXPF_CR,
+                            want_cand=False)
+    parity = first == res.id
+
+    def timed(accept):
+        for i in range(args.warmup):
+            step(1 + i, accept)
+        ts = []
+        for i in range(args.steps):
+            t0 = time.perf_counter()
+            step(1 + args.warmup + i, accept)
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        return {"median_us": ts[len(ts) // 2] * 1e6, "p10_us": ts[len(ts) // 10] * 1e6,
+                "p90_us": ts[(9 * len(ts)) // 10] * 1e6}
+
+    sample_only = timed(False)
+    with_accept = timed(True)
+    s.close()
+    med = sample_only["median_us"]
+    res_line = {
+        "metric": f"decode-step tail per token: hidden state in, {rows} x {cols} {args.lm_type} output "
+                  "projection, sampler, id out (us per token)",
+        "value": med, "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": med / 1e3, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 x int8 -> int32, fp32 terms; f32 sampler",
+        "data": f"synthetic GGUF rows rotated over {nbuf} copies; one fresh hidden state per step",
+        "config": {"workload": f"decode tail at the Llama-3.2-1B output shape {rows} x {cols} {args.lm_type}, "
+                               "B=1, defaultSampling (T 0.7, top-k 40, top-p 0.95, min-p 0.05, repeat "
+                               "penalty 1.1 over the last 64 ids)", "rows": rows, "cols": cols},
+        "chain": {"sample_id_to_pinned_host": sample_only, "generate_step_id_copied_back": with_accept},
+        "parity_first_step": {"bit_exact_id": bool(parity), "id": first, "oracle_id": int(res.id)},
+    }
+    if not args.no_cpu_baseline:
+        def cpu_step(nthreads):
+            import threading
+
+            t0 = time.perf_counter()
+            out = np.zeros((1, rows), np.float32)
+            bounds = [rows * k // nthreads for k in range(nthreads + 1)]
+
+            def worker(k):
+                out[:, bounds[k]:bounds[k + 1]] = O.matmul(t, w_np, rows, cols, xs[1:2], first=bounds[k],
+                                                           last=bounds[k + 1])[:, bounds[k]:bounds[k + 1]]
+            ths = [threading.Thread(target=worker, args=(k,)) for k in range(nthreads)]
+            for th in ths:
+                th.start()
+            for th in ths:
+                th.join()
+            t1 = time.perf_counter()
+            O.sample(op, out[0], hist[0], {}, 0.5, O.EXPF_LIBM, want_cand=False)
+            t2 = time.perf_counter()
+            return (t2 - t0) * 1e6, (t2 - t1) * 1e6
+
+        nt = host_cores()
+        reps = [cpu_step(nt) for _ in range(3)]
+        tot = sorted(r[0] for r in reps)[1]
+        smp = sorted(r[1] for r in reps)[1]
+        one = cpu_step(1)
+        res_line["cpu_baseline"] = {"value": one[0], "unit": "us per token", "cores": 1, "kind": "port",
+                                    "sample": f"one step on one thread (matmul {one[0] - one[1]:.0f} us + sample "
+                                              f"{one[1]:.0f} us); C restatement of model.nim:144-200 and "
+                                              "sampler.nim:59-121"}
+        res_line["cpu_baseline_all_cores"] = {"value": tot, "unit": "us per token", "cores": nt, "kind": "port",
+                                              "sample": f"median of 3 steps, matmul over {nt} threads (row "
+                                                        f"ranges, as parallelFor splits them), sample "
+                                                        f"{smp:.0f} us on one"}
+    else:
+        res_line["cpu_baseline"] = None
+    print(json.dumps(res_line), flush=True)
+
+
+def phase_stamps(args):
+    """Per-phase wall-clock of the k64 kernel on the workload, from the
+    `phases` build of the library, which this builds from the sources first
+    (make -C nim.llm_amd/csrc phases: only what changed is rebuilt): medians
+    over the rows' workgroups of the time each phase took, for the last of a
+    run of back-to-back calls.  The output names the sources' hash."""
+    import ctypes
+    import numpy as np
+    import torch
+
+    import glob
+
     path = os.path.join(PKG_DIR, "libnimllm_sampler_phases.so")
-    if not os.path.exists(path):
-        raise SystemExit(f"{path} is missing: make -C nim.llm_amd/csrc phases")
+    newest = max(os.path.getmtime(f) for pat in SOURCE_GLOBS for f in glob.glob(os.path.join(ROOT, pat)))
+    if not os.path.exists(path) or os.path.getmtime(path) < newest:
+        subprocess.run(["make", "-s", "-j16", "-C", os.path.join(PKG_DIR, "csrc"), "phases"], check=True,
+                       stdout=subprocess.DEVNULL)
+    pkg = load_pkg()
     pkg.LIB_PATH = path
+    print(f"# sources: source_hash {source_hash()} (the phases build of these sources)")
     L = pkg.lib()
     from nimllm_amd import workloads
 
@@ -685,7 +830,46 @@ def phase_stamps(args):
     if L.nls_generic_stamps(buf.ctypes.data_as(ctypes.c_void_p)) != 0:
         raise SystemExit("nls_generic_stamps failed")
     G = buf.reshape(4096, 16)[:w.B].astype(np.int64).copy()
+    plan, _ = s.plan()
     s.close()
+    if not plan.k64:
+        # stream_kernel rows (each instance's unit keeps its own stamps): 0
+        # start, 1 stream start, 2 stream end, 3 members start, 4 members
+        # done, 5 tail start, 6 tail done; 12 candidates, 13 threshold
+        # refreshes, 14 their ticks, 15 tiles
+        vec = "true" if w.V % 4 == 0 else "false"
+        fn = getattr(L, f"nls_stream_stamps_{plan.stream_threads}_{vec}")
+        buf[:] = 0
+        if fn(buf.ctypes.data_as(ctypes.c_void_p)) != 0:
+            raise SystemExit("nls_stream_stamps failed")
+        P = buf.reshape(4096, 16)[:w.B].astype(np.int64).copy()
+        ok = (P[:, 0] > 0) & (P[:, 6] > 0)
+        if not ok.any():
+            print(f"# no stream_kernel rows with every stamp in workload {args.workload}")
+            return
+        us = lambda d: d / 100.0  # 100 MHz counter
+        t0 = P[ok, 0].min()
+        rows = {"workgroup start after the first": us(P[:, 0] - t0),
+                "prologue: row constants, patch table": us(P[:, 1] - P[:, 0]),
+                "stream": us(P[:, 2] - P[:, 1]),
+                "  of which threshold refreshes": us(P[:, 14]),
+                "patched values, candidates": us(P[:, 3] - P[:, 2]),
+                "heap-rule members": us(P[:, 4] - P[:, 3]),
+                "sort of the members": us(P[:, 5] - P[:, 4]),
+                "tail: softmax, top-p, min-p, draw": us(P[:, 6] - P[:, 5]),
+                "workgroup total": us(P[:, 6] - P[:, 0])}
+        print(f"# stream_kernel phases, workload {args.workload} (B={w.B} V={w.V}), last of {args.steps} calls; "
+              f"{int(ok.sum())} rows with every stamp")
+        print("| Phase | median us | p10 | p90 |")
+        print("|---|---|---|---|")
+        for name, v in rows.items():
+            v = v[ok]
+            print(f"| {name} | {np.median(v):.2f} | {np.percentile(v, 10):.2f} | {np.percentile(v, 90):.2f} |")
+        print(f"per row (median / p90): tiles {np.median(P[ok, 15]):.0f} / {np.percentile(P[ok, 15], 90):.0f}; "
+              f"threshold refreshes {np.median(P[ok, 13]):.0f} / {np.percentile(P[ok, 13], 90):.0f}; "
+              f"candidates {np.median(P[ok, 12]):.0f} / {np.percentile(P[ok, 12], 90):.0f}")
+        print(f"kernel span (first start to last end): {us(P[ok, 6].max() - t0):.2f} us")
+        return
     gok = (G[:, 0] > 0) & (G[:, 7] > 0)
     if gok.any():
         g0 = G[gok, 0].min()
@@ -807,6 +991,9 @@ def main():
     ap.add_argument("--lm-cols", type=int, default=2048)
     ap.add_argument("--lm-nb", type=int, default=1)
     ap.add_argument("--lm-exact", action="store_true", help="exactMatmul: the float path")
+    ap.add_argument("--decode-chain", action="store_true",
+                    help="time one decode step's tail per token: hidden state in, nls_lm_head, nls_sample, "
+                         "id out (B = 1, the --lm-* output shape)")
     ap.add_argument("--lib", default="",
                     help="time this build of the library instead of nim.llm_amd/libnimllm_sampler.so")
     ap.add_argument("--phase-stamps", action="store_true",
@@ -833,6 +1020,8 @@ def main():
         return bench_sample_host(args)
     if args.lm_head:
         return bench_lm_head(args)
+    if args.decode_chain:
+        return bench_decode_chain(args)
     import numpy as np
     import torch
 
@@ -954,11 +1143,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded numpy; logits resident in HBM, rotated over "
                 f"{nbuf} buffers = {nbuf * row_bytes / 1e6:.0f} MB to defeat the Infinity Cache)",
-        "config": {"workload": f"{args.workload}: B={B} x V={V} fp32 logits N(0, 2.5^2); "
-                               "frequency 0.5 / presence 0.3 over 1024 Zipf(1.2) history ids; "
-                               "50 bias ids per row (5 at -inf); top-k 50, top-p 0.95, T 1.0"
-                   if args.workload == "headline" else args.workload,
-                   "B": B, "V": V, "seed": args.seed},
+        "config": {"workload": workloads.describe(args.workload, B, V), "B": B, "V": V, "seed": args.seed},
         "roofline": {"bound": "hbm", "achieved": dk["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": dk["frac"], "traffic": dk["traffic"],
                      "kernel": dom, "kernel_avg_us": dk["avg_us"], "kernel_avg_from": dk["avg_from"],

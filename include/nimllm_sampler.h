@@ -157,8 +157,13 @@ int nls_sample(nls_sampler* s, const float* d_logits, const double* d_u, int32_t
                const nls_debug* dbg);
 
 /* Blocking convenience for host-resident logits (a CPU model's output):
- * copies h_logits [batch x vocab] to the device, samples with the rows' own
- * RNGs and returns the ids in h_out [batch]. */
+ * samples h_logits [batch x vocab] with the rows' own RNGs and returns the
+ * ids in h_out [batch] -- `s.sample(logits)` of sampler.nim:59 for a CPU
+ * model.  The first call allocates a pinned host staging area (hipHostMalloc)
+ * held by the handle; each call copies the logits there, and up to 8 MiB of
+ * logits the kernels read them from it directly (larger batches go to device
+ * memory first); the kernels write the ids back there, and one stream
+ * synchronisation ends the call. */
 int nls_sample_host(nls_sampler* s, const float* h_logits, int64_t* h_out);
 
 /* No counterpart in the reference: nls_sample_host for callers that cannot

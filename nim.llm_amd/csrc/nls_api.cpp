@@ -182,6 +182,11 @@ struct nls_sampler {
   std::vector<int32_t> h_stage;
   float* tmp_logits = nullptr;
   int32_t* tmp_out = nullptr;
+  // nls_sample_host's pinned staging (hipHostMalloc, set up by its first
+  // call): the logits and, 256 bytes on, the int32 ids; host_stage_dev is the
+  // same memory as the device sees it
+  unsigned char* host_stage = nullptr;
+  unsigned char* host_stage_dev = nullptr;
   hipEvent_t prof_start = nullptr;
   hipEvent_t prof_stop = nullptr;
   hipEvent_t prof_gstart = nullptr;
@@ -207,6 +212,7 @@ struct nls_sampler {
     dfree(stage_ids);
     dfree(tmp_logits);
     dfree(tmp_out);
+    if (host_stage) (void)hipHostFree(host_stage);
   }
 
   // True when a row the streaming kernel runs may patch more distinct ids
@@ -958,19 +964,49 @@ int nls_get_plan(const nls_sampler* s, nls_plan* out, int32_t* row_streamed) {
   return NLS_OK;
 }
 
+// Up to this many bytes of logits, nls_sample_host's kernels read them
+// straight from the pinned staging (one transfer fewer in a call's chain of
+// latencies); larger batches are copied to device memory first.
+constexpr size_t kHostDirectBytes = size_t{8} << 20;
+
 int nls_sample_host(nls_sampler* s, const float* h_logits, int64_t* h_out) {
   if (!s || !h_logits || !h_out) return NLS_ERR_INVALID_ARGUMENT;
   const size_t n = (size_t)s->B * s->V;
+  const size_t ids_off = (n * 4 + 255) & ~(size_t)255;
   int rc;
-  if (!s->tmp_logits && (rc = dalloc(&s->tmp_logits, n))) return rc;
-  if (!s->tmp_out && (rc = dalloc(&s->tmp_out, (size_t)s->B))) return rc;
-  NLS_HIP(hipMemcpyAsync(s->tmp_logits, h_logits, n * 4, hipMemcpyHostToDevice, s->stream));
-  rc = nls_sample(s, s->tmp_logits, nullptr, s->tmp_out, nullptr);
-  if (rc) return rc;
-  std::vector<int32_t> o(s->B);
-  NLS_HIP(hipMemcpyAsync(o.data(), s->tmp_out, (size_t)s->B * 4, hipMemcpyDeviceToHost, s->stream));
+  if (!s->host_stage) {
+    void* h = nullptr;
+    void* d = nullptr;
+    NLS_HIP(hipHostMalloc(&h, ids_off + (size_t)s->B * 4, hipHostMallocDefault));
+    const hipError_t e = hipHostGetDevicePointer(&d, h, 0);
+    if (e != hipSuccess) {
+      (void)hipHostFree(h);
+      return hip_fail(e, "hipHostGetDevicePointer");
+    }
+    s->host_stage = static_cast<unsigned char*>(h);
+    s->host_stage_dev = static_cast<unsigned char*>(d);
+  }
+  // the previous call ended with a synchronisation: the staging is free
+  std::memcpy(s->host_stage, h_logits, n * 4);
+  const float* d_logits = reinterpret_cast<const float*>(s->host_stage_dev);
+  if (n * 4 > kHostDirectBytes) {
+    if (!s->tmp_logits && (rc = dalloc(&s->tmp_logits, n))) return rc;
+    NLS_HIP(hipMemcpyAsync(s->tmp_logits, s->host_stage, n * 4, hipMemcpyHostToDevice, s->stream));
+    d_logits = s->tmp_logits;
+  }
+  // the ids are written by the kernel into the pinned staging
+  rc = nls_sample(s, d_logits, nullptr, reinterpret_cast<int32_t*>(s->host_stage_dev + ids_off), nullptr);
+  if (rc) {
+    // a kernel of the failed call may still read the staging
+    (void)hipStreamSynchronize(s->stream);
+    return rc;
+  }
   NLS_HIP(hipStreamSynchronize(s->stream));
-  for (int b = 0; b < s->B; ++b) h_out[b] = o[b];
+  for (int b = 0; b < s->B; ++b) {
+    int32_t v;
+    std::memcpy(&v, s->host_stage + ids_off + (size_t)4 * b, sizeof v);
+    h_out[b] = v;
+  }
   return NLS_OK;
 }
 

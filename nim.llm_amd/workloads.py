@@ -144,6 +144,27 @@ def _zipf_ids(rng, n, V, a=1.2):
     return perm[(z - 1) % V].astype(np.int64)
 
 
+_PENALTY_ROWS = ("fp32 logits N(0, 2.5^2); frequency 0.5 / presence 0.3 over 1024 Zipf(1.2) history ids; "
+                 "50 bias ids per row (5 at -inf); top-k 50, top-p 0.95, T 1.0")
+DESCRIPTIONS = {
+    "single_32k": "fp32 logits N(0, 3^2); top-k 40, top-p 0.95, T 0.8; no history, no bias",
+    "zipf_minp_128k": ("fp32 logits N(0, 1) - 4.4 ln(rank), a random rank per id (Zipf head); "
+                       "full sort (k = 0), top-p 0.9, min-p 0.05, T 0.7; repeat penalty 1.1 over "
+                       "256 uniform history ids"),
+    "penalties_152k": _PENALTY_ROWS,
+    "headline": _PENALTY_ROWS,
+    "flat_topk1000": "fp32 logits N(0, 1); top-k 1000, top-p 0.99, T 1.2; no history, no bias",
+    "mixed_ties_152k": ("fp32 logits round(4 N(0, 8^2)) / 4 (heavy ties); each row at random greedy, "
+                        "full sort with min-p 0.1, top-k 20, or full sort with top-p 0.8 (T 1.0); "
+                        "repeat penalty 1.05 over 512 uniform history ids"),
+}
+
+
+def describe(name: str, B: int, V: int) -> str:
+    """The workload's full description, as the benchmark reports it."""
+    return f"{name}: B={B} x V={V} {DESCRIPTIONS[name]}"
+
+
 def make(name: str, seed: int = 1234, B: int | None = None, V: int | None = None) -> Workload:
     B0, V0 = SHAPES[name]
     B = B0 if B is None else B
