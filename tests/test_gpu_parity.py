@@ -839,6 +839,29 @@ def test_sample_host_and_single_row_sampler(pkg, torch):
         hist.append(got)
 
 
+@pytest.mark.parametrize("B,V", [(3, 50000), (40, 128256)])
+def test_sample_host_batches_both_sides_of_the_direct_limit(pkg, torch, B, V):
+    """nls_sample_host on batches whose logits the kernel reads from the pinned
+    staging directly (3 x 50000: 0.6 MB) and ones copied to device memory
+    first (40 x 128256: 20.5 MB, above 8 MiB), three calls in a row on one
+    handle, every id against the oracle with the rows' own RNG streams."""
+    rng = np.random.default_rng(B)
+    say(f"[sample_host_batches] B={B} V={V}")
+    plist = [dict(temperature=0.8, topK=[40, 0, 300, 1][b % 4], topP=0.95, minP=0.0, repeatPenalty=1.0,
+                  repeatLastN=0, presencePenalty=0.0, frequencyPenalty=0.0, seed=100 + b) for b in range(B)]
+    s = pkg.BatchSampler([to_pkg_params(pkg, p, {}) for p in plist], V)
+    try:
+        us = [O.uniforms(100 + b, 3) for b in range(B)]
+        for call in range(3):
+            x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
+            got = s.sample_host(x)
+            want = O.sample_batch([O.make_params(**p) for p in plist], x, None, None, None, None, None,
+                                  np.array([us[b][call] for b in range(B)]), O.EXPF_CR, nthreads=8)
+            assert np.array_equal(got, want), (B, V, call, np.flatnonzero(got != want)[:8])
+    finally:
+        s.close()
+
+
 def test_expf_exhaustive_checksum(pkg, torch):
     """Every binary32 input in (-104, 89) through the device exp; the order-free
     checksum must equal the one of the correctly rounded results computed on
