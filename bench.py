@@ -168,6 +168,38 @@ def traffic_summary(args):
     print("\n".join(lines))
 
 
+def trace_summary(args):
+    """Per-kernel launch durations from a rocprofv3 --kernel-trace run of this
+    script (the kernel_trace.csv under --trace-dir): every launch but each
+    kernel's first --skip (the parity check and the warmup, whose first
+    launches run cold), as median, mean, 10th and 90th percentile.  Prints
+    one JSON line."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    files = glob.glob(os.path.join(args.trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no kernel_trace.csv under {args.trace_dir}")
+    runs = defaultdict(list)
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                name = r["Kernel_Name"]
+                runs[name].append((int(r["Dispatch_Id"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    out = {}
+    for name, v in runs.items():
+        if "copyBuffer" in name or "fillBuffer" in name or name.startswith("at::") or "at::native" in name:
+            continue
+        v.sort()
+        d = sorted(x for _, x in v[args.skip:]) or sorted(x for _, x in v)
+        n = len(d)
+        short = name.split("(")[0].replace("void ", "").replace("nls::", "")
+        out[short] = {"launches": len(v), "kept": n, "median_us": d[n // 2], "mean_us": sum(d) / n,
+                      "p10_us": d[n // 10], "p90_us": d[(9 * n) // 10]}
+    print(json.dumps({"workload": args.workload, "skip": args.skip, "kernels": out}), flush=True)
+
+
 def copy_ref(dev):
     """A plain 256 MiB device copy, three times: the kernel of known size that
     scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes."""
@@ -980,6 +1012,11 @@ def main():
     ap.add_argument("--traffic-summary", action="store_true",
                     help="write the per-kernel traffic summary from two rocprofv3 --pmc runs "
                          "(--fetch-dir, --write-dir) to --out; no GPU needed")
+    ap.add_argument("--trace-summary", action="store_true",
+                    help="per-kernel launch durations (median, mean, p10, p90, skipping each kernel's "
+                         "first --skip launches) from a rocprofv3 --kernel-trace run (--trace-dir); no GPU needed")
+    ap.add_argument("--trace-dir")
+    ap.add_argument("--skip", type=int, default=6)
     ap.add_argument("--fetch-dir")
     ap.add_argument("--write-dir")
     ap.add_argument("--out")
@@ -1003,6 +1040,8 @@ def main():
         load_pkg().LIB_PATH = os.path.abspath(args.lib)
     if args.traffic_summary:
         return traffic_summary(args)
+    if args.trace_summary:
+        return trace_summary(args)
     if args.phase_stamps:
         return phase_stamps(args)
     if args.gpus != 1:
