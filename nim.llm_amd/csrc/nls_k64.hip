@@ -262,6 +262,7 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
   __shared__ int s_nf;                         // entries in the candidate list
   __shared__ int s_rank[kK64RankCap];          // each candidate's rank, summed over four threads
   __shared__ int s_mcnt;                       // members placed by the workgroup select
+  __shared__ uint32_t s_key_k;                 // the key of rank k (the entry just past the k-th)
   __shared__ __align__(16) uint64_t s_flist[kWave];  // the last wave's candidates above its bound
   __shared__ __align__(16) float s_chain[kWave];     // the tail's chains
   __shared__ int s_npl;                        // listed patched slots
@@ -1009,6 +1010,7 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
     if (rank_ok && tid < N) {
       const int r = s_rank[tid];
       if (r < kWave) s_flist[r] = cand[tid];
+      if (r == k) s_key_k = (uint32_t)(cand[tid] >> 32);  // (ranks run over 0..N-1)
     }
     // A list longer than the rank table (a flat top of the row: many values
     // near the k-th): the heap rule's k members by a workgroup radix select
@@ -1033,7 +1035,10 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
       const int nl = min(N, kWave);  // s_flist[0..nl) holds ranks 0..nl-1
       x = lane < nl ? s_flist[lane] : 0ull;
       const uint32_t T = (uint32_t)__builtin_amdgcn_readlane((int)(x >> 32), kk - 1);
-      const bool excess = N > kk && kk < kWave && (uint32_t)__builtin_amdgcn_readlane((int)(x >> 32), kk) == T;
+      // ties at the k-th key beyond k: the key of rank k (held in the wave
+      // for k < 64, else read from LDS) equals it
+      const uint32_t key_k = kk < kWave ? (uint32_t)__builtin_amdgcn_readlane((int)(x >> 32), kk) : s_key_k;
+      const bool excess = N > kk && key_k == T;
       if (excess) {
         const uint32_t kx = (uint32_t)(x >> 32);
         const int ge = (int)__popcll(__ballot(lane < nl && kx >= T));

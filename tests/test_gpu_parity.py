@@ -120,6 +120,66 @@ def test_small_random_rows(pkg, torch, V):
     compare_rows(x, plist, [list(h) for h in hist], biases, u, ids, dbg, f"V={V}")
 
 
+SWEEP = {
+    # name: (B, V, top-k choices, offset of the logits in floats)
+    "k64_rows": (300, 50000, (0, 1, 20, 64), 0),
+    "k64_rows_odd_vocab": (300, 50001, (0, 1, 20, 64), 0),
+    "k64_rows_unaligned": (280, 40000, (0, 5, 40), 1),
+    "k64_k_is_64_all_tied": (260, 20000, (64, 63, 62), 0),
+    "split_rows": (40, 100000, (0, 1, 20, 50), 0),
+    "split_rows_unaligned": (40, 100000, (0, 3, 64), 3),
+    "block_path_two_per_cu": (600, 30000, (65, 100, 300, 600), 0),
+    "whole_row_mix": (24, 70000, (0, 20, 1000, 3000), 0),
+    "small_rows_every_k": (16, 3000, (0, 1, 2999, 3000, 4000), 2),
+}
+
+
+@pytest.mark.parametrize("name", list(SWEEP))
+def test_random_batches_every_path(pkg, torch, name):
+    """Random batches over the planner's paths -- one workgroup per row
+    (k64_kernel), rows split over workgroups, the k > 64 block path with two
+    workgroups per CU, whole-row rows mixed in -- with vocabularies that are
+    not a multiple of 4 and logits that are not 16-byte aligned (4-byte
+    loads), random temperatures, top-k, top-p, min-p, penalties over
+    histories with out-of-range ids, and bias lists with -inf: every row's
+    id, n, total, candidates and probabilities against the oracle
+    (sampler.nim:59-121)."""
+    B, V, ks, off = SWEEP[name]
+    rng = np.random.default_rng(abs(sum(map(ord, name))))
+    say(f"[random_sweep] {name}: B={B} V={V} offset={off}")
+    x = (rng.standard_normal((B, V)) * rng.choice([1.0, 2.5, 4.0])).astype(np.float32)
+    nt = B if "tied" in name else B // 4  # rows on a 0.25 grid: ties at every cut
+    x[:nt] = (np.round(x[:nt] * 4.0) / 4.0).astype(np.float32)
+    plist, biases = [], []
+    for b in range(B):
+        p = rand_params(rng, V)
+        if p["temperature"] > 0:
+            p["topK"] = int(rng.choice(ks))
+        plist.append(p)
+        nb = int(rng.integers(0, min(V, 8) + 1))
+        ids = rng.choice(V, size=nb, replace=False) if nb else []
+        biases.append({int(i): float(rng.choice([-math.inf, -3.0, 0.5, 4.0])) for i in ids})
+    H = 96
+    hist = rng.integers(-3, V + 3, size=(B, H)).astype(np.int64)
+    u = rng.random(B)
+    u[:3] = [0.0, 1.0 - 2.0 ** -53, 0.5]
+    params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
+    s = pkg.BatchSampler(params, V)
+    try:
+        s.accept(hist)
+        flat = torch.zeros(B * V + off, dtype=torch.float32, device="cuda")
+        flat[off:] = torch.from_numpy(x.reshape(-1)).cuda()
+        d = flat[off:].view(B, V)
+        assert (d.data_ptr() % 16 == 0) == (off % 4 == 0)
+        ids, dbg = s.sample(d, torch.from_numpy(u).cuda(), debug_cap=64)
+        torch.cuda.synchronize()
+        ids = ids.cpu().numpy()
+        dbg = {k: v.cpu().numpy() for k, v in dbg.items()}
+    finally:
+        s.close()
+    compare_rows(x, plist, [list(h) for h in hist], biases, u, ids, dbg, name)
+
+
 def patch_designs(rng, x):
     """Rows whose penalised or biased ids fall below the threshold, rise above
     it, or sit on it (sampler.nim:64-76): one design per row, cycling."""
