@@ -131,7 +131,33 @@ SWEEP = {
     "block_path_two_per_cu": (600, 30000, (65, 100, 300, 600), 0),
     "whole_row_mix": (24, 70000, (0, 20, 1000, 3000), 0),
     "small_rows_every_k": (16, 3000, (0, 1, 2999, 3000, 4000), 2),
+    "split_rows_tied": (40, 100000, (64, 63, 33), 0),
+    "block_path_tied": (600, 30000, (65, 128, 1000), 0),
+    "whole_row_tied": (24, 70000, (0, 1024, 2048, 2049), 1),
+    "one_row_tied": (1, 32000, (64,), 0),
+    "one_row_large_tied": (1, 151936, (50,), 2),
+    "few_rows_tied": (3, 128256, (0, 64, 2000), 0),
+    # bias lists longer than the fixed stride (256) and than a workgroup (1024)
+    "long_bias_lists": (300, 50000, (0, 20, 64), 0, 1500),
+    "long_bias_lists_split": (24, 100000, (0, 1, 50, 300), 1, 600),
 }
+
+
+def _drawn_config(i):
+    """Random sweep configuration i: (B, V, top-k choices, offset), drawn from
+    a fixed seed with B x V at most 40 M logits."""
+    r = np.random.default_rng(1000 + i)
+    while True:
+        B = int(r.choice([1, 2, 5, 33, 200, 257, 520]))
+        V = int(r.choice([1000, 4097, 32000, 50001, 128256, 151936]))
+        if B * V <= 40_000_000:
+            break
+    ks = tuple(int(k) for k in r.choice([0, 1, 2, 17, 63, 64, 65, 200, 1024, 2048, V - 1, V], size=4))
+    return B, V, ks, int(r.integers(0, 4))
+
+
+for _i in range(12):
+    SWEEP[f"drawn_{_i}" + ("_tied" if _i % 3 == 0 else "")] = _drawn_config(_i)
 
 
 @pytest.mark.parametrize("name", list(SWEEP))
@@ -144,7 +170,8 @@ def test_random_batches_every_path(pkg, torch, name):
     histories with out-of-range ids, and bias lists with -inf: every row's
     id, n, total, candidates and probabilities against the oracle
     (sampler.nim:59-121)."""
-    B, V, ks, off = SWEEP[name]
+    B, V, ks, off = SWEEP[name][:4]
+    max_bias = SWEEP[name][4] if len(SWEEP[name]) > 4 else 8
     rng = np.random.default_rng(abs(sum(map(ord, name))))
     say(f"[random_sweep] {name}: B={B} V={V} offset={off}")
     x = (rng.standard_normal((B, V)) * rng.choice([1.0, 2.5, 4.0])).astype(np.float32)
@@ -156,13 +183,13 @@ def test_random_batches_every_path(pkg, torch, name):
         if p["temperature"] > 0:
             p["topK"] = int(rng.choice(ks))
         plist.append(p)
-        nb = int(rng.integers(0, min(V, 8) + 1))
+        nb = int(rng.integers(0, min(V, max_bias) + 1))
         ids = rng.choice(V, size=nb, replace=False) if nb else []
         biases.append({int(i): float(rng.choice([-math.inf, -3.0, 0.5, 4.0])) for i in ids})
     H = 96
     hist = rng.integers(-3, V + 3, size=(B, H)).astype(np.int64)
     u = rng.random(B)
-    u[:3] = [0.0, 1.0 - 2.0 ** -53, 0.5]
+    u[: min(3, B)] = [0.0, 1.0 - 2.0 ** -53, 0.5][: min(3, B)]
     params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
     s = pkg.BatchSampler(params, V)
     try:
