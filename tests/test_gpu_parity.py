@@ -1179,3 +1179,58 @@ def test_argmax_parity(pkg, torch):
     assert got.tolist() == [0, 0, 0]
     # the host-sequence form
     assert pkg.argmax([1.0, 3.0, 3.0, -2.0]) == 1
+
+
+@pytest.mark.parametrize("rows,V,off", [(6, 32000, 1), (6, 32000, 2), (5, 5003, 3), (3, 128256, 1)])
+def test_row_entry_points_on_unaligned_rows(pkg, torch, rows, V, off):
+    """topTokens, softmaxInPlace, logProb's term, perplexity's term and argmax
+    (sampler.nim:45-57,123-130; model.nim:578-583) on rows whose logits start
+    off a 16-byte boundary (the kernels' 4-byte load paths), every result
+    against the oracle as in the aligned tests."""
+    x = _softmax_rows_input(rows, V, 300 + V + off)
+    rng = np.random.default_rng(off)
+    t = rng.integers(0, V, size=rows).astype(np.int32)
+    flat = torch.zeros(rows * V + off, dtype=torch.float32, device="cuda")
+    flat[off:] = torch.from_numpy(x.reshape(-1)).cuda()
+    d = flat[off:].view(rows, V)
+    assert d.data_ptr() % 16 != 0
+    say(f"[unaligned_rows] rows={rows} V={V} offset={off}")
+    # topTokens (a row holding NaN has NaN probabilities, whose order the
+    # reference's comparator leaves open: ids 0 .. m-1, as documented)
+    for n in (1, 64, 700):
+        ids, pr = pkg.top_tokens_device(d, n)
+        ids, pr = ids.cpu().numpy(), pr.cpu().numpy()
+        for r in range(rows):
+            if np.isnan(x[r]).any():
+                assert np.array_equal(ids[r], np.arange(min(n, V))), (n, r)
+                continue
+            wi, wp = _oracle_top_tokens(x[r], n)
+            assert np.array_equal(ids[r], wi), (n, r)
+            assert np.array_equal(pr[r].view(np.uint32), wp.view(np.uint32)), (n, r)
+    # softmaxInPlace, out of place
+    got = pkg.softmax_device(d).cpu().numpy()
+    for r in range(rows):
+        want = O.softmax(x[r])
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got[r]), nan), r
+        assert np.array_equal(got[r][~nan].view(np.uint32), want[~nan].view(np.uint32)), r
+    # logProb's term
+    prob, _ = pkg.log_prob_device(d, torch.from_numpy(t).cuda())
+    prob = prob.cpu().numpy()
+    for r in range(rows):
+        wp, _ = O.log_prob(x[r], int(t[r]))
+        assert (prob[r] != prob[r]) if wp != wp else prob[r].view(np.uint32) == wp.view(np.uint32), r
+    # perplexity's term
+    nll = pkg.row_nll_device(d, torch.from_numpy(t)).cpu().numpy()
+    for r in range(rows):
+        ref = O.row_nll(x[r], int(t[r]))
+        if math.isfinite(ref):
+            assert abs(nll[r] - ref) <= 1e-12 * max(1.0, abs(ref)), r
+        else:
+            assert nll[r] == ref or (math.isnan(ref) and math.isnan(nll[r])), r
+    # argmax
+    am = pkg.argmax_device(d).cpu().numpy()
+    L = O.lib()
+    for r in range(rows):
+        row = np.ascontiguousarray(x[r])
+        assert am[r] == L.nlo_argmax(row.ctypes.data_as(O.ctypes.POINTER(O.ctypes.c_float)), V), r
