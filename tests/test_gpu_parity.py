@@ -1234,3 +1234,48 @@ def test_row_entry_points_on_unaligned_rows(pkg, torch, rows, V, off):
     for r in range(rows):
         row = np.ascontiguousarray(x[r])
         assert am[r] == L.nlo_argmax(row.ctypes.data_as(O.ctypes.POINTER(O.ctypes.c_float)), V), r
+
+
+@pytest.mark.parametrize("name", ["k64_rows", "split_rows_tied", "block_path_tied", "whole_row_mix",
+                                  "long_bias_lists", "drawn_2", "drawn_6_tied"])
+def test_random_batches_own_rng_streams(pkg, torch, name):
+    """The sweep's batches with u = NULL, three calls on one sampler: each
+    sampling row draws rand(1.0) from its own initRand(seed) stream once per
+    call and greedy rows draw nothing (sampler.nim:77-78,117), whichever
+    kernel serves the row -- including rows one kernel hands on to another,
+    which must not draw twice.  The history grows by each call's ids."""
+    B, V, ks, off = SWEEP[name][:4]
+    max_bias = SWEEP[name][4] if len(SWEEP[name]) > 4 else 8
+    rng = np.random.default_rng(abs(sum(map(ord, name))) + 1)
+    say(f"[rng_sweep] {name}: B={B} V={V}")
+    plist, biases = [], []
+    for b in range(B):
+        p = rand_params(rng, V)
+        if p["temperature"] > 0:
+            p["topK"] = int(rng.choice(ks))
+        p["seed"] = int(rng.integers(0, 1 << 40))
+        plist.append(p)
+        nb = int(rng.integers(0, min(V, max_bias) + 1))
+        ids = rng.choice(V, size=nb, replace=False) if nb else []
+        biases.append({int(i): float(rng.choice([-math.inf, -3.0, 0.5, 4.0])) for i in ids})
+    hist = [list(rng.integers(-3, V + 3, size=32)) for _ in range(B)]
+    streams = [list(O.uniforms(plist[b]["seed"], 3)) for b in range(B)]
+    drawn = [0] * B
+    s = pkg.BatchSampler([to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)], V)
+    try:
+        s.accept(np.array(hist, dtype=np.int64))
+        for call in range(3):
+            x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
+            if "tied" in name:
+                x = (np.round(x * 4.0) / 4.0).astype(np.float32)
+            ids = s.sample(torch.from_numpy(x).cuda()).cpu().numpy()
+            for b in range(B):
+                greedy = plist[b]["temperature"] <= 0
+                u = 0.5 if greedy else float(streams[b][drawn[b]])
+                res, _, _, _ = oracle_row(x[b], plist[b], hist[b], biases[b], u, O.EXPF_CR)
+                assert ids[b] == res.id, (name, call, b, int(ids[b]), res.id)
+                drawn[b] += 0 if greedy else 1
+                hist[b].append(int(ids[b]))
+            s.accept(ids.astype(np.int64).reshape(B, 1))
+    finally:
+        s.close()
