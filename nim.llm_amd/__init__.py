@@ -389,8 +389,9 @@ class BatchSampler:
 class Sampler:
     """One nimllm Sampler (sampler.nim:23-26) backed by a one-row BatchSampler.
 
-    ``sample(logits)`` accepts a host sequence/ndarray (copied to the device) or
-    a 1-D device tensor, and returns the id as a Python int.
+    ``sample(logits)`` accepts a host sequence/ndarray (through
+    nls_sample_host: the kernel reads it from the handle's pinned staging) or a
+    1-D device tensor, and returns the id as a Python int.
     """
 
     def __init__(self, p: SamplerParams, vocab: int):
