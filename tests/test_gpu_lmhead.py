@@ -174,3 +174,36 @@ def test_lm_head_rejects_mismatched_tensors(pkg):
     y = pkg.lm_head(w, t, rows, cols, x, lora=(a, b, 1.0))  # the well-formed call runs
     torch.cuda.synchronize()
     assert y.shape == (1, rows)
+
+
+def _drawn_lm_case(i):
+    """LM head sweep case i: (type, rows, cols, nb, exact, lora rank), drawn
+    from a fixed seed with rows x cols x nb at most 40 M."""
+    r = np.random.default_rng(500 + i)
+    names = sorted(TYPES)
+    while True:
+        t = TYPES[names[int(r.integers(0, len(names)))]]
+        bs = O.block_size(t)
+        rows = int(r.choice([1, 7, 63, 64, 65, 300, 1000, 4099]))
+        if bs == 1:
+            cols = int(r.choice([1, 3, 17, 256, 1000, 2049, 4096]))
+        elif bs == 32:
+            cols = 32 * int(r.choice([1, 3, 8, 28, 65, 96, 192]))
+        else:
+            cols = 256 * int(r.choice([1, 2, 3, 8, 12, 16]))
+        nb = int(r.choice([1, 2, 3, 4, 5, 8, 9, 16]))
+        if rows * cols * nb <= 40_000_000:
+            break
+    return t, rows, cols, nb, bool(r.integers(0, 4) == 0), int(r.choice([0, 0, 1, 4, 16]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(24))
+def test_lm_head_random_cases(pkg, i):
+    """Twenty-four drawn cases over every weight type, row counts around the
+    kernels' row groups (1, 63-65, 4099), column counts of one to many
+    blocks, 1 to 16 hidden states (both of the reference's paths, model.nim:
+    185), exactMatmul and LoRA ranks 0-16: every logit bit for bit."""
+    t, rows, cols, nb, exact, rank = _drawn_lm_case(i)
+    print(f"lm_head sweep {i}: type={t} rows={rows} cols={cols} nb={nb} exact={exact} lora={rank}", flush=True)
+    run_case(pkg, t, rows, cols, nb, exact=exact, lora_rank=rank, seed=900 + i)
