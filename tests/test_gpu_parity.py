@@ -1279,3 +1279,57 @@ def test_random_batches_own_rng_streams(pkg, torch, name):
             s.accept(ids.astype(np.int64).reshape(B, 1))
     finally:
         s.close()
+
+
+@pytest.mark.parametrize("B,V,ks", [(300, 50000, (0, 20, 64)), (40, 100000, (0, 1, 50)),
+                                    (600, 30000, (65, 300)), (24, 70000, (0, 1000, 3000))])
+def test_generate_step_every_path(pkg, torch, B, V, ks):
+    """nls_generate_step over the planner's paths (one workgroup per row,
+    split rows, the k > 64 block path, whole-row rows with the claiming
+    grid): six steps of B contexts with random parameters on their own RNG
+    streams, end-of-generation ids made likely on some rows, finished rows
+    sampling nothing (-1) in every kernel, and every id against per-row
+    oracle loops (chat.nim:204-208)."""
+    rng = np.random.default_rng(B + V)
+    steps = 6
+    eog = [3, 17, V - 2]
+    say(f"[generate_step_paths] B={B} V={V} k={ks}")
+    plist = []
+    for b in range(B):
+        p = rand_params(rng, V)
+        if p["temperature"] > 0:
+            p["topK"] = int(rng.choice(ks))
+        p["seed"] = int(rng.integers(0, 1 << 31))
+        plist.append(p)
+    streams = [list(O.uniforms(plist[b]["seed"], steps)) for b in range(B)]
+    used = [0] * B
+    hist = [[] for _ in range(B)]
+    done = [False] * B
+    s = pkg.BatchSampler([to_pkg_params(pkg, p, {}) for p in plist], V)
+    d_done = torch.zeros(B, dtype=torch.int32, device="cuda")
+    d_eog = torch.tensor(eog, dtype=torch.int32, device="cuda")
+    try:
+        for t in range(steps):
+            x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+            hot = rng.choice(B, size=max(1, B // 5), replace=False)
+            x[hot, eog[t % 3]] += 15.0  # these rows likely end here
+            out = s.generate_step(torch.from_numpy(x).cuda(), d_eog, d_done).cpu().numpy()
+            got_done = d_done.cpu().numpy()
+            for b in range(B):
+                if done[b]:
+                    assert out[b] == -1, (t, b, int(out[b]))
+                    continue
+                u = 0.0
+                if plist[b]["temperature"] > 0:
+                    u = streams[b][used[b]]
+                    used[b] += 1
+                res, _, _, _ = oracle_row(x[b], plist[b], hist[b], {}, u, O.EXPF_CR)
+                assert out[b] == res.id, (t, b, int(out[b]), res.id)
+                if res.id in eog:
+                    done[b] = True
+                else:
+                    hist[b].append(res.id)
+            assert [bool(v) for v in got_done] == done, t
+        assert any(done) and not all(done)
+    finally:
+        s.close()
