@@ -221,7 +221,80 @@ __device__ __forceinline__ int chain_walk(XPtr x, int cnt, float& acc, Stop stop
   return cnt;
 }
 
-template <int NT, typename VPtr, typename IPtr, typename EPtr>
+// chain_walk's contract over an LDS array, with the running value held whole
+// by every lane: each step is one dependent fp32 operation on a term that all
+// lanes read from the same LDS address (a broadcast), so no lane-to-lane move
+// sits in the chain and every branch is uniform.  Full blocks of 32 terms are
+// read as eight 16-byte loads; a partial block at either end with 4-byte
+// loads clamped into the array, padded with +0, which leaves the value (a sum
+// of terms >= 0 from +0, or a difference of them) unchanged.  stop is tested
+// once per block (it is monotone along the chain, or the value turned NaN),
+// and the block where it holds is walked again step by step.  Every lane
+// calls it.
+template <bool SUB, bool HAS_STOP, typename Stop>
+__device__ __forceinline__ int chain_lds(const float* x, int cnt, float& acc, Stop stop, float* at = nullptr) {
+  constexpr int B = 32;      // terms per block
+  constexpr int BQ = B / 4;  // 16-byte reads per block
+  int res = cnt;
+  float a = acc;
+  if (cnt <= 0) return res;
+  auto op = [](float s, float t) -> float { return SUB ? s - t : s + t; };
+  auto uni = [](bool c) -> bool { return __builtin_amdgcn_readfirstlane((int)c) != 0; };
+  // B steps over t (elements i0 ..); true when stop holds at one of them.
+  // The block where it holds is walked again from its start, its terms read
+  // from LDS once more (through an opaque index, so that neither the terms
+  // nor the running values of the first walk stay in registers for it).
+  auto run = [&](const float (&t)[B], int i0) -> bool {
+    const float a0 = a;
+#pragma unroll
+    for (int j = 0; j < B; ++j) a = op(a, t[j]);
+    if (HAS_STOP && uni(a != a || stop(a, i0 + B - 1))) {
+      float r = a0;
+      int o = i0;
+      asm volatile("" : "+v"(r), "+s"(o));
+#pragma unroll
+      for (int j = 0; j < B; ++j) {
+        r = op(r, o + j < cnt ? x[o + j] : 0.0f);
+        if (uni(stop(r, i0 + j))) {
+          res = i0 + j;
+          if (at) *at = r;
+          return true;
+        }
+      }
+    }
+    return false;
+  };
+  auto partial = [&](int i0, int m) -> bool {  // elements i0 .. i0 + m - 1 (m <= B)
+    float t[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j) t[j] = x[min(i0 + j, cnt - 1)];
+#pragma unroll
+    for (int j = 0; j < B; ++j) t[j] = j < m ? t[j] : 0.0f;
+    return run(t, i0);
+  };
+  const int head = min(cnt, (int)((16u - ((uint32_t)(uintptr_t)x & 15u)) & 15u) >> 2);
+  bool done = head > 0 && partial(0, head);
+  const int nb = (cnt - head) / B;
+  const float4* x4 = reinterpret_cast<const float4*>(x + head);
+  for (int b = 0; b < nb && !done; ++b) {
+    float t[B];
+#pragma unroll
+    for (int q = 0; q < BQ; ++q) {
+      const float4 c = x4[b * BQ + q];
+      t[4 * q + 0] = c.x;
+      t[4 * q + 1] = c.y;
+      t[4 * q + 2] = c.z;
+      t[4 * q + 3] = c.w;
+    }
+    done = run(t, head + b * B);
+  }
+  const int i1 = head + nb * B;
+  if (!done && i1 < cnt) partial(i1, cnt - i1);
+  acc = a;
+  return res;
+}
+
+template <int NT, bool E_LDS = false, typename VPtr, typename IPtr, typename EPtr>
 __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr e, int ncand, const RowParams& P,
                                        double u, int* smem) {
   const float mx = val[0];  // candidates are in non-increasing order
@@ -235,7 +308,10 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
   if (threadIdx.x < kWave) {
     // s = sum of e in order
     float s = 0.0f;
-    chain_walk<false, false>(e, ncand, s, [](float, int) { return false; });
+    if constexpr (E_LDS)
+      chain_lds<false, false>(e, ncand, s, [](float, int) { return false; });
+    else
+      chain_walk<false, false>(e, ncand, s, [](float, int) { return false; });
     if (lane == 0) s_sum = s;
   }
   __syncthreads();
@@ -250,8 +326,12 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
     if (P.topp_active) {
       // the first i with (double)(e_0 + ... + e_i) >= topP
       float cum = 0.0f, at = 0.0f;
-      const int stop =
-          chain_walk<false, true>(e, ncand, cum, [&](float c, int) { return (double)c >= P.topP; }, &at);
+      auto reached = [&](float c, int) { return (double)c >= P.topP; };
+      int stop;
+      if constexpr (E_LDS)
+        stop = chain_lds<false, true>(e, ncand, cum, reached, &at);
+      else
+        stop = chain_walk<false, true>(e, ncand, cum, reached, &at);
       if (stop < ncand) n = stop + 1;
       cum_n = stop < ncand ? at : cum;
     }
@@ -273,10 +353,17 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
     float total = 0.0f;
     if (P.topp_active && n == n_topp)
       total = cum_n;
+    else if constexpr (E_LDS)
+      chain_lds<false, false>(e, n, total, [](float, int) { return false; });
     else
       chain_walk<false, false>(e, n, total, [](float, int) { return false; });
     float r = (float)u * total;
-    const int hit = chain_walk<true, true>(e, n, r, [](float rr, int) { return rr <= 0.0f; });
+    auto drawn = [](float rr, int) { return rr <= 0.0f; };
+    int hit;
+    if constexpr (E_LDS)
+      hit = chain_lds<true, true>(e, n, r, drawn);
+    else
+      hit = chain_walk<true, true>(e, n, r, drawn);
     const int pos = hit < n ? hit : n - 1;
     if (lane == 0) {
       s_n = n;
@@ -860,17 +947,23 @@ void stream_kernel(const StreamArgs a) {
     int bi = 0x7fffffff;
     int buf_n = 0, cur = 0;
     uint32_t tau = 0u;
-    // Block path on a whole row: the first refresh (tile 0) takes the
-    // spec_rank-th largest key of the tile instead of the k-th, a rank that
-    // lets about 2k elements of the row through when the tile is typical of
-    // it, so that the buffer rarely fills again.  Such a threshold need not
-    // bound the k-th largest from below: the candidates are then checked to
-    // number at least k, and the row goes to the whole-row path otherwise.
+    // Block path on a whole row: the first refresh (tile 0) sets a threshold
+    // that lets about 2k elements of the row through when the tile is typical
+    // of it, so that the buffer rarely fills again: the spec_rank-th largest of
+    // the threads' maxima of the tile, where spec_rank is the number of the NT
+    // maxima (each over NE values) expected at or above the value that a
+    // fraction want / len of the row's values reach.  Such a threshold need
+    // not bound the k-th largest from below: the candidates are then checked
+    // to number at least k, and the row goes to the whole-row path otherwise.
     int spec_rank = 0;
     if (!WAVE && topk && a.S == 1 && len > UE) {
       const int64_t want = min(2LL * k, (int64_t)a.ccap * 7 / 8);  // passing elements aimed at
-      const int64_t r = (want * UE + len - 1) / len;
-      spec_rank = r < k ? (int)r : 0;
+      const double miss = 1.0 - (double)want / (double)len;     // of one value
+      double all = 1.0;                                          // of the NE values of a thread
+  #pragma unroll
+      for (int e = 0; e < NE; ++e) all *= miss;
+      const int r = (int)((1.0 - all) * NT + 0.5);
+      spec_rank = (want < k || r < 1) ? 0 : min(r, NT);
     }
     bool spec_used = false;
 #ifdef NLS_PHASE_STAMPS
@@ -1163,36 +1256,6 @@ void stream_kernel(const StreamArgs a) {
         ++st_refreshes;
 #endif
         uint64_t* nb = cand + (size_t)(cur ^ 1) * a.ccap;
-        uint32_t tops[Q];
-  #pragma unroll
-        for (int q = 0; q < Q; ++q) tops[q] = 0u;
-        int nmine = 0;
-        for (int i = tid; i < buf_n; i += NT) {
-          topq_insert<Q>(tops, (uint32_t)(cb[i] >> 32));
-          ++nmine;
-        }
-  #pragma unroll
-        for (int q = 0; q < NE; ++q) {
-          if (use(q) && key[q] >= tau) {
-            topq_insert<Q>(tops, key[q]);
-            ++nmine;
-          }
-        }
-        const int nv = min(nmine, Q);
-        const int tv = block_sum<NT>(nv, smem);
-        // t1 <= the k-th largest of the per-thread tops (k real elements), so t1
-        // is a lower bound of the k-th largest of everything seen.  A coarse
-        // digit prefix is enough while it admits few elements; otherwise refine
-        // to the exact k-th largest of the tops.
-        auto tops_select = [&](int rank, int fit) -> uint32_t {
-          return block_select<NT>(
-                     [&](auto fn) {
-  #pragma unroll
-                       for (int q = 0; q < Q; ++q) fn(tops[q], q < nv);
-                     },
-                     rank, fit, shist, smem)
-              .tau;
-        };
         auto count_ge = [&](uint32_t th) -> int {
           int c = 0;
           for (int i = tid; i < buf_n; i += NT) c += ((uint32_t)(cb[i] >> 32) >= th);
@@ -1202,16 +1265,53 @@ void stream_kernel(const StreamArgs a) {
         };
         uint32_t t1 = tau;
         int cnt = buf_n + ttot;
-        if (spec_rank > 0 && tv >= spec_rank) {
-          t1 = tops_select(spec_rank, -1);
+        if (spec_rank > 0) {
+          // the speculative threshold (above): one maximum per thread, a thread
+          // with no usable value offering the lowest key
+          uint32_t mx = 0u;
+  #pragma unroll
+          for (int q = 0; q < NE; ++q) mx = (use(q) && key[q] > mx) ? key[q] : mx;
+          t1 = block_select<NT>([&](auto fn) { fn(mx, true); }, spec_rank, -1, shist, smem).tau;
           cnt = count_ge(t1);
           spec_used = true;
-        } else if (tv >= k) {
-          t1 = tops_select(k, 2 * k);
-          cnt = count_ge(t1);
-          if (cnt > a.ccap / 2) {
-            t1 = tops_select(k, -1);
+        } else {
+          uint32_t tops[Q];
+  #pragma unroll
+          for (int q = 0; q < Q; ++q) tops[q] = 0u;
+          int nmine = 0;
+          for (int i = tid; i < buf_n; i += NT) {
+            topq_insert<Q>(tops, (uint32_t)(cb[i] >> 32));
+            ++nmine;
+          }
+  #pragma unroll
+          for (int q = 0; q < NE; ++q) {
+            if (use(q) && key[q] >= tau) {
+              topq_insert<Q>(tops, key[q]);
+              ++nmine;
+            }
+          }
+          const int nv = min(nmine, Q);
+          const int tv = block_sum<NT>(nv, smem);
+          // t1 <= the k-th largest of the per-thread tops (k real elements), so
+          // t1 is a lower bound of the k-th largest of everything seen.  A
+          // coarse digit prefix is enough while it admits few elements;
+          // otherwise refine to the exact k-th largest of the tops.
+          auto tops_select = [&](int rank, int fit) -> uint32_t {
+            return block_select<NT>(
+                       [&](auto fn) {
+  #pragma unroll
+                         for (int q = 0; q < Q; ++q) fn(tops[q], q < nv);
+                       },
+                       rank, fit, shist, smem)
+                .tau;
+          };
+          if (tv >= k) {
+            t1 = tops_select(k, 2 * k);
             cnt = count_ge(t1);
+            if (cnt > a.ccap / 2) {
+              t1 = tops_select(k, -1);
+              cnt = count_ge(t1);
+            }
           }
         }
         spec_rank = 0;
@@ -1703,7 +1803,7 @@ void stream_kernel(const StreamArgs a) {
     if (tid == 0) s_u = take_uniform(a.d_u, u_in, st0, st1, a.rng, row);
     __syncthreads();
     if (wv == 0) NLS_STAMP(row, 5);
-    const TailOut to = softmax_cutoff_draw<NT>(vals, ids, ebuf, k, P, s_u, smem);
+    const TailOut to = softmax_cutoff_draw<NT, true>(vals, ids, ebuf, k, P, s_u, smem);
     if (wv == 0) NLS_STAMP(row, 6);
     if (tid == 0) a.out[row] = to.id;
     write_debug<NT>(a.dbg, row, 2 | to.nan_cand, to.n, k, to.total, ids, ebuf);
