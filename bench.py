@@ -867,8 +867,9 @@ def phase_stamps(args):
     if not plan.k64:
         # stream_kernel rows (each instance's unit keeps its own stamps): 0
         # start, 1 stream start, 2 stream end, 3 members start, 4 members
-        # done, 5 tail start, 6 tail done; 12 candidates, 13 threshold
-        # refreshes, 14 their ticks, 15 tiles
+        # done, 5 tail start, 6 tail done; 7 ticks waiting for a unit's
+        # data, 11 ticks at the tile barriers (block path); 12 candidates, 13
+        # threshold refreshes, 14 their ticks, 15 tiles
         vec = "true" if w.V % 4 == 0 else "false"
         fn = getattr(L, f"nls_stream_stamps_{plan.stream_threads}_{vec}")
         buf[:] = 0
@@ -885,6 +886,8 @@ def phase_stamps(args):
                 "prologue: row constants, patch table": us(P[:, 1] - P[:, 0]),
                 "stream": us(P[:, 2] - P[:, 1]),
                 "  of which threshold refreshes": us(P[:, 14]),
+                "  of which waiting for a unit's data": us(P[:, 7]),
+                "  of which at the tile barriers (block path)": us(P[:, 11]),
                 "patched values, candidates": us(P[:, 3] - P[:, 2]),
                 "heap-rule members": us(P[:, 4] - P[:, 3]),
                 "sort of the members": us(P[:, 5] - P[:, 4]),

@@ -970,6 +970,8 @@ void stream_kernel(const StreamArgs a) {
     uint64_t st_refresh_ticks = 0;  // time inside block-path refreshes
     int st_refreshes = 0;
     uint64_t st_tiles = 0;
+    uint64_t st_data_ticks = 0;  // waiting for a unit's data (and issuing the next)
+    uint64_t st_bar_ticks = 0;   // at the block path's tile barrier
 #endif
     // wave path (k <= 64): this wave's buffer count, threshold and overflow
     int wn = 0;
@@ -1238,7 +1240,13 @@ void stream_kernel(const StreamArgs a) {
         int wbase = 0;
         if (lane == 0 && wtot) wbase = atomicAdd(&s_tile_cnt[slot], wtot);
         wbase = __shfl(wbase, 0, kWave);
+#ifdef NLS_PHASE_STAMPS
+        const uint64_t st_b0 = __builtin_amdgcn_s_memrealtime();
         __syncthreads();
+        st_bar_ticks += __builtin_amdgcn_s_memrealtime() - st_b0;
+#else
+        __syncthreads();
+#endif
         const int ttot = s_tile_cnt[slot];
         if (tid == 0) s_tile_cnt[(t + 2) % 3] = 0;
         uint64_t* cb = cand + (size_t)cur * a.ccap;
@@ -1371,6 +1379,9 @@ void stream_kernel(const StreamArgs a) {
           }
         }
         float v[NE];
+#ifdef NLS_PHASE_STAMPS
+        const uint64_t st_d0 = __builtin_amdgcn_s_memrealtime();
+#endif
   #pragma unroll
         for (int j = 0; j < NV4; ++j) {
           v[4 * j + 0] = R0[j].x;
@@ -1379,6 +1390,10 @@ void stream_kernel(const StreamArgs a) {
           v[4 * j + 3] = R0[j].w;
           R0[j] = load_group<GS, VEC>(rs, tn * UE, j, uth);
         }
+#ifdef NLS_PHASE_STAMPS
+        asm volatile("" ::"v"(v[NE - 1]));
+        st_data_ticks += __builtin_amdgcn_s_memrealtime() - st_d0;
+#endif
         process(v, t, first);
 #ifdef NLS_PHASE_STAMPS
         ++st_tiles;
@@ -1393,6 +1408,8 @@ void stream_kernel(const StreamArgs a) {
       NLS_STAMP_VALUE(row, 13, st_refreshes);
       NLS_STAMP_VALUE(row, 14, st_refresh_ticks);
       NLS_STAMP_VALUE(row, 15, st_tiles);
+      NLS_STAMP_VALUE(row, 7, st_data_ticks);
+      NLS_STAMP_VALUE(row, 11, st_bar_ticks);
     }
 #endif
     // The final value of patched slot p from its original logit: penalties then

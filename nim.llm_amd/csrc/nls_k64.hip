@@ -69,59 +69,37 @@ __device__ __forceinline__ uint32_t boot_addr(uint32_t b) {
 __device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
 // Heap-rule members (sampler.nim:88-95) when ties at the k-th largest key T
-// exceed k: mem[0..ge) holds every candidate >= T (ge <= 256; gt of them
-// > T).  Members = {> T} plus the m = k - gt largest indices among the ties
-// whose index is at most p*, the index at which the running count of {>= T}
-// in index order reaches k.  Writes the k members to mem[0..k) (any order).
-__device__ __forceinline__ bool tie_members(uint64_t* mem, int ge, int gt, int k, uint32_t T) {
+// exceed k: mem[0..ge) holds every candidate >= T (ge <= 64, one per lane; gt
+// of them > T).  Members = {> T} plus the m = k - gt largest indices among the
+// ties whose index is at most p*, the index at which the running count of
+// {>= T} in index order reaches k.  Indices are below 2^ibits.  Writes the k
+// members to mem[0..k) (any order).
+__device__ __forceinline__ bool tie_members(uint64_t* mem, int ge, int gt, int k, uint32_t T, int ibits) {
   const int lane = lane_id();
-  constexpr int PER = kWaveCap / kWave;
-  uint64_t x[PER];
-  uint32_t idx[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int i = lane + j * kWave;
-    x[j] = i < ge ? mem[i] : 0ull;
-    idx[j] = i < ge ? (uint32_t)x[j] : 0xffffffffu;
-  }
-  // p*: the smallest r with at least k indices <= r (indices < 2^31)
+  const bool have = lane < ge;
+  const uint64_t x = have ? mem[lane] : 0ull;
+  const uint32_t idx = have ? (uint32_t)x : 0xffffffffu;
+  // p*: the smallest r with at least k indices <= r
   uint32_t r = 0u;
-  for (int b = 30; b >= 0; --b) {
+  for (int b = ibits - 1; b >= 0; --b) {
     const uint32_t c = r | ((1u << b) - 1u);
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) cnt += __popcll(__ballot(idx[j] <= c));
-    if (cnt < k) r |= 1u << b;
+    if ((int)__popcll(__ballot(idx <= c)) < k) r |= 1u << b;
   }
   const uint32_t pstar = r;
   const int m = k - gt;
-  uint32_t tie[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const bool t = idx[j] != 0xffffffffu && (uint32_t)(x[j] >> 32) == T && idx[j] <= pstar;
-    tie[j] = t ? idx[j] : 0xffffffffu;
-  }
+  const bool tie = have && (uint32_t)(x >> 32) == T && idx <= pstar;
   // the m-th largest tie index: the largest q with at least m tie indices >= q
   uint32_t q = 0u;
-  for (int b = 30; b >= 0; --b) {
+  for (int b = ibits - 1; b >= 0; --b) {
     const uint32_t c = q | (1u << b);
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) cnt += __popcll(__ballot(tie[j] != 0xffffffffu && tie[j] >= c));
-    if (cnt >= m) q = c;
+    if ((int)__popcll(__ballot(tie && idx >= c)) >= m) q = c;
   }
   wave_lds_sync();
-  int base = 0;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const bool in = idx[j] != 0xffffffffu &&
-                    ((uint32_t)(x[j] >> 32) > T || (tie[j] != 0xffffffffu && tie[j] >= q));
-    const uint64_t mk = __ballot(in);
-    if (in) mem[base + (int)__popcll(mk & lanes_below())] = x[j];
-    base += (int)__popcll(mk);
-  }
+  const bool in = have && ((uint32_t)(x >> 32) > T || (tie && idx >= q));
+  const uint64_t mk = __ballot(in);
+  if (in) mem[(int)__popcll(mk & lanes_below())] = x;
   wave_lds_sync();
-  return base == k;
+  return (int)__popcll(mk) == k;
 }
 
 // Descending rank sort of n <= 64 distinct 64-bit entries mem[0..n) (LDS,
@@ -1046,7 +1024,7 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
         // all entries >= T must lie within the 64 ranks held
         if (ge == nl && N > nl) {
           rovf = true;
-        } else if (tie_members(s_flist, ge, gt, kk, T)) {
+        } else if (tie_members(s_flist, ge, gt, kk, T, 32 - __clz(len > 1 ? len - 1 : 1))) {
           x = rank_sort64(s_flist, kk);
         } else {
           rovf = true;
