@@ -625,6 +625,85 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
 // stream leaves them out -- only where a value would be kept or would raise
 // the argmax does it test the bitmap -- and they rejoin the candidates (or
 // the argmax) after the stream.
+// LDS word of bin b of a 4096-bin histogram laid out for one wave's scan:
+// bins form 64 ranges r of 64 consecutive bins j; the 4 bins 4q..4q+3 of
+// range r sit at words (q * 64 + r) * 4 .. +3, so that the 64 lanes reading
+// their ranges' bins 4q..4q+3 with one 16-byte load each cover 1 KB without
+// bank conflicts.
+__device__ __forceinline__ uint32_t hist4k_addr(uint32_t b) {
+  const uint32_t r = b >> 6, j = b & 63u;
+  return ((j >> 2) * 64u + r) * 4u + (j & 3u);
+}
+
+// One wave: the bin b of a 4096-bin histogram (hist4k_addr layout) where the
+// count from the top bin down reaches `rank`, and the count in the bins
+// above it.  Returns false when the whole histogram holds fewer.
+__device__ __forceinline__ bool hist4k_rank(const uint32_t* hist, int rank, int& bin, int& above) {
+  const int lane = lane_id();
+  const int range = kWave - 1 - lane;  // lane l sums range 63 - l (largest first)
+  int c = 0;
+  const uint4* h4 = reinterpret_cast<const uint4*>(hist);
+#pragma unroll
+  for (int q = 0; q < kWave / 4; ++q) {
+    const uint4 v = h4[q * kWave + range];
+    c += (int)(v.x + v.y + v.z + v.w);
+  }
+  const int incl = wave_incl_scan(c);
+  const uint64_t mk = __ballot(incl - c < rank && incl >= rank);
+  if (!mk) return false;
+  const int sl = __ffsll((unsigned long long)mk) - 1;
+  const int ab = __builtin_amdgcn_readlane(incl - c, sl);
+  const int r = kWave - 1 - sl;
+  const int cb = (int)hist[hist4k_addr((uint32_t)(r * kWave + kWave - 1 - lane))];  // this lane's bin, from the top
+  const int inc2 = wave_incl_scan(cb) + ab;
+  const uint64_t m2 = __ballot(inc2 - cb < rank && inc2 >= rank);
+  const int l2 = __ffsll((unsigned long long)m2) - 1;
+  bin = r * kWave + (kWave - 1 - l2);
+  above = __builtin_amdgcn_readlane(inc2 - cb, l2);
+  return true;
+}
+
+// The rank-th largest of one key per thread (rank >= 1), to 24 bits: the
+// returned key, with its low 8 bits zero, is at most that key, and every key
+// at or above it agrees with that key in its top 24 bits.  Two 4096-bin
+// histogram rounds (the top 12 bits, then the next 12 within the chosen bin)
+// over h1 and h2 (4096 words each, LDS, free); every thread calls it.
+template <int NT>
+__device__ __forceinline__ uint32_t block_rank24(uint32_t key, int rank, uint32_t* h1, uint32_t* h2, int* smem) {
+  constexpr int NW = NT / kWave;
+  const int tid = threadIdx.x;
+  uint4* z1 = reinterpret_cast<uint4*>(h1);
+  uint4* z2 = reinterpret_cast<uint4*>(h2);
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+  for (int i = tid; i < 1024; i += NT) {
+    z1[i] = z;
+    z2[i] = z;
+  }
+  __syncthreads();
+  atomicAdd(&h1[hist4k_addr(key >> 20)], 1u);
+  __syncthreads();
+  if (tid < kWave) {
+    int b = 0, ab = 0;
+    if (!hist4k_rank(h1, rank, b, ab)) b = 0, ab = 0;
+    if (tid == 0) {
+      smem[NW + 1] = b;
+      smem[NW + 2] = ab;
+    }
+  }
+  __syncthreads();
+  const uint32_t b1 = (uint32_t)smem[NW + 1];
+  const int r2 = rank - smem[NW + 2];
+  if ((key >> 20) == b1) atomicAdd(&h2[hist4k_addr((key >> 8) & 4095u)], 1u);
+  __syncthreads();
+  if (tid < kWave) {
+    int b = 0, ab = 0;
+    if (!hist4k_rank(h2, r2, b, ab)) b = 0;
+    if (tid == 0) smem[NW + 3] = b;
+  }
+  __syncthreads();
+  return (b1 << 20) | ((uint32_t)smem[NW + 3] << 8);
+}
+
 template <int NT, bool VEC, int Q, bool WAVE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT <= 512 ? 4 : 2)))
 void stream_kernel(const StreamArgs a) {
@@ -1279,8 +1358,15 @@ void stream_kernel(const StreamArgs a) {
           uint32_t mx = 0u;
   #pragma unroll
           for (int q = 0; q < NE; ++q) mx = (use(q) && key[q] > mx) ? key[q] : mx;
-          t1 = block_select<NT>([&](auto fn) { fn(mx, true); }, spec_rank, -1, shist, smem).tau;
-          cnt = count_ge(t1);
+          if (buf_n == 0 && a.ccap >= 2048) {
+            // (both buffers are empty: they hold the two histograms)
+            t1 = block_rank24<NT>(mx, spec_rank, reinterpret_cast<uint32_t*>(cand),
+                                  reinterpret_cast<uint32_t*>(cand + a.ccap), smem);
+            cnt = -1;  // counted by the compaction below
+          } else {
+            t1 = block_select<NT>([&](auto fn) { fn(mx, true); }, spec_rank, -1, shist, smem).tau;
+            cnt = count_ge(t1);
+          }
           spec_used = true;
         } else {
           uint32_t tops[Q];
@@ -1335,6 +1421,10 @@ void stream_kernel(const StreamArgs a) {
         for (int q = 0; q < NE; ++q) c1 += (use(q) && key[q] >= t1);
         int tot;
         int pos = block_excl_scan<NT>(c1, smem, tot);
+        if (tot > a.ccap) {  // (uniform; a count left to this scan)
+          ovf = true;
+          return;
+        }
         for (int i = tid; i < buf_n; i += NT) {
           const uint64_t x = cb[i];
           if ((uint32_t)(x >> 32) >= t1) nb[pos++] = x;
