@@ -164,7 +164,9 @@ struct nls_sampler {
   uint32_t* arrive = nullptr;
   uint64_t* rng = nullptr;
   int32_t* generic_list = nullptr;
-  int32_t* generic_count = nullptr;  // [4]
+  int32_t* generic_count = nullptr;  // [6]: handed-on counts, claim counters, fallback counts (each by call parity)
+  int32_t* fb_list = nullptr;        // [B] the rows the grouped launch leaves to the whole-row launch
+  double* fb_u = nullptr;            // [B] their uniforms, when drawn there
   int32_t* all_rows = nullptr;       // no streaming rows: 0 .. B-1, then B (the count), then a spare
   // k64_kernel with full-sort rows in the batch: the streamed rows (its
   // grid) and the others (the whole-row kernel's fixed list)
@@ -204,6 +206,8 @@ struct nls_sampler {
     dfree(rng);
     dfree(generic_list);
     dfree(generic_count);
+    dfree(fb_list);
+    dfree(fb_u);
     dfree(all_rows);
     dfree(k64_list);
     dfree(full_list);
@@ -625,7 +629,11 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   if ((rc = dalloc(&s->arrive, B))) return fail(rc);
   if ((rc = dalloc(&s->rng, (size_t)2 * B))) return fail(rc);
   if ((rc = dalloc(&s->generic_list, B))) return fail(rc);
-  if ((rc = dalloc(&s->generic_count, 4))) return fail(rc);  // counts, then claim counters (by call parity)
+  if ((rc = dalloc(&s->generic_count, 6))) return fail(rc);  // counts, claim and fallback counters (by call parity)
+  if (s->plan.gen_lds > 0) {
+    if ((rc = dalloc(&s->fb_list, B))) return fail(rc);
+    if ((rc = dalloc(&s->fb_u, B))) return fail(rc);
+  }
   if (s->plan.no_stream) {
     std::vector<int32_t> rows((size_t)B + 2);
     for (int b = 0; b < B; ++b) rows[b] = b;
@@ -680,7 +688,7 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
     return fail(hip_fail(e, "clear counters"));
   if ((e = hipMemsetAsync(s->done, 0, sizeof(uint32_t), st)) != hipSuccess)
     return fail(hip_fail(e, "clear counters"));
-  if ((e = hipMemsetAsync(s->generic_count, 0, sizeof(int32_t) * 4, st)) != hipSuccess)
+  if ((e = hipMemsetAsync(s->generic_count, 0, sizeof(int32_t) * 6, st)) != hipSuccess)
     return fail(hip_fail(e, "clear counters"));
   if ((e = hipStreamSynchronize(st)) != hipSuccess) return fail(hip_fail(e, "sync"));
   *out = s;
@@ -858,6 +866,15 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   ga.out = d_out;
   ga.dbg = dp;
   ga.grouped = s->plan.gen_lds > 0 ? 1 : 0;
+  if (ga.grouped && s->fb_list && !dp.cand_ids && !dp.cand_probs) {
+    // the grouped rows in a launch of their own, then the rows it leaves
+    // (candidate lists are written by the whole-row sort, so a call asking
+    // for them keeps the one launch, where a grouped row is sorted as well)
+    ga.fb_list = s->fb_list;
+    ga.fb_count = s->generic_count + 4 + s->parity;
+    ga.fb_next = s->generic_count + 4 + (s->parity ^ 1);
+    ga.fb_u = s->fb_u;
+  }
   LaunchPlan lp = s->plan;
   a.gen_inline = s->gen_inline;
   if (a.gen_inline && s->window_may_overflow()) {

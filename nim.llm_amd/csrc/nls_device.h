@@ -603,28 +603,12 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
   }
 }
 
-template <int NT, bool GROUPED = false, bool CLAIM = false>
+template <int NT, bool GROUPED = false, bool CLAIM = false, bool ONLY = false>
 __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int nw, int count, uint32_t* wcnt,
                                              uint32_t* dbase, uint32_t* drun, int* smem, double* s_u_p,
                                              int* s_i, float* s_rv, int* s_ri,
                                              unsigned char* glds = nullptr);
 
-// ---------------------------------------------------------------------------
-// 1. stream_kernel
-// ---------------------------------------------------------------------------
-// Dynamic LDS: cand[2][ccap] u64 | region A.
-// Region A up to the final selection: bitmap[nwords] u32 | wpre[nwords] u16
-// (padded to 4 bytes) | pfin[pcap] f32 | pbias[pcap] f32 | pflag[pcap] u32 |
-// pid[pcap] i32.  Afterwards it holds the tail: mem[mcap] u64 |
-// vals[kcap] f32 | ids[kcap] i32 | e[kcap] f32.
-//
-// Penalties and bias touch few ids of a slice [lo, lo + len) (the patched
-// ids).  Bit (id - lo) of `bitmap` marks them; patch p of a marked id sits
-// at wpre[w] + popcount(bits of word w below it).  Their original logits are
-// gathered up front and their final values (pfin) computed once, so the
-// stream leaves them out -- only where a value would be kept or would raise
-// the argmax does it test the bitmap -- and they rejoin the candidates (or
-// the argmax) after the stream.
 // LDS word of bin b of a 4096-bin histogram laid out for one wave's scan:
 // bins form 64 ranges r of 64 consecutive bins j; the 4 bins 4q..4q+3 of
 // range r sit at words (q * 64 + r) * 4 .. +3, so that the 64 lanes reading
@@ -704,6 +688,22 @@ __device__ __forceinline__ uint32_t block_rank24(uint32_t key, int rank, uint32_
   return (b1 << 20) | ((uint32_t)smem[NW + 3] << 8);
 }
 
+// ---------------------------------------------------------------------------
+// 1. stream_kernel
+// ---------------------------------------------------------------------------
+// Dynamic LDS: cand[2][ccap] u64 | region A.
+// Region A up to the final selection: bitmap[nwords] u32 | wpre[nwords] u16
+// (padded to 4 bytes) | pfin[pcap] f32 | pbias[pcap] f32 | pflag[pcap] u32 |
+// pid[pcap] i32.  Afterwards it holds the tail: mem[mcap] u64 |
+// vals[kcap] f32 | ids[kcap] i32 | e[kcap] f32.
+//
+// Penalties and bias touch few ids of a slice [lo, lo + len) (the patched
+// ids).  Bit (id - lo) of `bitmap` marks them; patch p of a marked id sits
+// at wpre[w] + popcount(bits of word w below it).  Their original logits are
+// gathered up front and their final values (pfin) computed once, so the
+// stream leaves them out -- only where a value would be kept or would raise
+// the argmax does it test the bitmap -- and they rejoin the candidates (or
+// the argmax) after the stream.
 template <int NT, bool VEC, int Q, bool WAVE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT <= 512 ? 4 : 2)))
 void stream_kernel(const StreamArgs a) {
@@ -2733,7 +2733,7 @@ __device__ __forceinline__ bool window_topk(const GenericArgs& a, int row, const
 // Rows of the list from index w0 on, every nw-th: the whole-row path.  LDS
 // scratch is passed in (wcnt: NW * 256 words, dbase and drun: 256 each), so
 // that the streaming kernel's last workgroup can run it too.
-template <int NT, bool GROUPED, bool CLAIM>
+template <int NT, bool GROUPED, bool CLAIM, bool ONLY>
 __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int nw, int count, uint32_t* wcnt,
                                              uint32_t* dbase, uint32_t* drun, int* smem, double* s_u_p,
                                              int* s_i, float* s_rv, int* s_ri, unsigned char* glds) {
@@ -2761,7 +2761,10 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
     return s_claim;
   };
   for (int li = next_row(w0); li < nfx + count; li = next_row(li + nw)) {
-    const int row = li < nfx ? a.fixed_list[li] : load_agent(&a.generic_list[li - nfx]);
+    int row = li < nfx ? a.fixed_list[li] : load_agent(&a.generic_list[li - nfx]);
+    // (a fallback list's row may carry the uniform the grouped launch drew)
+    const bool u_saved = a.fb_in && (row & kFbUSaved) != 0;
+    row &= ~kFbUSaved;
     if (a.row_done && a.row_done[row] != 0) {  // a finished row of a batched loop
       if (tid == 0) a.out[row] = -1;
       continue;
@@ -2772,7 +2775,7 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
     GroupOut gout;
     gout.ok = 0;
     if constexpr (GROUPED) {
-      if (P.mode == kModeFull && a.grouped) {
+      if (P.mode == kModeFull && a.grouped && !a.fb_in) {
         if (tid == 0) *s_u_p = row_uniform(a.d_u, a.rng, row);
         __syncthreads();
         u_taken = true;
@@ -2794,6 +2797,17 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
         }
         __syncthreads();
       }
+    }
+    if constexpr (ONLY) {
+      // the grouped launch: every other row (or a grouped one that failed)
+      // goes to the fallback list for the next launch
+      if (tid == 0) {
+        const int i = atomicAdd(a.fb_count, 1);
+        a.fb_list[i] = row | (u_taken ? kFbUSaved : 0);
+        if (u_taken) a.fb_u[row] = *s_u_p;
+      }
+      __syncthreads();
+      continue;
     }
     // window counts (kB) and bias slots + 1 (iB) per id (:64-76)
     for (int i = tid; i < n; i += NT) {
@@ -2877,7 +2891,7 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
     radix_sort_pass<NT>(kA, iA, kB, iB, n, 16, wcnt, dbase, drun);
     radix_sort_pass<NT>(kB, iB, kA, iA, n, 24, wcnt, dbase, drun);
     // kA: ~key ascending (value descending, index ascending on ties)
-    if (tid == 0 && !u_taken) *s_u_p = row_uniform(a.d_u, a.rng, row);
+    if (tid == 0 && !u_taken) *s_u_p = u_saved ? a.fb_u[row] : row_uniform(a.d_u, a.rng, row);
     __syncthreads();
     if (P.mode == kModeFull) {
       // candidates = the whole sorted row (:96-97); values into work, ids stay in iA
@@ -2979,6 +2993,30 @@ __global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
   }
   const int count = *a.generic_count;
   generic_rows<NT, true, CLAIM>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri,
+                         glds);
+}
+
+// The grouped rows alone (a launch without the whole-row sort's code, whose
+// registers it does not share): the rows it does not finish are listed for a
+// generic_kernel launch after it.
+template <int NT, bool CLAIM>
+__global__ __launch_bounds__(NT) void generic_grouped_kernel(const GenericArgs a) {
+  constexpr int NW = NT / kWave;
+  __shared__ uint32_t wcnt[NW * 256];
+  __shared__ uint32_t dbase[256];
+  __shared__ uint32_t drun[256];
+  __shared__ int smem[NW + 4];
+  __shared__ double s_u;
+  __shared__ int s_i[4];
+  __shared__ float s_rv[NW];
+  __shared__ int s_ri[NW];
+  extern __shared__ __align__(16) unsigned char glds[];  // group_lds_bytes(V) when a.grouped
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *a.next_count = 0;
+    if (a.next_claim) *a.next_claim = 0;
+  }
+  const int count = *a.generic_count;
+  generic_rows<NT, true, CLAIM, true>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri,
                          glds);
 }
 

@@ -6,21 +6,49 @@
 namespace nls {
 
 hipError_t launch_generic(const GenericArgs& ga, const LaunchPlan& lp, hipStream_t s) {
-  if (ga.claim)
-    hipLaunchKernelGGL((generic_kernel<kGenericThreads, true>), dim3(lp.gen_blocks), dim3(kGenericThreads),
-                       ga.grouped ? lp.gen_lds : 0, s, ga);
-  else
-    hipLaunchKernelGGL((generic_kernel<kGenericThreads, false>), dim3(lp.gen_blocks), dim3(kGenericThreads),
-                       ga.grouped ? lp.gen_lds : 0, s, ga);
+  const size_t lds = ga.grouped ? lp.gen_lds : 0;
+  if (ga.fb_list) {
+    // grouped rows first; the rows they leave (fallback list) after them
+    if (ga.claim)
+      hipLaunchKernelGGL((generic_grouped_kernel<kGenericThreads, true>), dim3(lp.gen_blocks),
+                         dim3(kGenericThreads), lds, s, ga);
+    else
+      hipLaunchKernelGGL((generic_grouped_kernel<kGenericThreads, false>), dim3(lp.gen_blocks),
+                         dim3(kGenericThreads), lds, s, ga);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    GenericArgs fb = ga;
+    fb.generic_list = ga.fb_list;
+    fb.generic_count = ga.fb_count;
+    fb.next_count = ga.fb_next;
+    fb.claim = nullptr;
+    fb.next_claim = nullptr;
+    fb.fixed_list = nullptr;
+    fb.n_fixed = 0;
+    fb.fb_in = 1;
+    hipLaunchKernelGGL((generic_kernel<kGenericThreads, false>), dim3(lp.gen_blocks), dim3(kGenericThreads), lds,
+                       s, fb);
+  } else if (ga.claim) {
+    hipLaunchKernelGGL((generic_kernel<kGenericThreads, true>), dim3(lp.gen_blocks), dim3(kGenericThreads), lds,
+                       s, ga);
+  } else {
+    hipLaunchKernelGGL((generic_kernel<kGenericThreads, false>), dim3(lp.gen_blocks), dim3(kGenericThreads), lds,
+                       s, ga);
+  }
   return hipGetLastError();
 }
 
 hipError_t set_generic_attributes() {
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&generic_kernel<kGenericThreads, true>),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)group_lds_bytes(kGrpMaxV));
-  if (e != hipSuccess) return e;
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(&generic_kernel<kGenericThreads, false>),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)group_lds_bytes(kGrpMaxV));
+  const int lds = (int)group_lds_bytes(kGrpMaxV);
+  const void* fns[4] = {reinterpret_cast<const void*>(&generic_kernel<kGenericThreads, true>),
+                        reinterpret_cast<const void*>(&generic_kernel<kGenericThreads, false>),
+                        reinterpret_cast<const void*>(&generic_grouped_kernel<kGenericThreads, true>),
+                        reinterpret_cast<const void*>(&generic_grouped_kernel<kGenericThreads, false>)};
+  for (const void* f : fns) {
+    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace nls

@@ -143,7 +143,18 @@ struct GenericArgs {
   // served before the listed ones; null: none
   const int32_t* fixed_list;
   int n_fixed;
+  // Two launches (grouped rows first, then the rest): the first lists every
+  // row it does not finish in fb_list (counted in fb_count), with the row's
+  // uniform in fb_u when it drew it; the second takes that list (fb_in = 1)
+  // as its list of rows.
+  int32_t* fb_list;
+  int32_t* fb_count;
+  int32_t* fb_next;  // the next call's fallback count, zeroed by the second launch
+  double* fb_u;
+  int fb_in;
 };
+// A row of the fallback list whose uniform the grouped launch drew (fb_u).
+constexpr int32_t kFbUSaved = 1 << 30;
 
 struct StreamArgs {
   const float* logits;

@@ -205,6 +205,15 @@ def test_random_batches_every_path(pkg, torch, name):
     finally:
         s.close()
     compare_rows(x, plist, [list(h) for h in hist], biases, u, ids, dbg, name)
+    # the same batch on a fresh sampler without candidate lists (a caller's
+    # launches: full-sort rows in a grouped launch, then the rows it leaves)
+    s = pkg.BatchSampler(params, V)
+    try:
+        s.accept(hist)
+        ids_plain = s.sample(d, torch.from_numpy(u).cuda()).cpu().numpy()
+    finally:
+        s.close()
+    assert np.array_equal(ids_plain, ids), (name, np.nonzero(ids_plain != ids)[0][:10].tolist())
 
 
 def patch_designs(rng, x):
@@ -674,6 +683,12 @@ def test_workload_parity(pkg, torch, name):
     # first min(n, 64) kept candidates' ids and probabilities)
     bad = np.nonzero(ids != oc)[0]
     assert bad.size == 0, (name, bad[:10].tolist())
+    # the same call without candidate lists (the launches a caller's call
+    # makes: with full-sort rows the grouped rows in a launch of their own,
+    # then the rows it leaves)
+    ids_plain, _ = run_gpu(pkg, torch, w.logits, params, w.hist, w.u)
+    bad = np.nonzero(ids_plain != oc)[0]
+    assert bad.size == 0, (name, "without candidate lists", bad[:10].tolist())
     cand_rows = 0
     for b in range(w.B):
         r = rc[b]
