@@ -256,7 +256,8 @@ typedef struct nls_plan {
   int32_t streamed_rows;   /* rows the streaming kernel runs to the end          */
   int64_t first_unit_bytes;/* logits a non-streamed row's workgroup requests before it leaves */
   int32_t k64;             /* 1: the streaming kernel is k64_kernel (1024 threads, k <= 64) */
-  int32_t reserved;
+  int32_t walk_split;      /* 1: the full-sort rows' walks over their groups run in a launch of their own,
+                              one wave per row (more full-sort rows than CUs)    */
 } nls_plan;
 /* row_streamed: NULL or host [batch], 1 where the streaming kernel runs the row. */
 int nls_get_plan(const nls_sampler* s, nls_plan* out, int32_t* row_streamed);

@@ -86,7 +86,7 @@ class NlsPlan(ctypes.Structure):
         ("streamed_rows", ctypes.c_int32),
         ("first_unit_bytes", ctypes.c_int64),
         ("k64", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("walk_split", ctypes.c_int32),
     ]
 
 

@@ -164,9 +164,20 @@ struct nls_sampler {
   uint32_t* arrive = nullptr;
   uint64_t* rng = nullptr;
   int32_t* generic_list = nullptr;
-  int32_t* generic_count = nullptr;  // [6]: handed-on counts, claim counters, fallback counts (each by call parity)
+  int32_t* generic_count = nullptr;  // [10]: handed-on, claim, fallback, walk and search counts (each by call parity)
   int32_t* fb_list = nullptr;        // [B] the rows the grouped launch leaves to the whole-row launch
   double* fb_u = nullptr;            // [B] their uniforms, when drawn there
+  // the grouped rows' walks in a launch of their own (many full-sort rows per CU)
+  bool walk_split = false;
+  float* gt_e = nullptr;      // [B * kGrpHashCap]
+  uint32_t* gt_c = nullptr;   // [B * kGrpHashCap]
+  uint32_t* gt_k = nullptr;   // [B * kGrpHashCap]
+  int32_t* gt_n = nullptr;    // [B]
+  int32_t* w_list = nullptr;  // [B]
+  int32_t* p3_list = nullptr; // [B]
+  uint32_t* p3_rec = nullptr; // [B]
+  uint32_t* p3_key = nullptr; // [B]
+  int64_t* p3_t = nullptr;    // [B]
   int32_t* all_rows = nullptr;       // no streaming rows: 0 .. B-1, then B (the count), then a spare
   // k64_kernel with full-sort rows in the batch: the streamed rows (its
   // grid) and the others (the whole-row kernel's fixed list)
@@ -208,6 +219,15 @@ struct nls_sampler {
     dfree(generic_count);
     dfree(fb_list);
     dfree(fb_u);
+    dfree(gt_e);
+    dfree(gt_c);
+    dfree(gt_k);
+    dfree(gt_n);
+    dfree(w_list);
+    dfree(p3_list);
+    dfree(p3_rec);
+    dfree(p3_key);
+    dfree(p3_t);
     dfree(all_rows);
     dfree(k64_list);
     dfree(full_list);
@@ -629,10 +649,29 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   if ((rc = dalloc(&s->arrive, B))) return fail(rc);
   if ((rc = dalloc(&s->rng, (size_t)2 * B))) return fail(rc);
   if ((rc = dalloc(&s->generic_list, B))) return fail(rc);
-  if ((rc = dalloc(&s->generic_count, 6))) return fail(rc);  // counts, claim and fallback counters (by call parity)
+  if ((rc = dalloc(&s->generic_count, 10))) return fail(rc);  // the launches' counters (by call parity)
   if (s->plan.gen_lds > 0) {
     if ((rc = dalloc(&s->fb_list, B))) return fail(rc);
     if ((rc = dalloc(&s->fb_u, B))) return fail(rc);
+    // Many full-sort rows per CU: their walks (single-wave serial work) run
+    // side by side in a launch of their own instead of one after another on
+    // each CU, so the groups are stored between the launches.
+    int n_full = 0;
+    for (int b = 0; b < B; ++b) n_full += s->h_rp[b].mode == kModeFull ? 1 : 0;
+    if (n_full > ncu && env_int("NLS_WALK_SPLIT", 1)) {
+      const size_t cells = (size_t)B * kGrpHashCap;
+      if ((rc = dalloc(&s->gt_e, cells))) return fail(rc);
+      if ((rc = dalloc(&s->gt_c, cells))) return fail(rc);
+      if ((rc = dalloc(&s->gt_k, cells))) return fail(rc);
+      if ((rc = dalloc(&s->gt_n, B))) return fail(rc);
+      if ((rc = dalloc(&s->w_list, B))) return fail(rc);
+      if ((rc = dalloc(&s->p3_list, B))) return fail(rc);
+      if ((rc = dalloc(&s->p3_rec, B))) return fail(rc);
+      if ((rc = dalloc(&s->p3_key, B))) return fail(rc);
+      if ((rc = dalloc(&s->p3_t, B))) return fail(rc);
+      s->walk_split = true;
+      s->plan.walk_blocks = std::min(B, 8 * ncu);
+    }
   }
   if (s->plan.no_stream) {
     std::vector<int32_t> rows((size_t)B + 2);
@@ -688,7 +727,7 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
     return fail(hip_fail(e, "clear counters"));
   if ((e = hipMemsetAsync(s->done, 0, sizeof(uint32_t), st)) != hipSuccess)
     return fail(hip_fail(e, "clear counters"));
-  if ((e = hipMemsetAsync(s->generic_count, 0, sizeof(int32_t) * 6, st)) != hipSuccess)
+  if ((e = hipMemsetAsync(s->generic_count, 0, sizeof(int32_t) * 10, st)) != hipSuccess)
     return fail(hip_fail(e, "clear counters"));
   if ((e = hipStreamSynchronize(st)) != hipSuccess) return fail(hip_fail(e, "sync"));
   *out = s;
@@ -866,14 +905,34 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   ga.out = d_out;
   ga.dbg = dp;
   ga.grouped = s->plan.gen_lds > 0 ? 1 : 0;
+  // every call zeroes the other parity's counters of the split launches
+  // (whichever of its kernels runs), so calls of either form can follow
+  if (s->fb_list) ga.fb_next = s->generic_count + 4 + (s->parity ^ 1);
+  if (s->walk_split) {
+    ga.w_next = s->generic_count + 6 + (s->parity ^ 1);
+    ga.p3_next = s->generic_count + 8 + (s->parity ^ 1);
+  }
   if (ga.grouped && s->fb_list && !dp.cand_ids && !dp.cand_probs) {
     // the grouped rows in a launch of their own, then the rows it leaves
     // (candidate lists are written by the whole-row sort, so a call asking
     // for them keeps the one launch, where a grouped row is sorted as well)
     ga.fb_list = s->fb_list;
     ga.fb_count = s->generic_count + 4 + s->parity;
-    ga.fb_next = s->generic_count + 4 + (s->parity ^ 1);
     ga.fb_u = s->fb_u;
+    if (s->walk_split) {
+      ga.walk_split = 1;
+      ga.gt_e = s->gt_e;
+      ga.gt_c = s->gt_c;
+      ga.gt_k = s->gt_k;
+      ga.gt_n = s->gt_n;
+      ga.w_list = s->w_list;
+      ga.w_count = s->generic_count + 6 + s->parity;
+      ga.p3_list = s->p3_list;
+      ga.p3_count = s->generic_count + 8 + s->parity;
+      ga.p3_rec = s->p3_rec;
+      ga.p3_key = s->p3_key;
+      ga.p3_t = s->p3_t;
+    }
   }
   LaunchPlan lp = s->plan;
   a.gen_inline = s->gen_inline;
@@ -968,6 +1027,7 @@ int nls_get_plan(const nls_sampler* s, nls_plan* out, int32_t* row_streamed) {
   out->slices = s->S;
   out->generic_launch = s->gen_inline ? 0 : 1;
   out->k64 = s->plan.k64 ? 1 : 0;
+  out->walk_split = s->walk_split ? 1 : 0;
   // a workgroup requests its first unit (kStreamVec4 float4 per thread)
   // before it reads the row's constants
   out->first_unit_bytes = (s->plan.lds > 0 && !s->plan.no_stream)

@@ -603,6 +603,15 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
   }
 }
 
+// The next call's counters of the whole-row launches (each call's launches
+// count in one parity's set and zero the other's, whichever launches the
+// call makes).
+__device__ __forceinline__ void zero_next_counters(const GenericArgs& g) {
+  if (g.fb_next) store_agent(g.fb_next, 0);
+  if (g.w_next) store_agent(g.w_next, 0);
+  if (g.p3_next) store_agent(g.p3_next, 0);
+}
+
 template <int NT, bool GROUPED = false, bool CLAIM = false, bool ONLY = false>
 __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int nw, int count, uint32_t* wcnt,
                                              uint32_t* dbase, uint32_t* drun, int* smem, double* s_u_p,
@@ -1940,6 +1949,7 @@ void stream_kernel(const StreamArgs a) {
       if (threadIdx.x == 0) {
         store_agent(a.done, 0u);
         store_agent(a.ga.next_count, 0);
+        zero_next_counters(a.ga);
       }
       uint32_t* dl = reinterpret_cast<uint32_t*>(lds);
       generic_rows<NT>(a.ga, 0, 1, count, shist, dl, dl + 256, smem, &s_u, reinterpret_cast<int*>(dl + 512),
@@ -2143,7 +2153,11 @@ struct GroupOut {
   float total;
 };
 
-template <int NT>
+// STAGE 0: the whole grouped path.  STAGE 1 (the grouped launch): the same,
+// except that with a.walk_split the row's groups are stored once sorted and
+// the row is left for the walk launch (ok = 2).  STAGE 3 (the search launch):
+// the patch table, then the search for the member a.p3_* names.
+template <int NT, int STAGE = 0>
 __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, const RowParams& P, double u,
                                 const GroupLds& L, int* smem) {
   constexpr int NW = NT / kWave;
@@ -2167,11 +2181,13 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   res.n = 0;
   res.total = 0.0f;
 
-  NLS_GSTAMP(row, 0);
+  if constexpr (STAGE != 3) NLS_GSTAMP(row, 0);
   for (int i = tid; i < nw; i += NT) L.bitmap[i] = 0u;
-  for (int i = tid; i < kGrpHashCap; i += NT) {
-    L.hkey[i] = kGrpEmpty;
-    L.hcnt[i] = 0u;
+  if constexpr (STAGE != 3) {
+    for (int i = tid; i < kGrpHashCap; i += NT) {
+      L.hkey[i] = kGrpEmpty;
+      L.hcnt[i] = 0u;
+    }
   }
   for (int i = tid; i < kGrpPatchCap; i += NT) {
     L.pcnt[i] = 0u;
@@ -2253,11 +2269,20 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     L.pfin[sl] = v * P.invT;  // (:80-81)
   }
   __syncthreads();
-  NLS_GSTAMP(row, 1);
+  if constexpr (STAGE != 3) NLS_GSTAMP(row, 1);
   const bool vec = (V % 4 == 0) && ((reinterpret_cast<uintptr_t>(src) & 15) == 0);
   const float4* __restrict__ src4 = reinterpret_cast<const float4*>(src);
   const float invT = P.invT;
   const int V4 = V >> 2;
+  // the drawn member: its group's value and count record, its rank among them
+  float vg = 0.0f;
+  int64_t t = 0;
+  uint64_t grec = 0;
+  if constexpr (STAGE == 3) {
+    vg = key2f(a.p3_key[row]);
+    grec = a.p3_rec[row];
+    t = a.p3_t[row];
+  } else {
   // ---- the row maximum (:53) and the values that can move the sum ----
   // Counting needs the maximum: a value counts when fl(v - mx) >= kGroupFloor.
   // One fused pass counts every value within kGroupFloor of a running
@@ -2458,6 +2483,22 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
     atomicAdd(&s_held, (unsigned long long)group_count(e));
   }
   __syncthreads();
+  if constexpr (STAGE == 1) {
+    if (a.walk_split) {
+      // the groups for the walk launch
+      const size_t o = (size_t)row * kGrpHashCap;
+      for (int g = tid; g < G; g += NT) {
+        const uint64_t e = L.gsort[g];
+        a.gt_e[o + g] = ge[g];
+        a.gt_c[o + g] = (uint32_t)e;
+        a.gt_k[o + g] = ~(uint32_t)(e >> 32);
+      }
+      if (tid == 0) a.gt_n[row] = G | (s_held == (unsigned long long)V ? kGtComplete : 0);
+      res.ok = 2;
+      __syncthreads();
+      return res;
+    }
+  }
   // wave 0 walks the groups (its lanes look ahead 64 groups at a time)
   if (tid < kWave) {
     float s = 0.0f;
@@ -2504,13 +2545,15 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   __syncthreads();
   NLS_GSTAMP(row, 6);
   if (s_draw.status != kGroupOk) return res;
+  vg = key2f(~(uint32_t)(L.gsort[s_g] >> 32));
+  t = s_t;
+  grec = L.gsort[s_g];
+  }
   // ---- the drawn candidate: the t-th lowest index holding value vg ----
   // Blocks of 64 lanes x W values (W = 4 with 16-byte loads): each wave
   // counts the members of its blocks (counts kept in the patch table's
   // count/bias arrays, free by now), then wave 0 finds the block holding the
   // t-th member and the lane and element inside it.
-  const float vg = key2f(~(uint32_t)(L.gsort[s_g] >> 32));
-  const int64_t t = s_t;
   const int wv = tid >> 6;
   uint32_t* bcnt = L.pcnt;  // pcnt and pbias are adjacent: 2 * kGrpPatchCap entries
   auto final_at = [&](int i, float x) -> float {
@@ -2567,7 +2610,6 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   // c members, else from the row's end for the (c - 1 - t)-th member from the
   // top (on average a quarter of the row is read).  The patched members go
   // in first.
-  const uint64_t grec = L.gsort[s_g];
   if ((uint32_t)grec & kGrpOne) {
     // a value that occurs once: its member was kept when it was counted
     if (tid == 0) s_id = (int)((uint32_t)grec & ~kGrpOne);
@@ -2654,8 +2696,10 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   if (s_id < 0) return res;
   res.ok = 1;
   res.id = s_id;
-  res.n = (int)s_draw.n;
-  res.total = s_draw.total;
+  if constexpr (STAGE != 3) {
+    res.n = (int)s_draw.n;
+    res.total = s_draw.total;
+  }
   __syncthreads();
   return res;
 }
@@ -2779,7 +2823,18 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
         if (tid == 0) *s_u_p = row_uniform(a.d_u, a.rng, row);
         __syncthreads();
         u_taken = true;
-        gout = grouped_row<NT>(a, row, P, *s_u_p, group_lds(glds, (int)((a.V + 31) >> 5)), smem);
+        gout = grouped_row<NT, ONLY ? 1 : 0>(a, row, P, *s_u_p, group_lds(glds, (int)((a.V + 31) >> 5)), smem);
+        if constexpr (ONLY) {
+          if (gout.ok == 2) {
+            // groups stored: the walk launch takes the row, with its uniform
+            if (tid == 0) {
+              a.fb_u[row] = *s_u_p;
+              a.w_list[atomicAdd(a.w_count, 1)] = row;
+            }
+            __syncthreads();
+            continue;
+          }
+        }
         if (gout.ok) {
           if (tid == 0) {
             a.out[row] = gout.id;
@@ -2990,6 +3045,7 @@ __global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     *a.next_count = 0;
     if (a.next_claim) *a.next_claim = 0;
+    zero_next_counters(a);
   }
   const int count = *a.generic_count;
   generic_rows<NT, true, CLAIM>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri,
@@ -3014,10 +3070,118 @@ __global__ __launch_bounds__(NT) void generic_grouped_kernel(const GenericArgs a
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     *a.next_count = 0;
     if (a.next_claim) *a.next_claim = 0;
+    zero_next_counters(a);
   }
   const int count = *a.generic_count;
   generic_rows<NT, true, CLAIM, true>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri,
                          glds);
+}
+
+
+// A row that leaves the grouped path for the whole-row launch, its uniform
+// kept (fb_u holds it).
+__device__ __forceinline__ void push_fallback(const GenericArgs& a, int row) {
+  a.fb_list[atomicAdd(a.fb_count, 1)] = row | kFbUSaved;
+}
+
+// The walks of the rows the grouped launch stored (a.w_list), one wave per
+// row: the softmax sum, top-p, min-p, total and the draw over the groups
+// (nls_grouped.h), then the drawn group.  A group of one candidate names it;
+// otherwise the row is listed for the search launch.  The groups are read
+// into LDS first (kGrpHashCap exponentials and counts).
+template <int NT>  // one wave: NT = kWave
+__global__ __launch_bounds__(NT) void walk_kernel(const GenericArgs a) {
+  extern __shared__ __align__(16) unsigned char wlds[];
+  float* ge = reinterpret_cast<float*>(wlds);
+  uint32_t* gc = reinterpret_cast<uint32_t*>(ge + kGrpHashCap);
+  const int lane = lane_id();
+  if (blockIdx.x == 0 && lane == 0) *a.w_next = 0;
+  const int count = *a.w_count;
+  const int V = (int)a.V;
+  for (int li = blockIdx.x; li < count; li += gridDim.x) {
+    const int row = a.w_list[li];
+    const RowParams P = a.rp[row];
+    const double u = a.fb_u[row];
+    const int gn = a.gt_n[row];
+    const int G = gn & ~kGtComplete;
+    const bool complete = (gn & kGtComplete) != 0;
+    const size_t o = (size_t)row * kGrpHashCap;
+    for (int g = lane; g < G; g += kWave) {
+      ge[g] = a.gt_e[o + g];
+      gc[g] = group_count((uint64_t)a.gt_c[o + g]);
+    }
+    __syncthreads();  // (one wave: orders the LDS writes before the reads)
+    float s = 0.0f;
+    if (!group_sum(ge, gc, G, s)) {
+      if (lane == 0) push_fallback(a, row);
+      continue;
+    }
+    NLS_GSTAMP(row, 5);
+    for (int g = lane; g < G; g += kWave) ge[g] = ge[g] / s;  // (:57)
+    __syncthreads();  // (one wave: orders the LDS writes before the reads)
+    const GroupDraw dr = group_cut_draw(ge, gc, G, complete, a.V, P.topp_active != 0, P.topP,
+                                        P.minp_active != 0, P.minP32, u);
+    if (dr.status != kGroupOk) {
+      if (lane == 0) push_fallback(a, row);
+      continue;
+    }
+    // the drawn group: the first g with gc[0] + ... + gc[g] > pos, 64 groups
+    // per step
+    int g = 0;
+    int64_t pos = dr.pos;
+    for (int base = 0; base < G; base += kWave) {
+      const int c = base + lane < G ? (int)gc[base + lane] : 0;
+      const int incl = wave_incl_scan(c);
+      const int tot = __shfl(incl, kWave - 1, kWave);
+      if (pos < (int64_t)tot || base + kWave >= G) {
+        const uint64_t past = __ballot((int64_t)incl > pos);
+        const int hl = past ? __ffsll((unsigned long long)past) - 1 : min(G - base, kWave) - 1;
+        g = base + hl;
+        pos -= (int64_t)(__shfl(incl, hl, kWave) - __shfl(c, hl, kWave));
+        break;
+      }
+      pos -= tot;
+    }
+    NLS_GSTAMP(row, 6);
+    if (lane == 0) {
+      const uint32_t rec = a.gt_c[o + g];
+      if (a.dbg.n) a.dbg.n[row] = (int)dr.n;
+      if (a.dbg.ncand) a.dbg.ncand[row] = V;
+      if (a.dbg.total) a.dbg.total[row] = dr.total;
+      if (a.dbg.path) a.dbg.path[row] = 3;
+      if (rec & kGrpOne) {
+        // a value that occurs once: its member was kept when it was counted
+        a.out[row] = (int32_t)(rec & ~kGrpOne);
+      } else {
+        a.p3_rec[row] = rec;
+        a.p3_key[row] = a.gt_k[o + g];
+        a.p3_t[row] = pos;
+        a.p3_list[atomicAdd(a.p3_count, 1)] = row;
+      }
+    }
+  }
+}
+
+// The drawn members the walk launch could not name (a.p3_list): the row's
+// patch table again, then the member search (grouped_row's last step).
+template <int NT>
+__global__ __launch_bounds__(NT) void member_kernel(const GenericArgs a) {
+  __shared__ int smem[NT / kWave + 4];
+  extern __shared__ __align__(16) unsigned char glds[];  // group_lds_bytes(V)
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.p3_next = 0;
+  const int count = *a.p3_count;
+  for (int li = blockIdx.x; li < count; li += gridDim.x) {
+    const int row = a.p3_list[li];
+    const RowParams P = a.rp[row];
+    const GroupOut r = grouped_row<NT, 3>(a, row, P, 0.0, group_lds(glds, (int)((a.V + 31) >> 5)), smem);
+    if (threadIdx.x == 0) {
+      if (r.ok)
+        a.out[row] = r.id;
+      else
+        push_fallback(a, row);
+    }
+    __syncthreads();
+  }
 }
 
 }  // namespace nls

@@ -1,5 +1,7 @@
 // generic_kernel (full-sort rows and rows the streaming kernel hands on; see
 // nls_device.h) and its launcher.
+#include <algorithm>
+
 #include "nls_device.h"
 #include "nls_launch.h"
 
@@ -17,6 +19,14 @@ hipError_t launch_generic(const GenericArgs& ga, const LaunchPlan& lp, hipStream
                          dim3(kGenericThreads), lds, s, ga);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (ga.walk_split) {
+      // the stored rows' walks, one wave each; then the member searches
+      const int wgrid = std::max(1, std::min(lp.walk_blocks, 65535));
+      hipLaunchKernelGGL((walk_kernel<kWave>), dim3(wgrid), dim3(kWave), (size_t)kGrpHashCap * 8, s, ga);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      hipLaunchKernelGGL((member_kernel<kGenericThreads>), dim3(lp.gen_blocks), dim3(kGenericThreads), lds, s, ga);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     GenericArgs fb = ga;
     fb.generic_list = ga.fb_list;
     fb.generic_count = ga.fb_count;
@@ -40,10 +50,11 @@ hipError_t launch_generic(const GenericArgs& ga, const LaunchPlan& lp, hipStream
 
 hipError_t set_generic_attributes() {
   const int lds = (int)group_lds_bytes(kGrpMaxV);
-  const void* fns[4] = {reinterpret_cast<const void*>(&generic_kernel<kGenericThreads, true>),
+  const void* fns[5] = {reinterpret_cast<const void*>(&generic_kernel<kGenericThreads, true>),
                         reinterpret_cast<const void*>(&generic_kernel<kGenericThreads, false>),
                         reinterpret_cast<const void*>(&generic_grouped_kernel<kGenericThreads, true>),
-                        reinterpret_cast<const void*>(&generic_grouped_kernel<kGenericThreads, false>)};
+                        reinterpret_cast<const void*>(&generic_grouped_kernel<kGenericThreads, false>),
+                        reinterpret_cast<const void*>(&member_kernel<kGenericThreads>)};
   for (const void* f : fns) {
     const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;

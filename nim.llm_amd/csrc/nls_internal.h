@@ -152,9 +152,31 @@ struct GenericArgs {
   int32_t* fb_next;  // the next call's fallback count, zeroed by the second launch
   double* fb_u;
   int fb_in;
+  // The grouped rows' walks in a launch of their own (walk_split = 1): the
+  // grouped launch stores each row's groups (gt_*, kGrpHashCap per row) and
+  // lists the row in w_list; the walk launch (one wave per row) lists the
+  // rows whose drawn member must be searched for in p3_list, with the group's
+  // count record and value key and the member's rank; the search launch
+  // finishes them.  Rows that fail any step go to the fallback list.
+  int walk_split;
+  float* gt_e;      // [B][kGrpHashCap] the groups' exponentials
+  uint32_t* gt_c;   // [B][kGrpHashCap] their count records (count, or kGrpOne | index)
+  uint32_t* gt_k;   // [B][kGrpHashCap] their value keys
+  int32_t* gt_n;    // [B] the groups, | kGtComplete when they hold every candidate
+  int32_t* w_list;
+  int32_t* w_count;
+  int32_t* w_next;
+  int32_t* p3_list;
+  int32_t* p3_count;
+  int32_t* p3_next;
+  uint32_t* p3_rec;  // [B] the drawn group's count record
+  uint32_t* p3_key;  // [B] its value key
+  int64_t* p3_t;     // [B] the drawn member's rank among the group's members
 };
 // A row of the fallback list whose uniform the grouped launch drew (fb_u).
 constexpr int32_t kFbUSaved = 1 << 30;
+// gt_n: the groups hold every candidate of the row.
+constexpr int32_t kGtComplete = 1 << 30;
 
 struct StreamArgs {
   const float* logits;
@@ -220,6 +242,7 @@ struct LaunchPlan {
   int gen_blocks;
   size_t gen_lds;  // dynamic LDS bytes of the whole-row kernel (grouped path), 0 = none
   bool no_stream;  // no row is a streaming row: the whole-row kernel alone, over every row
+  int walk_blocks;  // walk launch: one-wave workgroups (the grouped rows' walks)
 };
 
 hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const LaunchPlan& lp,

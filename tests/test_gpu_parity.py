@@ -402,6 +402,99 @@ def test_mixed_batch_consecutive_calls(pkg, torch):
         s.close()
 
 
+def _walk_split_batch(B, V, rng):
+    """A batch with more full-sort rows than an MI355X has CUs: rows on a 0.25
+    grid (heavy ties: drawn groups of many members), some with distinct values
+    (groups of one, or more distinct values than the group table holds), and
+    cutoffs that need candidates below the grouped path's floor."""
+    plist, hists, biases = [], [], []
+    for b in range(B):
+        kind = b % 10
+        d = dict(temperature=1.0, topK=0, topP=1.0, minP=0.0, repeatPenalty=1.0, repeatLastN=0,
+                 presencePenalty=0.0, frequencyPenalty=0.0, seed=4)
+        h, bias = [], {}
+        if kind == 0:
+            d.update(temperature=0.0)
+        elif kind == 1:
+            d.update(topK=20)
+        elif kind == 2:
+            d.update(topP=0.9)
+        elif kind == 3:
+            d.update(temperature=0.7, minP=0.05)
+        elif kind == 4:
+            d.update(repeatPenalty=1.3, presencePenalty=0.5, repeatLastN=16)
+            h = [int(i) for i in rng.integers(0, V, 24)]
+            bias = {int(rng.integers(0, V)): 2.5, int(rng.integers(0, V)): -math.inf}
+        elif kind == 5:  # top-p just below 1 at a low temperature: the cut may need every candidate
+            d.update(temperature=0.5, topP=1.0 - 1e-9)
+        elif kind == 7:
+            d.update(topP=0.5, minP=0.1)
+        elif kind == 8:
+            d.update(temperature=2.0, topP=0.95)
+        plist.append(d)
+        hists.append(h)
+        biases.append(bias)
+    return plist, hists, biases
+
+
+def test_grouped_walk_split_consecutive_calls(pkg, torch, monkeypatch):
+    """More full-sort rows than CUs: the grouped launch stores each row's
+    groups, a launch of one-wave workgroups walks them (softmax sum, top-p,
+    min-p, total, draw; sampler.nim:101-121) and a third searches the drawn
+    member; rows any step cannot finish go to the whole-row launch with their
+    uniform.  One sampler, five calls in a row, alternating between calls
+    without candidate lists (the split launches) and calls with them (one
+    launch): every row of every call against the oracle.  The same batch with
+    the split switched off (NLS_WALK_SPLIT=0) gives the same ids."""
+    B, V = 640, 32000
+    rng = np.random.default_rng(91)
+    plist, hists, biases = _walk_split_batch(B, V, rng)
+    params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
+    calls = []
+    for call in range(5):
+        x = (np.round(rng.standard_normal((B, V)) * 8.0) / 4.0).astype(np.float32)
+        x[9::10] = (rng.standard_normal((len(range(9, B, 10)), V)) * 3.0).astype(np.float32)
+        calls.append((x, rng.random(B)))
+    s = pkg.BatchSampler(params, V)
+    try:
+        plan, _ = s.plan()
+        say(f"[walk_split_calls] B={B} V={V} walk_split={plan.walk_split}")
+        assert plan.walk_split == 1
+        for b in range(B):
+            if hists[b]:
+                s.accept(hists[b], row=b)
+        first = None
+        for call, (x, u) in enumerate(calls):
+            d = torch.from_numpy(x).cuda()
+            du = torch.from_numpy(u).cuda()
+            if call % 2:
+                ids, dbg = s.sample(d, du, debug_cap=64)
+                dbg = {k: v.cpu().numpy() for k, v in dbg.items()}
+            else:
+                ids, dbg = s.sample(d, du), None
+            ids = ids.cpu().numpy()
+            torch.cuda.synchronize()
+            say(f"[walk_split_calls] call {call} debug={dbg is not None}")
+            compare_rows(x, plist, hists, biases, u, ids, dbg, f"call {call}")
+            if call == 0:
+                first = ids
+    finally:
+        s.close()
+    monkeypatch.setenv("NLS_WALK_SPLIT", "0")
+    s = pkg.BatchSampler(params, V)
+    try:
+        plan, _ = s.plan()
+        assert plan.walk_split == 0
+        for b in range(B):
+            if hists[b]:
+                s.accept(hists[b], row=b)
+        x, u = calls[0]
+        ids = s.sample(torch.from_numpy(x).cuda(), torch.from_numpy(u).cuda()).cpu().numpy()
+    finally:
+        s.close()
+    assert np.array_equal(ids, first)
+
+
 @pytest.mark.parametrize("B", [12, 264])
 def test_greedy_rows_resting_on_patched_ids_or_neg_inf(pkg, torch, B):
     """Greedy rows (sampler.nim:45-49, :77-78) whose argmax rests on -inf or
