@@ -919,6 +919,25 @@ def phase_stamps(args):
             "pass 3: the drawn member": (G[:, 7] - G[:, 6]) / 100.0,
             "row total": (G[:, 7] - G[:, 0]) / 100.0,
         }
+        if plan.walk_split:
+            # three launches: the groups stored (slots 0-4), the walks (8, 5,
+            # 6), the member search (9, 7); each launch's rows start after
+            # the previous launch's last row
+            grows = {
+                "start after the first grouped row": (G[:, 0] - g0) / 100.0,
+                "zero tables, patch table": (G[:, 1] - G[:, 0]) / 100.0,
+                "pass 1: row maximum": (G[:, 2] - G[:, 1]) / 100.0,
+                "pass 2: count distinct values": (G[:, 3] - G[:, 2]) / 100.0,
+                "sort the groups, store them": (G[:, 4] - G[:, 3]) / 100.0,
+                "walk launch: start after the first walk": (G[:, 8] - G[gok, 8].min()) / 100.0,
+                "walk launch: softmax sum over groups": (G[:, 5] - G[:, 8]) / 100.0,
+                "walk launch: top-p / min-p / draw over groups": (G[:, 6] - G[:, 5]) / 100.0,
+                "search launch: start after the first search": (G[:, 9] - G[gok, 9].min()) / 100.0,
+                "search launch: patch table, the drawn member": (G[:, 7] - G[:, 9]) / 100.0,
+            }
+            print(f"grouped launch span {(G[gok, 4].max() - g0) / 100.0:.2f} us; walk launch span "
+                  f"{(G[gok, 6].max() - G[gok, 8].min()) / 100.0:.2f} us; search launch span "
+                  f"{(G[gok, 7].max() - G[gok, 9].min()) / 100.0:.2f} us")
         print(f"# grouped path (whole-row kernel) phases, {int(gok.sum())} rows")
         print("| Phase | median us | p10 | p90 |")
         print("|---|---|---|---|")

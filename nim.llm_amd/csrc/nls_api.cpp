@@ -671,6 +671,8 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
       if ((rc = dalloc(&s->p3_t, B))) return fail(rc);
       s->walk_split = true;
       s->plan.walk_blocks = std::min(B, 8 * ncu);
+      s->plan.member_blocks = std::min(B, 2 * ncu);
+      s->plan.member_lds = group_patch_lds_bytes(vocab);
     }
   }
   if (s->plan.no_stream) {

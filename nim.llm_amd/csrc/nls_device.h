@@ -2182,6 +2182,7 @@ __device__ __forceinline__ GroupOut grouped_row(const GenericArgs& a, int row, c
   res.total = 0.0f;
 
   if constexpr (STAGE != 3) NLS_GSTAMP(row, 0);
+  if constexpr (STAGE == 3) NLS_GSTAMP(row, 9);
   for (int i = tid; i < nw; i += NT) L.bitmap[i] = 0u;
   if constexpr (STAGE != 3) {
     for (int i = tid; i < kGrpHashCap; i += NT) {
@@ -3100,6 +3101,7 @@ __global__ __launch_bounds__(NT) void walk_kernel(const GenericArgs a) {
   const int V = (int)a.V;
   for (int li = blockIdx.x; li < count; li += gridDim.x) {
     const int row = a.w_list[li];
+    NLS_GSTAMP(row, 8);
     const RowParams P = a.rp[row];
     const double u = a.fb_u[row];
     const int gn = a.gt_n[row];
@@ -3152,6 +3154,8 @@ __global__ __launch_bounds__(NT) void walk_kernel(const GenericArgs a) {
       if (rec & kGrpOne) {
         // a value that occurs once: its member was kept when it was counted
         a.out[row] = (int32_t)(rec & ~kGrpOne);
+        NLS_GSTAMP(row, 9);
+        NLS_GSTAMP(row, 7);
       } else {
         a.p3_rec[row] = rec;
         a.p3_key[row] = a.gt_k[o + g];
@@ -3164,8 +3168,11 @@ __global__ __launch_bounds__(NT) void walk_kernel(const GenericArgs a) {
 
 // The drawn members the walk launch could not name (a.p3_list): the row's
 // patch table again, then the member search (grouped_row's last step).
+// Two workgroups per CU: the launch carries only the patch table's LDS
+// (group_patch_lds_bytes) and the registers are held to 64.
 template <int NT>
-__global__ __launch_bounds__(NT) void member_kernel(const GenericArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2 * NT / kWave / 4))) void member_kernel(
+    const GenericArgs a) {
   __shared__ int smem[NT / kWave + 4];
   extern __shared__ __align__(16) unsigned char glds[];  // group_lds_bytes(V)
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.p3_next = 0;

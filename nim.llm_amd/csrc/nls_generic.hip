@@ -24,7 +24,8 @@ hipError_t launch_generic(const GenericArgs& ga, const LaunchPlan& lp, hipStream
       const int wgrid = std::max(1, std::min(lp.walk_blocks, 65535));
       hipLaunchKernelGGL((walk_kernel<kWave>), dim3(wgrid), dim3(kWave), (size_t)kGrpHashCap * 8, s, ga);
       if ((e = hipGetLastError()) != hipSuccess) return e;
-      hipLaunchKernelGGL((member_kernel<kGenericThreads>), dim3(lp.gen_blocks), dim3(kGenericThreads), lds, s, ga);
+      hipLaunchKernelGGL((member_kernel<kGenericThreads>), dim3(lp.member_blocks), dim3(kGenericThreads),
+                         lp.member_lds, s, ga);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     GenericArgs fb = ga;

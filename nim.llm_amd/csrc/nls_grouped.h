@@ -200,6 +200,11 @@ NLS_RD GroupDraw group_cut_draw(const float* pg, const uint32_t* gc, int G, bool
   out.total = 0.0f;
   int budget = kGroupBudget;
   int64_t n = V;
+  // The total (:115-116) adds the same probabilities in the same order from
+  // the same 0 as the top-p running sum: where top-p sets n and min-p keeps
+  // it, the running sum at the cut is the total.
+  bool cut_sum = false;
+  float cum_at_cut = 0.0f;
   // top-p (:103-108): n = first i + 1 with (double)cum >= topP
   if (topp_active) {
     float cum = 0.0f;
@@ -218,6 +223,8 @@ NLS_RD GroupDraw group_cut_draw(const float* pg, const uint32_t* gc, int G, bool
       if (j) {
         n = pos + j;
         found = true;
+        cut_sum = true;
+        cum_at_cut = cum;
         break;
       }
       pos += gc[g];
@@ -246,11 +253,16 @@ NLS_RD GroupDraw group_cut_draw(const float* pg, const uint32_t* gc, int G, bool
       return out;
     }
     int64_t m = cnt < 1 ? 1 : cnt;
-    n = m < n ? m : n;
+    if (m < n) {
+      n = m;
+      cut_sum = false;
+    }
   }
   // total (:115-116) over the first n candidates
   float total = 0.0f;
-  {
+  if (cut_sum) {
+    total = cum_at_cut;
+  } else {
     int64_t pos = 0;
     bool more = true;
     for (int g = 0; g < G && pos < n; ++g) {

@@ -114,6 +114,14 @@ inline size_t group_lds_bytes(int64_t V) {
   return nw * 8 + (size_t)kGrpPatchCap * 16 + (size_t)kGrpHashCap * 16;
 }
 
+// The member search's dynamic LDS: the bitmap, its prefix counts and the
+// patch table (the front of group_lds_bytes' layout).
+inline size_t group_patch_lds_bytes(int64_t V) {
+  if (V < 1 || V > kGrpMaxV) return 0;
+  const size_t nw = (size_t)((V + 31) / 32);
+  return nw * 8 + (size_t)kGrpPatchCap * 16;
+}
+
 struct GenericArgs {
   const float* logits;
   int64_t V;
@@ -243,6 +251,8 @@ struct LaunchPlan {
   size_t gen_lds;  // dynamic LDS bytes of the whole-row kernel (grouped path), 0 = none
   bool no_stream;  // no row is a streaming row: the whole-row kernel alone, over every row
   int walk_blocks;  // walk launch: one-wave workgroups (the grouped rows' walks)
+  int member_blocks;   // search launch: workgroups (two per CU)
+  size_t member_lds;   // and their dynamic LDS (group_patch_lds_bytes)
 };
 
 hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const LaunchPlan& lp,
