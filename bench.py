@@ -864,6 +864,45 @@ def phase_stamps(args):
     G = buf.reshape(4096, 16)[:w.B].astype(np.int64).copy()
     plan, _ = s.plan()
     s.close()
+    if plan.floor_slices > 0:
+        # floor_kernel, by workgroup (row * S + slice): 0 start, 1 row constants,
+        # 2 patch table, 3 slice maximum, 4 kept values, 5 published; the
+        # merging workgroup 6 records read, 7 merged, 8 sorted, 9 tail, 10 the
+        # values merged
+        S = plan.floor_slices
+        buf[:] = 0
+        if L.nls_floor_stamps(buf.ctypes.data_as(ctypes.c_void_p)) != 0:
+            raise SystemExit("nls_floor_stamps failed")
+        F = buf.reshape(4096, 16)[:w.B * S].astype(np.int64).copy()
+        ok = (F[:, 0] > 0) & (F[:, 5] > 0)
+        mg = ok & (F[:, 9] > 0) & (F[:, 9] > F[:, 5])
+        t0 = F[ok, 0].min()
+        us = lambda d: d / 100.0  # 100 MHz counter
+        rows = {"workgroup start after the first": us(F[:, 0] - t0),
+                "row constants in": us(F[:, 1] - F[:, 0]),
+                "patch table": us(F[:, 2] - F[:, 1]),
+                "slice maximum (slice in)": us(F[:, 3] - F[:, 2]),
+                "kept values": us(F[:, 4] - F[:, 3]),
+                "published, arrival counted": us(F[:, 5] - F[:, 4]),
+                "slice total": us(F[:, 5] - F[:, 0])}
+        print(f"# floor_kernel phases, workload {args.workload} (B={w.B} V={w.V}, {S} slices per row), "
+              f"last of {args.steps} calls; {int(ok.sum())} workgroups, {int(mg.sum())} merges")
+        print("| Phase | median us | p10 | p90 |")
+        print("|---|---|---|---|")
+        for name, v in rows.items():
+            v = v[ok]
+            print(f"| {name} | {np.median(v):.2f} | {np.percentile(v, 10):.2f} | {np.percentile(v, 90):.2f} |")
+        mrows = {"merge: slice records read": us(F[:, 6] - F[:, 5]),
+                 "merge: values gathered": us(F[:, 7] - F[:, 6]),
+                 "merge: sort": us(F[:, 8] - F[:, 7]),
+                 "merge: softmax, top-p, min-p, draw": us(F[:, 9] - F[:, 8]),
+                 "merging workgroup total": us(F[:, 9] - F[:, 0])}
+        for name, v in mrows.items():
+            v = v[mg]
+            print(f"| {name} | {np.median(v):.2f} | {np.percentile(v, 10):.2f} | {np.percentile(v, 90):.2f} |")
+        print(f"values merged per row (median / max): {np.median(F[mg, 10]):.0f} / {F[mg, 10].max()}")
+        print(f"kernel span (first start to last end): {us(F[mg, 9].max() - t0):.2f} us")
+        return
     if not plan.k64:
         # stream_kernel rows (each instance's unit keeps its own stamps): 0
         # start, 1 stream start, 2 stream end, 3 members start, 4 members
@@ -1181,10 +1220,20 @@ def main():
     s_avg, s_med = stats(ev_s)
     sname = "k64_kernel" if plan.k64 else "stream_kernel"
     kernels = {}
-    if plan.streamed_rows > 0:  # (a batch of full sorts only runs the whole-row kernel alone)
+    if plan.floor_slices > 0:
+        # (a batch of full sorts only, split over slices: floor_kernel reads every
+        # row; the whole-row kernel after it takes the rows floor_kernel leaves)
+        kernels["floor_kernel"] = {"rows": B, "algorithmic_bytes_per_launch": pipe_bytes,
+                                   "event_pair_avg_us": s_avg * 1e3, "event_pair_median_us": s_med * 1e3}
+        generic_bytes = 0.0
+    elif plan.streamed_rows > 0:  # (a batch of full sorts only runs the whole-row kernel alone)
         kernels[sname] = {"rows": int(sum(streamed)), "algorithmic_bytes_per_launch": stream_bytes,
                           "event_pair_avg_us": s_avg * 1e3, "event_pair_median_us": s_med * 1e3}
-    if ev_g:
+    if ev_g and plan.floor_slices > 0:
+        g_avg, g_med = stats(ev_g)
+        kernels["generic_kernel"] = {"rows": 0, "algorithmic_bytes_per_launch": 0.0,
+                                     "event_pair_avg_us": g_avg * 1e3, "event_pair_median_us": g_med * 1e3}
+    elif ev_g:
         g_avg, g_med = stats(ev_g)
         kernels["generic_kernel"] = {"rows": int(B - sum(streamed)), "algorithmic_bytes_per_launch": generic_bytes,
                                      "event_pair_avg_us": g_avg * 1e3, "event_pair_median_us": g_med * 1e3}
@@ -1193,7 +1242,7 @@ def main():
     # whole-row kernel alone) the kernel's average launch
     # duration is the time of the K back-to-back calls of (1) over K; otherwise
     # the event pairs of (2).
-    single = not plan.generic_launch or plan.streamed_rows == 0
+    single = not plan.generic_launch or (plan.streamed_rows == 0 and plan.floor_slices == 0)
     for name, k in kernels.items():
         k["avg_us"] = ms * 1e3 if single else k["event_pair_avg_us"]
         k["avg_from"] = "back-to-back calls" if single else "event pairs"

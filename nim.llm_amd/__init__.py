@@ -87,6 +87,7 @@ class NlsPlan(ctypes.Structure):
         ("first_unit_bytes", ctypes.c_int64),
         ("k64", ctypes.c_int32),
         ("walk_split", ctypes.c_int32),
+        ("floor_slices", ctypes.c_int32),
     ]
 
 

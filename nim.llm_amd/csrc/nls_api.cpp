@@ -178,6 +178,10 @@ struct nls_sampler {
   uint32_t* p3_rec = nullptr; // [B]
   uint32_t* p3_key = nullptr; // [B]
   int64_t* p3_t = nullptr;    // [B]
+  // floor_kernel's slice records (a batch of full sorts only, no more rows than CUs)
+  uint64_t* floor_part = nullptr;  // [B][S][kFloorKeep]
+  int32_t* floor_n = nullptr;      // [B][S]
+  uint32_t* floor_max = nullptr;   // [B][S]
   int32_t* all_rows = nullptr;       // no streaming rows: 0 .. B-1, then B (the count), then a spare
   // k64_kernel with full-sort rows in the batch: the streamed rows (its
   // grid) and the others (the whole-row kernel's fixed list)
@@ -228,6 +232,9 @@ struct nls_sampler {
     dfree(p3_rec);
     dfree(p3_key);
     dfree(p3_t);
+    dfree(floor_part);
+    dfree(floor_n);
+    dfree(floor_max);
     dfree(all_rows);
     dfree(k64_list);
     dfree(full_list);
@@ -606,6 +613,16 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   // A batch without streaming rows (full sorts only) runs the whole-row
   // kernel alone over a fixed list of every row.
   s->plan.no_stream = !any_fast;
+  // A batch of full sorts only, of no more rows than CUs: each row is split
+  // over slices (floor_kernel), and the whole-row kernel takes the rows that
+  // cannot be finished from the values near their maximum.
+  s->plan.floor_slices = 0;
+  if (s->plan.no_stream && B <= ncu && env_int("NLS_FLOOR", 1)) {
+    bool all_full = true;
+    for (int b = 0; b < B; ++b) all_full &= s->h_rp[b].mode == kModeFull;
+    const int64_t S = (vocab + kFloorSlice - 1) / kFloorSlice;
+    if (all_full && S <= kFloorMaxSlices) s->plan.floor_slices = (int)S;
+  }
   s->plan.gen_blocks = any_full ? std::min(B, 256) : 1;
   s->plan.gen_lds = group_lds_bytes(vocab);
   // ... and then its last workgroup serves that row itself, saving a launch
@@ -674,6 +691,12 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
       s->plan.member_blocks = std::min(B, 2 * ncu);
       s->plan.member_lds = group_patch_lds_bytes(vocab);
     }
+  }
+  if (s->plan.floor_slices > 0) {
+    const size_t parts = (size_t)B * s->plan.floor_slices;
+    if ((rc = dalloc(&s->floor_part, parts * kFloorKeep))) return fail(rc);
+    if ((rc = dalloc(&s->floor_n, parts))) return fail(rc);
+    if ((rc = dalloc(&s->floor_max, parts))) return fail(rc);
   }
   if (s->plan.no_stream) {
     std::vector<int32_t> rows((size_t)B + 2);
@@ -914,7 +937,8 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
     ga.w_next = s->generic_count + 6 + (s->parity ^ 1);
     ga.p3_next = s->generic_count + 8 + (s->parity ^ 1);
   }
-  if (ga.grouped && s->fb_list && !dp.cand_ids && !dp.cand_probs) {
+  // (after floor_kernel the whole-row launch usually finds no row: one launch)
+  if (ga.grouped && s->fb_list && !dp.cand_ids && !dp.cand_probs && s->plan.floor_slices == 0) {
     // the grouped rows in a launch of their own, then the rows it leaves
     // (candidate lists are written by the whole-row sort, so a call asking
     // for them keeps the one launch, where a grouped row is sorted as well)
@@ -959,7 +983,34 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   a.hbits = s->hbits;
   a.row_done = d_done;
   ga.row_done = d_done;
-  if (lp.no_stream) {
+  FloorArgs fa;
+  std::memset(&fa, 0, sizeof fa);
+  if (lp.floor_slices > 0) {
+    // every row through floor_kernel; the whole-row launch takes the rows it lists
+    fa.logits = d_logits;
+    fa.V = s->V;
+    fa.B = s->B;
+    fa.S = lp.floor_slices;
+    fa.rp = s->rp;
+    fa.hist = s->hist;
+    fa.hist_len = s->hist_len;
+    fa.hcap = s->hcap;
+    fa.bias_ids = s->bias_ids;
+    fa.bias_vals = s->bias_vals;
+    fa.bstride = s->bstride;
+    fa.d_u = d_u;
+    fa.rng = s->rng;
+    fa.out = d_out;
+    fa.dbg = dp;
+    fa.row_done = d_done;
+    fa.generic_list = s->generic_list;
+    fa.generic_count = cnt_now;
+    fa.part = s->floor_part;
+    fa.part_n = s->floor_n;
+    fa.part_max = s->floor_max;
+    fa.arrive = s->arrive;
+    a.gen_inline = 0;
+  } else if (lp.no_stream) {
     // every row, a constant count (the spare slot takes the kernel's reset of
     // the next call's counter)
     ga.generic_list = s->all_rows;
@@ -977,7 +1028,7 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
   hipEvent_t e0 = s->prof_start, e1 = s->prof_stop, g0 = s->prof_gstart, g1 = s->prof_gstop;
   s->prof_start = s->prof_stop = s->prof_gstart = s->prof_gstop = nullptr;
-  const hipError_t le = launch_sample(a, ga, lp, s->stream, e0, e1, g0, g1);
+  const hipError_t le = launch_sample(a, ga, fa, lp, s->stream, e0, e1, g0, g1);
   if (le != hipSuccess) {
     // a kernel of this call may have run and left its counters for the next
     s->counters_dirty = true;
@@ -1030,6 +1081,7 @@ int nls_get_plan(const nls_sampler* s, nls_plan* out, int32_t* row_streamed) {
   out->generic_launch = s->gen_inline ? 0 : 1;
   out->k64 = s->plan.k64 ? 1 : 0;
   out->walk_split = s->walk_split ? 1 : 0;
+  out->floor_slices = s->plan.floor_slices;
   // a workgroup requests its first unit (kStreamVec4 float4 per thread)
   // before it reads the row's constants
   out->first_unit_bytes = (s->plan.lds > 0 && !s->plan.no_stream)

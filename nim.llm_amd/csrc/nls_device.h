@@ -294,9 +294,13 @@ __device__ __forceinline__ int chain_lds(const float* x, int cnt, float& acc, St
   return res;
 }
 
+// beyond (a workgroup-shared flag, or null): set when a step ran past the
+// last candidate -- top-p not reached, min-p keeping every candidate, or the
+// draw not ended -- so that a caller holding only the row's leading
+// candidates can tell whether the rest of the row could have mattered.
 template <int NT, bool E_LDS = false, typename VPtr, typename IPtr, typename EPtr>
 __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr e, int ncand, const RowParams& P,
-                                       double u, int* smem) {
+                                       double u, int* smem, int* beyond = nullptr) {
   const float mx = val[0];  // candidates are in non-increasing order
   for (int i = threadIdx.x; i < ncand; i += NT) e[i] = expf_cr(val[i] - mx);
   __syncthreads();
@@ -323,6 +327,7 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
     // the top-p running sum is the same fp32 sequence as the total over its
     // first n terms: when min-p keeps n, the total is the running sum there
     float cum_n = 0.0f;
+    bool past = false;
     if (P.topp_active) {
       // the first i with (double)(e_0 + ... + e_i) >= topP
       float cum = 0.0f, at = 0.0f;
@@ -334,6 +339,7 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
         stop = chain_walk<false, true>(e, ncand, cum, reached, &at);
       if (stop < ncand) n = stop + 1;
       cum_n = stop < ncand ? at : cum;
+      past = stop >= ncand;
     }
     const int n_topp = n;
     if (P.minp_active) {
@@ -348,6 +354,7 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
           break;
         }
       }
+      past |= m == ncand;
       n = m;
     }
     float total = 0.0f;
@@ -365,10 +372,12 @@ __device__ __forceinline__ TailOut softmax_cutoff_draw(VPtr val, IPtr ids, EPtr 
     else
       hit = chain_walk<true, true>(e, n, r, drawn);
     const int pos = hit < n ? hit : n - 1;
+    past |= hit >= n && n == ncand;
     if (lane == 0) {
       s_n = n;
       s_total = total;
       s_pos = pos;
+      if (beyond) *beyond = past ? 1 : 0;
     }
   }
   __syncthreads();

@@ -186,6 +186,48 @@ constexpr int32_t kFbUSaved = 1 << 30;
 // gt_n: the groups hold every candidate of the row.
 constexpr int32_t kGtComplete = 1 << 30;
 
+// floor_kernel: the full-sort rows of a batch of only such rows, each row
+// split over slices of kFloorSlice values, one workgroup each.  A slice keeps
+// its values within kGroupFloor of its maximum (at most kFloorKeep), and the
+// last slice of a row to finish merges them (at most kFloorMerge) and runs the
+// row's tail; any row it cannot finish goes to the whole-row list.
+constexpr int kFloorThreads = 512;
+constexpr int kFloorVec4 = 8;  // float4 per thread: the slice sits in registers
+constexpr int kFloorSlice = kFloorThreads * kFloorVec4 * 4;
+constexpr int kFloorPatchCap = 1024;  // patched ids per slice
+constexpr int kFloorKeep = 2048;
+constexpr int kFloorMerge = 2048;
+constexpr int kFloorMaxSlices = 16;  // V <= 16 * kFloorSlice = 262144
+// dynamic LDS: the slice's tables, then (reused) the merge's records and tail arrays
+constexpr size_t kFloorLds1 = (size_t)kFloorSlice / 32 * 8 + (size_t)kFloorPatchCap * 16 + (size_t)kFloorKeep * 8;
+constexpr size_t kFloorLds2 = (size_t)kFloorMerge * 20;
+constexpr size_t kFloorLds = kFloorLds1 > kFloorLds2 ? kFloorLds1 : kFloorLds2;
+
+struct FloorArgs {
+  const float* logits;
+  int64_t V;
+  int B;
+  int S;  // slices per row
+  const RowParams* rp;
+  const int32_t* hist;
+  const int64_t* hist_len;
+  int hcap;
+  const int32_t* bias_ids;
+  const float* bias_vals;
+  int bstride;  // > 0: row b's bias list at b * bstride, padded with -1
+  const double* d_u;
+  uint64_t* rng;
+  int32_t* out;
+  DebugPtrs dbg;
+  const int32_t* row_done;
+  int32_t* generic_list;  // rows for the whole-row launch after this one
+  int32_t* generic_count;
+  uint64_t* part;      // [B][S][kFloorKeep] (key << 32 | index) of the kept values
+  int32_t* part_n;     // [B][S] kept values, -1: the row goes to the whole-row launch
+  uint32_t* part_max;  // [B][S] the slice maximum's key
+  uint32_t* arrive;    // [B] slices finished (reset by the last)
+};
+
 struct StreamArgs {
   const float* logits;
   int64_t V;
@@ -250,12 +292,13 @@ struct LaunchPlan {
   int gen_blocks;
   size_t gen_lds;  // dynamic LDS bytes of the whole-row kernel (grouped path), 0 = none
   bool no_stream;  // no row is a streaming row: the whole-row kernel alone, over every row
+  int floor_slices;  // > 0: floor_kernel over every row (no streamed rows), then the whole-row launch
   int walk_blocks;  // walk launch: one-wave workgroups (the grouped rows' walks)
   int member_blocks;   // search launch: workgroups (two per CU)
   size_t member_lds;   // and their dynamic LDS (group_patch_lds_bytes)
 };
 
-hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const LaunchPlan& lp,
+hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const FloorArgs& fa, const LaunchPlan& lp,
                          hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, hipEvent_t gev_start,
                          hipEvent_t gev_stop);
 hipError_t launch_accept_host(const int32_t* d_ids, const int32_t* d_cnt, int B, int count,

@@ -572,11 +572,15 @@ static hipError_t launch_stream(const StreamArgs& a, const LaunchPlan& p, hipStr
   return p.vec4 ? launch_stream_variant<256, true>(a, p, s) : launch_stream_variant<256, false>(a, p, s);
 }
 
-hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const LaunchPlan& lp,
+hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const FloorArgs& fa, const LaunchPlan& lp,
                          hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, hipEvent_t gev_start,
                          hipEvent_t gev_stop) {
   hipError_t e;
-  if (!lp.no_stream) {
+  if (lp.floor_slices > 0) {
+    if (ev_start && (e = hipEventRecord(ev_start, s)) != hipSuccess) return e;
+    if ((e = launch_floor(fa, lp, lp.vec4, s)) != hipSuccess) return e;
+    if (ev_stop && (e = hipEventRecord(ev_stop, s)) != hipSuccess) return e;
+  } else if (!lp.no_stream) {
     if (ev_start && (e = hipEventRecord(ev_start, s)) != hipSuccess) return e;
     if ((e = lp.k64 ? launch_k64(sa, lp, s) : launch_stream(sa, lp, s)) != hipSuccess) return e;
     if (ev_stop && (e = hipEventRecord(ev_stop, s)) != hipSuccess) return e;
@@ -630,6 +634,7 @@ size_t max_dynamic_lds() { return 143 * 1024; }  // 160 KB of LDS less the large
 hipError_t set_kernel_attributes() {
   hipError_t e;
   if ((e = set_generic_attributes()) != hipSuccess) return e;
+  if ((e = set_floor_attributes()) != hipSuccess) return e;
   if ((e = set_k64_attributes()) != hipSuccess) return e;
   if ((e = set_stream_attributes<512, true>()) != hipSuccess) return e;
   if ((e = set_stream_attributes<512, false>()) != hipSuccess) return e;

@@ -19,6 +19,9 @@ hipError_t launch_k64(const StreamArgs& a, const LaunchPlan& p, hipStream_t s);
 hipError_t set_k64_attributes();
 
 hipError_t launch_generic(const GenericArgs& ga, const LaunchPlan& lp, hipStream_t s);
+
+hipError_t launch_floor(const FloorArgs& fa, const LaunchPlan& lp, bool vec4, hipStream_t s);
+hipError_t set_floor_attributes();
 hipError_t set_generic_attributes();
 
 }  // namespace nls

@@ -495,6 +495,96 @@ def test_grouped_walk_split_consecutive_calls(pkg, torch, monkeypatch):
     assert np.array_equal(ids, first)
 
 
+def _floor_batch(B, V, rng):
+    """Full-sort rows only: peaked rows (a Zipf head over noise, few values
+    near the maximum), flat rows (every value near it: more than a slice
+    keeps), rows on a 0.25 grid (ties), a NaN row and an all -inf row but one
+    id; top-p, min-p, both or neither; penalties over windows and biases."""
+    x = rng.standard_normal((B, V)).astype(np.float32)
+    plist, hists, biases = [], [], []
+    for b in range(B):
+        kind = b % 8
+        if kind in (0, 1, 2, 3):  # peaked
+            x[b] += (-4.4 * np.log(1 + rng.permutation(V))).astype(np.float32)
+        elif kind == 4:  # ties
+            x[b] = (np.round(x[b] * 8.0) / 4.0).astype(np.float32)
+        elif kind == 5:  # flat
+            x[b] *= np.float32(0.5)
+        d = dict(temperature=float(rng.choice([0.5, 0.7, 1.0, 1.5])), topK=0,
+                 topP=float(rng.choice([1.0, 0.9, 0.5, 0.999])), minP=float(rng.choice([0.0, 0.05, 0.2])),
+                 repeatPenalty=float(rng.choice([1.0, 1.1])), repeatLastN=int(rng.choice([0, 16])),
+                 presencePenalty=float(rng.choice([0.0, -2.0, 0.5])), frequencyPenalty=0.0, seed=5)
+        if b % 16 == 6:
+            d.update(topP=1.0, minP=0.0)  # neither cut: every candidate kept
+        h = [int(i) for i in rng.integers(0, V, 40)] if b % 3 else []
+        top = int(np.argmax(x[b]))
+        if b % 5 == 0:
+            h += [top] * 3  # the maximum penalised
+        bias = {}
+        if b % 4 == 1:
+            bias = {int(rng.integers(0, V)): 6.0, top: -math.inf}
+        plist.append(d)
+        hists.append(h)
+        biases.append(bias)
+    if B > 7:
+        x[7, V // 2] = np.nan
+    if B > 15:
+        x[15, :] = -np.inf
+        x[15, V - 1] = 0.0
+    return x, plist, hists, biases
+
+
+@pytest.mark.parametrize("B,V", [(8, 1000), (33, 16384), (16, 16385), (40, 50001), (64, 128256),
+                                 (24, 151936), (256, 32000)])
+def test_full_sort_rows_split_over_slices(pkg, torch, monkeypatch, B, V):
+    """A batch of full-sort rows only (sampler.nim:96-121), no more rows than
+    CUs: each row split over slices of 16384 values whose workgroups keep the
+    values within the floor of their maximum, the last one merging and running
+    the tail; rows it cannot finish (flat rows, NaN, a chain past the kept
+    values, candidate lists longer than them) go to the whole-row kernel.  Two
+    calls on one sampler (with and without candidate lists) against the
+    oracle, then the same batch with the split switched off (NLS_FLOOR=0)."""
+    rng = np.random.default_rng(B * 7 + V)
+    x, plist, hists, biases = _floor_batch(B, V, rng)
+    params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
+    say(f"[floor_rows] B={B} V={V}")
+    u = rng.random(B)
+    u[: min(3, B)] = [0.0, 1.0 - 2.0 ** -53, 0.5][: min(3, B)]
+    d = torch.from_numpy(x).cuda()
+    du = torch.from_numpy(u).cuda()
+    s = pkg.BatchSampler(params, V)
+    try:
+        plan, _ = s.plan()
+        assert plan.floor_slices == (V + 16383) // 16384, plan.floor_slices
+        for b in range(B):
+            if hists[b]:
+                s.accept(hists[b], row=b)
+        ids, dbg = s.sample(d, du, debug_cap=64)
+        torch.cuda.synchronize()
+        ids = ids.cpu().numpy()
+        dbg = {k: v.cpu().numpy() for k, v in dbg.items()}
+        ok = np.array([not (np.isnan(x[b]).any()) for b in range(B)])
+        compare_rows(x[ok], [p for p, o in zip(plist, ok) if o], [h for h, o in zip(hists, ok) if o],
+                     [c for c, o in zip(biases, ok) if o], u[ok], ids[ok],
+                     {k: v[ok] for k, v in dbg.items()}, f"floor B={B} V={V} lists")
+        ids2 = s.sample(d, du).cpu().numpy()
+        torch.cuda.synchronize()
+        assert np.array_equal(ids2, ids), np.nonzero(ids2 != ids)[0][:10].tolist()
+    finally:
+        s.close()
+    monkeypatch.setenv("NLS_FLOOR", "0")
+    s = pkg.BatchSampler(params, V)
+    try:
+        assert s.plan()[0].floor_slices == 0
+        for b in range(B):
+            if hists[b]:
+                s.accept(hists[b], row=b)
+        ids3 = s.sample(d, du).cpu().numpy()
+    finally:
+        s.close()
+    assert np.array_equal(ids3, ids), np.nonzero(ids3 != ids)[0][:10].tolist()
+
+
 @pytest.mark.parametrize("B", [12, 264])
 def test_greedy_rows_resting_on_patched_ids_or_neg_inf(pkg, torch, B):
     """Greedy rows (sampler.nim:45-49, :77-78) whose argmax rests on -inf or
