@@ -62,6 +62,83 @@ __device__ __forceinline__ uint64_t floor_rec(float v, int idx) {
   return ((uint64_t)f2key(v) << 32) | (uint32_t)~(uint32_t)idx;
 }
 
+// softmax_cutoff_draw (nls_device.h) for at most 64 candidates: one wave
+// holds them, one per lane, and runs each fp32 chain in order with the
+// terms read across lanes -- the same operations in the same sequence (the
+// softmax sum :51-57, top-p :103-108, min-p :110-114, the total :115-116 and
+// the draw :117-120).  Every thread of the workgroup calls it.
+template <int NT>
+__device__ __forceinline__ TailOut small_tail(const float* vals, const int32_t* ids, float* probs, int ncand,
+                                              const RowParams& P, double u, int* beyond) {
+  __shared__ float s_total;
+  __shared__ int s_n, s_pos;
+  if (threadIdx.x < kWave) {
+    const int lane = (int)threadIdx.x;
+    auto at = [](float x, int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i)); };
+    const float mx = vals[0];  // candidates are in non-increasing order
+    float e = lane < ncand ? expf_cr(vals[lane] - mx) : 0.0f;
+    float s = 0.0f;
+    for (int i = 0; i < ncand; ++i) s = s + at(e, i);
+    e = e / s;
+    if (lane < ncand) probs[lane] = e;
+    int n = ncand;
+    float cum_n = 0.0f;
+    bool past = false;
+    if (P.topp_active) {
+      float cum = 0.0f;
+      int stop = ncand;
+      for (int i = 0; i < ncand; ++i) {
+        cum = cum + at(e, i);
+        if ((double)cum >= P.topP) {
+          stop = i;
+          break;
+        }
+      }
+      if (stop < ncand) n = stop + 1;
+      cum_n = cum;
+      past = stop >= ncand;
+    }
+    const int n_topp = n;
+    if (P.minp_active) {
+      const float thr = at(e, 0) * P.minP32;
+      int m = n;
+      const uint64_t fail = __ballot(lane >= 1 && lane < n && !(e >= thr));
+      if (fail) m = __ffsll((unsigned long long)fail) - 1;
+      past |= m == ncand;
+      n = m;
+    }
+    float total = 0.0f;
+    if (P.topp_active && n == n_topp) {
+      total = cum_n;
+    } else {
+      for (int i = 0; i < n; ++i) total = total + at(e, i);
+    }
+    float r = (float)u * total;
+    int hit = n;
+    for (int i = 0; i < n; ++i) {
+      r = r - at(e, i);
+      if (r <= 0.0f) {
+        hit = i;
+        break;
+      }
+    }
+    past |= hit >= n && n == ncand;
+    if (lane == 0) {
+      s_n = n;
+      s_total = total;
+      s_pos = hit < n ? hit : n - 1;
+      *beyond = past ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  TailOut t;
+  t.n = s_n;
+  t.total = s_total;
+  t.id = ids[s_pos];
+  t.nan_cand = 0;  // (rows with a NaN never reach the merge)
+  return t;
+}
+
 }  // namespace
 
 // Two 512-thread workgroups per CU: registers held to 128 (the slice takes 64
@@ -423,7 +500,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2 * NT / kWa
     st[1] = a.rng[2 * row + 1];
     u = nim_rand_unit(st);
   }
-  const TailOut to = softmax_cutoff_draw<NT, true>(vals, ids, ebuf, n, P, u, smem, &s_beyond);
+  const TailOut to = n <= kWave ? small_tail<NT>(vals, ids, ebuf, n, P, u, &s_beyond)
+                                : softmax_cutoff_draw<NT, true>(vals, ids, ebuf, n, P, u, smem, &s_beyond);
   const bool complete = n == V;
   // with neither top-p nor min-p the sort path keeps every candidate (n = V)
   const bool no_cut = !P.topp_active && !P.minp_active;
