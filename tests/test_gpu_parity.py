@@ -1086,6 +1086,59 @@ def test_generate_step_batched_contexts(pkg, torch):
         s.close()
 
 
+def test_generate_step_full_sort_rows_split(pkg, torch):
+    """nls_generate_step over a batch of full-sort rows only (the rows split
+    over slices, sampler.nim:96-121): rows draw from their own RNG streams,
+    which must advance once per step whether the slices finish the row or hand
+    it on (a flat row every step: more values near its maximum than the slices
+    keep); a row drawing an end-of-generation id finishes and samples nothing
+    after; step by step against per-row oracle loops."""
+    rng = np.random.default_rng(505)
+    V, B, steps = 20000, 8, 25
+    eog = [5, 9, V - 2]
+    say(f"[generate_step_split] V={V} B={B} steps={steps}")
+    plist = [dict(temperature=[0.7, 1.0, 0.9, 1.2, 0.6, 1.0, 0.8, 1.1][b], topK=0,
+                  topP=[0.9, 1.0, 0.95, 1.0, 0.8, 1.0, 0.5, 1.0][b], minP=[0.05, 0.0, 0.0, 0.0, 0.1, 0.2, 0.0, 0.0][b],
+                  repeatPenalty=1.2, repeatLastN=[0, 8, 16, 0, 4, 0, 32, 2][b], presencePenalty=0.3,
+                  frequencyPenalty=0.2, seed=[7, 8, 9, 10, 11, 12, 13, 14][b]) for b in range(B)]
+    s = pkg.BatchSampler([to_pkg_params(pkg, p, {}) for p in plist], V)
+    streams = [list(O.uniforms(plist[b]["seed"], steps)) for b in range(B)]
+    used = [0] * B
+    hist = [[] for _ in range(B)]
+    done = [False] * B
+    d_done = torch.zeros(B, dtype=torch.int32, device="cuda")
+    d_eog = torch.tensor(eog, dtype=torch.int32, device="cuda")
+    try:
+        assert s.plan()[0].floor_slices == 2
+        for t in range(steps):
+            x = rng.standard_normal((B, V)).astype(np.float32)
+            for b in range(B):
+                if b == 3:
+                    x[b] *= np.float32(0.2)  # flat: handed on
+                else:
+                    x[b] += (-4.4 * np.log(1 + rng.permutation(V))).astype(np.float32)
+            if t % 6 == 4:
+                x[t % B, eog[t % 3]] = x[t % B].max() + 8.0
+            out = s.generate_step(torch.from_numpy(x).cuda(), d_eog, d_done).cpu().numpy()
+            got_done = d_done.cpu().numpy()
+            for b in range(B):
+                if done[b]:
+                    assert out[b] == -1, (t, b, int(out[b]))
+                    continue
+                u = streams[b][used[b]]
+                used[b] += 1
+                res, _, _, _ = oracle_row(x[b], plist[b], hist[b], {}, u, O.EXPF_CR)
+                assert out[b] == res.id, (t, b, int(out[b]), res.id)
+                if res.id in eog:
+                    done[b] = True
+                else:
+                    hist[b].append(res.id)
+            assert [bool(v) for v in got_done] == done, (t, got_done, done)
+        assert any(done) and not all(done), done
+    finally:
+        s.close()
+
+
 def test_nim_binding_call_sequence(pkg, torch):
     """tests/nim_binding_check.c makes exactly the calls of the Nim binding of the
     sampler (create, set the RNG state from the Nim Rand, replay the
