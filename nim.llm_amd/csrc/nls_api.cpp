@@ -164,7 +164,7 @@ struct nls_sampler {
   uint32_t* arrive = nullptr;
   uint64_t* rng = nullptr;
   int32_t* generic_list = nullptr;
-  int32_t* generic_count = nullptr;  // [10]: handed-on, claim, fallback, walk and search counts (each by call parity)
+  int32_t* generic_count = nullptr;  // [8]: handed-on, claim, fallback and walk counts (each by call parity)
   int32_t* fb_list = nullptr;        // [B] the rows the grouped launch leaves to the whole-row launch
   double* fb_u = nullptr;            // [B] their uniforms, when drawn there
   // the grouped rows' walks in a launch of their own (many full-sort rows per CU)
@@ -174,7 +174,6 @@ struct nls_sampler {
   uint32_t* gt_k = nullptr;   // [B * kGrpHashCap]
   int32_t* gt_n = nullptr;    // [B]
   int32_t* w_list = nullptr;  // [B]
-  int32_t* p3_list = nullptr; // [B]
   uint32_t* p3_rec = nullptr; // [B]
   uint32_t* p3_key = nullptr; // [B]
   int64_t* p3_t = nullptr;    // [B]
@@ -228,7 +227,6 @@ struct nls_sampler {
     dfree(gt_k);
     dfree(gt_n);
     dfree(w_list);
-    dfree(p3_list);
     dfree(p3_rec);
     dfree(p3_key);
     dfree(p3_t);
@@ -666,7 +664,7 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   if ((rc = dalloc(&s->arrive, B))) return fail(rc);
   if ((rc = dalloc(&s->rng, (size_t)2 * B))) return fail(rc);
   if ((rc = dalloc(&s->generic_list, B))) return fail(rc);
-  if ((rc = dalloc(&s->generic_count, 10))) return fail(rc);  // the launches' counters (by call parity)
+  if ((rc = dalloc(&s->generic_count, 8))) return fail(rc);  // the launches' counters (by call parity)
   if (s->plan.gen_lds > 0) {
     if ((rc = dalloc(&s->fb_list, B))) return fail(rc);
     if ((rc = dalloc(&s->fb_u, B))) return fail(rc);
@@ -682,14 +680,12 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
       if ((rc = dalloc(&s->gt_k, cells))) return fail(rc);
       if ((rc = dalloc(&s->gt_n, B))) return fail(rc);
       if ((rc = dalloc(&s->w_list, B))) return fail(rc);
-      if ((rc = dalloc(&s->p3_list, B))) return fail(rc);
       if ((rc = dalloc(&s->p3_rec, B))) return fail(rc);
       if ((rc = dalloc(&s->p3_key, B))) return fail(rc);
       if ((rc = dalloc(&s->p3_t, B))) return fail(rc);
       s->walk_split = true;
-      s->plan.walk_blocks = std::min(B, 8 * ncu);
-      s->plan.member_blocks = std::min(B, 2 * ncu);
-      s->plan.member_lds = group_patch_lds_bytes(vocab);
+      s->plan.walk_blocks = std::min((B + kWalkRows - 1) / kWalkRows, 2 * ncu);  // two workgroups per CU
+      s->plan.walk_lds = walk_member_lds_bytes(vocab);
     }
   }
   if (s->plan.floor_slices > 0) {
@@ -752,7 +748,7 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
     return fail(hip_fail(e, "clear counters"));
   if ((e = hipMemsetAsync(s->done, 0, sizeof(uint32_t), st)) != hipSuccess)
     return fail(hip_fail(e, "clear counters"));
-  if ((e = hipMemsetAsync(s->generic_count, 0, sizeof(int32_t) * 10, st)) != hipSuccess)
+  if ((e = hipMemsetAsync(s->generic_count, 0, sizeof(int32_t) * 8, st)) != hipSuccess)
     return fail(hip_fail(e, "clear counters"));
   if ((e = hipStreamSynchronize(st)) != hipSuccess) return fail(hip_fail(e, "sync"));
   *out = s;
@@ -935,7 +931,6 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   if (s->fb_list) ga.fb_next = s->generic_count + 4 + (s->parity ^ 1);
   if (s->walk_split) {
     ga.w_next = s->generic_count + 6 + (s->parity ^ 1);
-    ga.p3_next = s->generic_count + 8 + (s->parity ^ 1);
   }
   // (after floor_kernel the whole-row launch usually finds no row: one launch)
   if (ga.grouped && s->fb_list && !dp.cand_ids && !dp.cand_probs && s->plan.floor_slices == 0) {
@@ -953,8 +948,6 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
       ga.gt_n = s->gt_n;
       ga.w_list = s->w_list;
       ga.w_count = s->generic_count + 6 + s->parity;
-      ga.p3_list = s->p3_list;
-      ga.p3_count = s->generic_count + 8 + s->parity;
       ga.p3_rec = s->p3_rec;
       ga.p3_key = s->p3_key;
       ga.p3_t = s->p3_t;

@@ -618,7 +618,6 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
 __device__ __forceinline__ void zero_next_counters(const GenericArgs& g) {
   if (g.fb_next) store_agent(g.fb_next, 0);
   if (g.w_next) store_agent(g.w_next, 0);
-  if (g.p3_next) store_agent(g.p3_next, 0);
 }
 
 template <int NT, bool GROUPED = false, bool CLAIM = false, bool ONLY = false>
@@ -3094,109 +3093,124 @@ __device__ __forceinline__ void push_fallback(const GenericArgs& a, int row) {
   a.fb_list[atomicAdd(a.fb_count, 1)] = row | kFbUSaved;
 }
 
-// The walks of the rows the grouped launch stored (a.w_list), one wave per
-// row: the softmax sum, top-p, min-p, total and the draw over the groups
-// (nls_grouped.h), then the drawn group.  A group of one candidate names it;
-// otherwise the row is listed for the search launch.  The groups are read
-// into LDS first (kGrpHashCap exponentials and counts).
-template <int NT>  // one wave: NT = kWave
-__global__ __launch_bounds__(NT) void walk_kernel(const GenericArgs a) {
-  extern __shared__ __align__(16) unsigned char wlds[];
-  float* ge = reinterpret_cast<float*>(wlds);
-  uint32_t* gc = reinterpret_cast<uint32_t*>(ge + kGrpHashCap);
+// The walk over the groups the grouped launch stored for `row`, by one wave:
+// the softmax sum, top-p, min-p, total and the draw over the groups
+// (nls_grouped.h), then the drawn group.  A group of one candidate names the
+// id; a row that cannot be finished goes to the fallback list.  Returns true
+// when the drawn member must be searched for: the group's count record,
+// value key and the member's rank are then in a.p3_*[row].  ge/gc: this
+// wave's LDS for kGrpHashCap exponentials and counts.
+__device__ __forceinline__ bool walk_row(const GenericArgs& a, int row, float* ge, uint32_t* gc) {
   const int lane = lane_id();
-  if (blockIdx.x == 0 && lane == 0) *a.w_next = 0;
-  const int count = *a.w_count;
-  const int V = (int)a.V;
-  for (int li = blockIdx.x; li < count; li += gridDim.x) {
-    const int row = a.w_list[li];
-    NLS_GSTAMP(row, 8);
-    const RowParams P = a.rp[row];
-    const double u = a.fb_u[row];
-    const int gn = a.gt_n[row];
-    const int G = gn & ~kGtComplete;
-    const bool complete = (gn & kGtComplete) != 0;
-    const size_t o = (size_t)row * kGrpHashCap;
-    for (int g = lane; g < G; g += kWave) {
-      ge[g] = a.gt_e[o + g];
-      gc[g] = group_count((uint64_t)a.gt_c[o + g]);
+  // (LDS writes of the wave before its lanes read them: a workgroup-scope
+  // fence waits for them; no barrier, since the other waves do not take part)
+  auto lds_sync = []() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup"); };
+  NLS_GSTAMP(row, 8);
+  const RowParams P = a.rp[row];
+  const double u = a.fb_u[row];
+  const int gn = a.gt_n[row];
+  const int G = gn & ~kGtComplete;
+  const bool complete = (gn & kGtComplete) != 0;
+  const size_t o = (size_t)row * kGrpHashCap;
+  for (int g = lane; g < G; g += kWave) {
+    ge[g] = a.gt_e[o + g];
+    gc[g] = group_count((uint64_t)a.gt_c[o + g]);
+  }
+  lds_sync();
+  float s = 0.0f;
+  if (!group_sum(ge, gc, G, s)) {
+    if (lane == 0) push_fallback(a, row);
+    return false;
+  }
+  NLS_GSTAMP(row, 5);
+  for (int g = lane; g < G; g += kWave) ge[g] = ge[g] / s;  // (:57)
+  lds_sync();
+  const GroupDraw dr = group_cut_draw(ge, gc, G, complete, a.V, P.topp_active != 0, P.topP,
+                                      P.minp_active != 0, P.minP32, u);
+  if (dr.status != kGroupOk) {
+    if (lane == 0) push_fallback(a, row);
+    return false;
+  }
+  // the drawn group: the first g with gc[0] + ... + gc[g] > pos, 64 groups
+  // per step
+  int g = 0;
+  int64_t pos = dr.pos;
+  for (int base = 0; base < G; base += kWave) {
+    const int c = base + lane < G ? (int)gc[base + lane] : 0;
+    const int incl = wave_incl_scan(c);
+    const int tot = __shfl(incl, kWave - 1, kWave);
+    if (pos < (int64_t)tot || base + kWave >= G) {
+      const uint64_t past = __ballot((int64_t)incl > pos);
+      const int hl = past ? __ffsll((unsigned long long)past) - 1 : min(G - base, kWave) - 1;
+      g = base + hl;
+      pos -= (int64_t)(__shfl(incl, hl, kWave) - __shfl(c, hl, kWave));
+      break;
     }
-    __syncthreads();  // (one wave: orders the LDS writes before the reads)
-    float s = 0.0f;
-    if (!group_sum(ge, gc, G, s)) {
-      if (lane == 0) push_fallback(a, row);
-      continue;
-    }
-    NLS_GSTAMP(row, 5);
-    for (int g = lane; g < G; g += kWave) ge[g] = ge[g] / s;  // (:57)
-    __syncthreads();  // (one wave: orders the LDS writes before the reads)
-    const GroupDraw dr = group_cut_draw(ge, gc, G, complete, a.V, P.topp_active != 0, P.topP,
-                                        P.minp_active != 0, P.minP32, u);
-    if (dr.status != kGroupOk) {
-      if (lane == 0) push_fallback(a, row);
-      continue;
-    }
-    // the drawn group: the first g with gc[0] + ... + gc[g] > pos, 64 groups
-    // per step
-    int g = 0;
-    int64_t pos = dr.pos;
-    for (int base = 0; base < G; base += kWave) {
-      const int c = base + lane < G ? (int)gc[base + lane] : 0;
-      const int incl = wave_incl_scan(c);
-      const int tot = __shfl(incl, kWave - 1, kWave);
-      if (pos < (int64_t)tot || base + kWave >= G) {
-        const uint64_t past = __ballot((int64_t)incl > pos);
-        const int hl = past ? __ffsll((unsigned long long)past) - 1 : min(G - base, kWave) - 1;
-        g = base + hl;
-        pos -= (int64_t)(__shfl(incl, hl, kWave) - __shfl(c, hl, kWave));
-        break;
-      }
-      pos -= tot;
-    }
-    NLS_GSTAMP(row, 6);
-    if (lane == 0) {
-      const uint32_t rec = a.gt_c[o + g];
-      if (a.dbg.n) a.dbg.n[row] = (int)dr.n;
-      if (a.dbg.ncand) a.dbg.ncand[row] = V;
-      if (a.dbg.total) a.dbg.total[row] = dr.total;
-      if (a.dbg.path) a.dbg.path[row] = 3;
-      if (rec & kGrpOne) {
-        // a value that occurs once: its member was kept when it was counted
-        a.out[row] = (int32_t)(rec & ~kGrpOne);
-        NLS_GSTAMP(row, 9);
-        NLS_GSTAMP(row, 7);
-      } else {
-        a.p3_rec[row] = rec;
-        a.p3_key[row] = a.gt_k[o + g];
-        a.p3_t[row] = pos;
-        a.p3_list[atomicAdd(a.p3_count, 1)] = row;
-      }
+    pos -= tot;
+  }
+  NLS_GSTAMP(row, 6);
+  const uint32_t rec = a.gt_c[o + g];
+  if (lane == 0) {
+    if (a.dbg.n) a.dbg.n[row] = (int)dr.n;
+    if (a.dbg.ncand) a.dbg.ncand[row] = (int)a.V;
+    if (a.dbg.total) a.dbg.total[row] = dr.total;
+    if (a.dbg.path) a.dbg.path[row] = 3;
+    if (rec & kGrpOne) {
+      // a value that occurs once: its member was kept when it was counted
+      a.out[row] = (int32_t)(rec & ~kGrpOne);
+      NLS_GSTAMP(row, 9);
+      NLS_GSTAMP(row, 7);
+    } else {
+      a.p3_rec[row] = rec;
+      a.p3_key[row] = a.gt_k[o + g];
+      a.p3_t[row] = pos;
     }
   }
+  return (rec & kGrpOne) == 0u;
 }
 
-// The drawn members the walk launch could not name (a.p3_list): the row's
-// patch table again, then the member search (grouped_row's last step).
-// Two workgroups per CU: the launch carries only the patch table's LDS
-// (group_patch_lds_bytes) and the registers are held to 64.
+// The walks and member searches of the rows the grouped launch stored
+// (a.w_list), kWalkRows rows at a time per workgroup: waves 0 .. kWalkRows-1
+// walk one row each (walk_row), then the whole workgroup runs the member
+// search of each row whose drawn value occurs more than once (the row's patch
+// table again, then grouped_row's last step).  Dynamic LDS: the waves' walk
+// tables, later the search's patch table (walk_member_lds_bytes).
 template <int NT>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2 * NT / kWave / 4))) void member_kernel(
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2 * NT / kWave / 4))) void walk_member_kernel(
     const GenericArgs a) {
+  static_assert(NT / kWave >= kWalkRows, "one wave per row");
   __shared__ int smem[NT / kWave + 4];
-  extern __shared__ __align__(16) unsigned char glds[];  // group_lds_bytes(V)
-  if (blockIdx.x == 0 && threadIdx.x == 0) *a.p3_next = 0;
-  const int count = *a.p3_count;
-  for (int li = blockIdx.x; li < count; li += gridDim.x) {
-    const int row = a.p3_list[li];
-    const RowParams P = a.rp[row];
-    const GroupOut r = grouped_row<NT, 3>(a, row, P, 0.0, group_lds(glds, (int)((a.V + 31) >> 5)), smem);
-    if (threadIdx.x == 0) {
-      if (r.ok)
-        a.out[row] = r.id;
-      else
-        push_fallback(a, row);
+  __shared__ int s_row[kWalkRows];
+  extern __shared__ __align__(16) unsigned char glds[];
+  const int wv = threadIdx.x >> 6;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.w_next = 0;
+  const int count = *a.w_count;
+  const int nw = (int)((a.V + 31) >> 5);
+  for (int l0 = blockIdx.x * kWalkRows; l0 < count; l0 += gridDim.x * kWalkRows) {
+    if (wv < kWalkRows) {
+      int need = -1;
+      if (l0 + wv < count) {
+        const int row = a.w_list[l0 + wv];
+        float* ge = reinterpret_cast<float*>(glds) + (size_t)wv * 2 * kGrpHashCap;
+        if (walk_row(a, row, ge, reinterpret_cast<uint32_t*>(ge + kGrpHashCap))) need = row;
+      }
+      if (lane_id() == 0) s_row[wv] = need;
     }
-    __syncthreads();
+    __syncthreads();  // the walks (and their p3_* records) are done
+    for (int j = 0; j < kWalkRows; ++j) {
+      const int row = s_row[j];
+      if (row < 0) continue;  // (uniform)
+      const RowParams P = a.rp[row];
+      const GroupOut r = grouped_row<NT, 3>(a, row, P, 0.0, group_lds(glds, nw), smem);
+      if (threadIdx.x == 0) {
+        if (r.ok)
+          a.out[row] = r.id;
+        else
+          push_fallback(a, row);
+      }
+      __syncthreads();
+    }
+    __syncthreads();  // s_row and the LDS are free for the next rows
   }
 }
 

@@ -20,12 +20,9 @@ hipError_t launch_generic(const GenericArgs& ga, const LaunchPlan& lp, hipStream
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ga.walk_split) {
-      // the stored rows' walks, one wave each; then the member searches
-      const int wgrid = std::max(1, std::min(lp.walk_blocks, 65535));
-      hipLaunchKernelGGL((walk_kernel<kWave>), dim3(wgrid), dim3(kWave), (size_t)kGrpHashCap * 8, s, ga);
-      if ((e = hipGetLastError()) != hipSuccess) return e;
-      hipLaunchKernelGGL((member_kernel<kGenericThreads>), dim3(lp.member_blocks), dim3(kGenericThreads),
-                         lp.member_lds, s, ga);
+      // the stored rows' walks, one wave each, and their member searches
+      hipLaunchKernelGGL((walk_member_kernel<kGenericThreads>), dim3(std::max(1, lp.walk_blocks)),
+                         dim3(kGenericThreads), lp.walk_lds, s, ga);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     GenericArgs fb = ga;
@@ -55,7 +52,7 @@ hipError_t set_generic_attributes() {
                         reinterpret_cast<const void*>(&generic_kernel<kGenericThreads, false>),
                         reinterpret_cast<const void*>(&generic_grouped_kernel<kGenericThreads, true>),
                         reinterpret_cast<const void*>(&generic_grouped_kernel<kGenericThreads, false>),
-                        reinterpret_cast<const void*>(&member_kernel<kGenericThreads>)};
+                        reinterpret_cast<const void*>(&walk_member_kernel<kGenericThreads>)};
   for (const void* f : fns) {
     const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;

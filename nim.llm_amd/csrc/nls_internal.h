@@ -162,10 +162,10 @@ struct GenericArgs {
   int fb_in;
   // The grouped rows' walks in a launch of their own (walk_split = 1): the
   // grouped launch stores each row's groups (gt_*, kGrpHashCap per row) and
-  // lists the row in w_list; the walk launch (one wave per row) lists the
-  // rows whose drawn member must be searched for in p3_list, with the group's
-  // count record and value key and the member's rank; the search launch
-  // finishes them.  Rows that fail any step go to the fallback list.
+  // lists the row in w_list; the walk launch walks them (one wave per row)
+  // and, for a drawn value that occurs more than once, keeps the group's
+  // count record and value key and the member's rank (p3_*) for its member
+  // search.  Rows that fail any step go to the fallback list.
   int walk_split;
   float* gt_e;      // [B][kGrpHashCap] the groups' exponentials
   uint32_t* gt_c;   // [B][kGrpHashCap] their count records (count, or kGrpOne | index)
@@ -174,9 +174,6 @@ struct GenericArgs {
   int32_t* w_list;
   int32_t* w_count;
   int32_t* w_next;
-  int32_t* p3_list;
-  int32_t* p3_count;
-  int32_t* p3_next;
   uint32_t* p3_rec;  // [B] the drawn group's count record
   uint32_t* p3_key;  // [B] its value key
   int64_t* p3_t;     // [B] the drawn member's rank among the group's members
@@ -185,6 +182,15 @@ struct GenericArgs {
 constexpr int32_t kFbUSaved = 1 << 30;
 // gt_n: the groups hold every candidate of the row.
 constexpr int32_t kGtComplete = 1 << 30;
+// walk_member_kernel: rows walked side by side per workgroup, one wave each
+constexpr int kWalkRows = 2;
+// its dynamic LDS: the waves' walk tables (kGrpHashCap exponentials and
+// counts each), later the member search's patch table
+inline size_t walk_member_lds_bytes(int64_t V) {
+  const size_t walk = (size_t)kWalkRows * kGrpHashCap * 8;
+  const size_t search = group_patch_lds_bytes(V);
+  return walk > search ? walk : search;
+}
 
 // floor_kernel: the full-sort rows of a batch of only such rows, each row
 // split over slices of kFloorSlice values, one workgroup each.  A slice keeps
@@ -293,9 +299,8 @@ struct LaunchPlan {
   size_t gen_lds;  // dynamic LDS bytes of the whole-row kernel (grouped path), 0 = none
   bool no_stream;  // no row is a streaming row: the whole-row kernel alone, over every row
   int floor_slices;  // > 0: floor_kernel over every row (no streamed rows), then the whole-row launch
-  int walk_blocks;  // walk launch: one-wave workgroups (the grouped rows' walks)
-  int member_blocks;   // search launch: workgroups (two per CU)
-  size_t member_lds;   // and their dynamic LDS (group_patch_lds_bytes)
+  int walk_blocks;  // walk launch (walk_member_kernel): workgroups, kWalkRows rows each at a time
+  size_t walk_lds;  // and their dynamic LDS (walk_member_lds_bytes)
 };
 
 hipError_t launch_sample(const StreamArgs& sa, const GenericArgs& ga, const FloorArgs& fa, const LaunchPlan& lp,

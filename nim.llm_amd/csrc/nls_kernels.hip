@@ -601,16 +601,16 @@ hipError_t launch_accept_host(const int32_t* d_ids, const int32_t* d_cnt, int B,
 }
 
 // Zeroes a handle's per-call counters: the S > 1 arrival counts, the
-// finished-workgroup count and the ten counters of the whole-row launches.
+// finished-workgroup count and the eight counters of the whole-row launches.
 __global__ void clear_counters_kernel(uint32_t* arrive, int B, uint32_t* done, int32_t* gcount) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < B) arrive[i] = 0u;
   if (i == 0) *done = 0u;
-  if (i < 10) gcount[i] = 0;
+  if (i < 8) gcount[i] = 0;
 }
 
 hipError_t launch_clear_counters(uint32_t* arrive, int B, uint32_t* done, int32_t* gcount, hipStream_t s) {
-  const int n = B > 10 ? B : 10;
+  const int n = B > 8 ? B : 8;
   hipLaunchKernelGGL(clear_counters_kernel, dim3((n + 255) / 256), dim3(256), 0, s, arrive, B, done, gcount);
   return hipGetLastError();
 }
