@@ -149,6 +149,10 @@ struct nls_sampler {
   int S = 1, L = 0, xcd_map = 0;
   int ccap = 0, nwords = 0, pcap = 0, mcap = 0, kcap = 0, offA = 0, pc = 0;
   int parity = 0;  // which generic counter this call uses
+  // the split launches' counters of each parity may hold counts: a call that
+  // splits leaves them in its parity's set, a whole-row launch zeroes the
+  // other parity's, a call served inline by the streaming kernel leaves both
+  bool split_dirty[2] = {false, false};
   // set when a call failed after some of its kernels may have run: the
   // counters it would have handed on are cleared before the next call
   bool counters_dirty = false;
@@ -866,6 +870,7 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
     NLS_HIP(launch_clear_counters(s->arrive, s->B, s->done, s->generic_count, s->stream));
     s->parity = 0;
     s->counters_dirty = false;
+    s->split_dirty[0] = s->split_dirty[1] = false;
   }
   int32_t* cnt_now = s->generic_count + s->parity;
   int32_t* cnt_next = s->generic_count + (s->parity ^ 1);
@@ -913,6 +918,7 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   ga.generic_list = s->generic_list;
   ga.generic_count = cnt_now;
   ga.next_count = cnt_next;
+  ga.list_cap = s->B;
   if (!s->gen_inline && !s->plan.no_stream) {
     // every call of this sampler launches the whole-row kernel, which zeroes
     // the next call's claim counter
@@ -1021,12 +1027,23 @@ int sample_impl(nls_sampler* s, const float* d_logits, const double* d_u, int32_
   lp.vec4 = (s->V % 4 == 0) && ((reinterpret_cast<uintptr_t>(d_logits) & 15) == 0);
   hipEvent_t e0 = s->prof_start, e1 = s->prof_stop, g0 = s->prof_gstart, g1 = s->prof_gstop;
   s->prof_start = s->prof_stop = s->prof_gstart = s->prof_gstop = nullptr;
+  // A call that splits the whole-row launches counts in its parity's split
+  // counters; counts a split call two back left there (the call between was
+  // served inline, so nothing zeroed them) are cleared first.
+  const bool whole_row = !a.gen_inline;
+  const bool splits = whole_row && ga.fb_list != nullptr;
+  if (splits && s->split_dirty[s->parity]) {
+    NLS_HIP(launch_clear_counters(s->arrive, s->B, s->done, s->generic_count, s->stream));
+    s->split_dirty[0] = s->split_dirty[1] = false;
+  }
   const hipError_t le = launch_sample(a, ga, fa, lp, s->stream, e0, e1, g0, g1);
   if (le != hipSuccess) {
     // a kernel of this call may have run and left its counters for the next
     s->counters_dirty = true;
     return hip_fail(le, "launch_sample");
   }
+  if (whole_row) s->split_dirty[s->parity ^ 1] = false;  // zeroed by the whole-row launches
+  if (splits) s->split_dirty[s->parity] = true;
   s->parity ^= 1;
   return NLS_OK;
 }

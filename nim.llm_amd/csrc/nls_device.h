@@ -612,9 +612,10 @@ __device__ __forceinline__ void wave_tail(uint64_t* mem, int k, const RowParams&
   }
 }
 
-// The next call's counters of the whole-row launches (each call's launches
-// count in one parity's set and zero the other's, whichever launches the
-// call makes).
+// The next call's counters of the split whole-row launches, zeroed by every
+// whole-row launch (a call whose rows the streaming kernel's last workgroup
+// serves makes none: the host clears stale counts before a later call that
+// splits).
 __device__ __forceinline__ void zero_next_counters(const GenericArgs& g) {
   if (g.fb_next) store_agent(g.fb_next, 0);
   if (g.w_next) store_agent(g.w_next, 0);
@@ -1957,7 +1958,6 @@ void stream_kernel(const StreamArgs a) {
       if (threadIdx.x == 0) {
         store_agent(a.done, 0u);
         store_agent(a.ga.next_count, 0);
-        zero_next_counters(a.ga);
       }
       uint32_t* dl = reinterpret_cast<uint32_t*>(lds);
       generic_rows<NT>(a.ga, 0, 1, count, shist, dl, dl + 256, smem, &s_u, reinterpret_cast<int*>(dl + 512),
@@ -2838,7 +2838,8 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
             // groups stored: the walk launch takes the row, with its uniform
             if (tid == 0) {
               a.fb_u[row] = *s_u_p;
-              a.w_list[atomicAdd(a.w_count, 1)] = row;
+              const int i = atomicAdd(a.w_count, 1);
+              if (i < a.list_cap) a.w_list[i] = row;  // (a list never holds more than the batch)
             }
             __syncthreads();
             continue;
@@ -2867,7 +2868,7 @@ __device__ __forceinline__ void generic_rows(const GenericArgs& a, int w0, int n
       // goes to the fallback list for the next launch
       if (tid == 0) {
         const int i = atomicAdd(a.fb_count, 1);
-        a.fb_list[i] = row | (u_taken ? kFbUSaved : 0);
+        if (i < a.list_cap) a.fb_list[i] = row | (u_taken ? kFbUSaved : 0);
         if (u_taken) a.fb_u[row] = *s_u_p;
       }
       __syncthreads();
@@ -3056,7 +3057,7 @@ __global__ __launch_bounds__(NT) void generic_kernel(const GenericArgs a) {
     if (a.next_claim) *a.next_claim = 0;
     zero_next_counters(a);
   }
-  const int count = *a.generic_count;
+  const int count = min(*a.generic_count, a.list_cap);  // (a list never holds more than the batch)
   generic_rows<NT, true, CLAIM>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri,
                          glds);
 }
@@ -3081,7 +3082,7 @@ __global__ __launch_bounds__(NT) void generic_grouped_kernel(const GenericArgs a
     if (a.next_claim) *a.next_claim = 0;
     zero_next_counters(a);
   }
-  const int count = *a.generic_count;
+  const int count = min(*a.generic_count, a.list_cap);  // (a list never holds more than the batch)
   generic_rows<NT, true, CLAIM, true>(a, blockIdx.x, gridDim.x, count, wcnt, dbase, drun, smem, &s_u, s_i, s_rv, s_ri,
                          glds);
 }
@@ -3090,7 +3091,8 @@ __global__ __launch_bounds__(NT) void generic_grouped_kernel(const GenericArgs a
 // A row that leaves the grouped path for the whole-row launch, its uniform
 // kept (fb_u holds it).
 __device__ __forceinline__ void push_fallback(const GenericArgs& a, int row) {
-  a.fb_list[atomicAdd(a.fb_count, 1)] = row | kFbUSaved;
+  const int i = atomicAdd(a.fb_count, 1);
+  if (i < a.list_cap) a.fb_list[i] = row | kFbUSaved;
 }
 
 // The walk over the groups the grouped launch stored for `row`, by one wave:
@@ -3184,7 +3186,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2 * NT / kWa
   extern __shared__ __align__(16) unsigned char glds[];
   const int wv = threadIdx.x >> 6;
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.w_next = 0;
-  const int count = *a.w_count;
+  const int count = min(*a.w_count, a.list_cap);
   const int nw = (int)((a.V + 31) >> 5);
   for (int l0 = blockIdx.x * kWalkRows; l0 < count; l0 += gridDim.x * kWalkRows) {
     if (wv < kWalkRows) {

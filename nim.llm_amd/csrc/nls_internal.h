@@ -134,6 +134,11 @@ struct GenericArgs {
   const int32_t* generic_list;
   const int32_t* generic_count;  // this call's counter
   int32_t* next_count;           // the next call's counter, zeroed here
+  // the next call's fallback and walk counts (fb_count, w_count below), which
+  // every call zeroes whichever launches it makes (kept beside next_count: a
+  // kernel that zeroes them reads no further kernel-argument line for them)
+  int32_t* fb_next;
+  int32_t* w_next;
   // the next unclaimed list position (workgroups claim rows one at a time;
   // null: workgroup w takes positions w, w + n, ...) and the next call's
   // claim counter, zeroed here
@@ -157,7 +162,7 @@ struct GenericArgs {
   // as its list of rows.
   int32_t* fb_list;
   int32_t* fb_count;
-  int32_t* fb_next;  // the next call's fallback count, zeroed by the second launch
+  int list_cap;  // the batch: no list holds more rows (a push past it is dropped)
   double* fb_u;
   int fb_in;
   // The grouped rows' walks in a launch of their own (walk_split = 1): the
@@ -173,7 +178,6 @@ struct GenericArgs {
   int32_t* gt_n;    // [B] the groups, | kGtComplete when they hold every candidate
   int32_t* w_list;
   int32_t* w_count;
-  int32_t* w_next;
   uint32_t* p3_rec;  // [B] the drawn group's count record
   uint32_t* p3_key;  // [B] its value key
   int64_t* p3_t;     // [B] the drawn member's rank among the group's members

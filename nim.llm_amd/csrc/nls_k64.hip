@@ -1075,7 +1075,6 @@ __global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(2))) void k
       if (threadIdx.x == 0) {
         store_agent(a.done, 0u);
         store_agent(a.ga.next_count, 0);
-        zero_next_counters(a.ga);
       }
       uint32_t* dl = reinterpret_cast<uint32_t*>(lds);
       generic_rows<kNT>(a.ga, 0, 1, count, whist, dl, dl + 256, smem, &s_u, reinterpret_cast<int*>(dl + 512),

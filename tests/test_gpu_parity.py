@@ -1086,6 +1086,47 @@ def test_generate_step_batched_contexts(pkg, torch):
         s.close()
 
 
+def test_split_calls_around_an_inline_call(pkg, torch):
+    """Top-k rows (sampler.nim:85-121) whose penalty windows overflow the
+    streaming kernel's table: such a call hands every row to the whole-row
+    launches (the first lists the rows it leaves for the second); after
+    clear_history the next call is served by the streaming kernel alone, and
+    after a long window again the call after it splits once more, on the same
+    counter set as the first.  Four calls, each against the oracle."""
+    rng = np.random.default_rng(77)
+    B, V, H, distinct = 12, 50000, 6000, 4500
+    say(f"[split_inline_split] B={B} V={V} H={H}")
+    plist = [dict(temperature=1.0, topK=50, topP=0.95, minP=0.0, repeatPenalty=1.1, repeatLastN=0,
+                  presencePenalty=0.3, frequencyPenalty=0.5, seed=1) for _ in range(B)]
+    params = [to_pkg_params(pkg, p, {}) for p in plist]
+    s = pkg.BatchSampler(params, V)
+
+    def long_hist():
+        h = np.empty((B, H), dtype=np.int64)
+        for b in range(B):
+            ids = rng.choice(V, distinct, replace=False)
+            h[b] = np.concatenate([ids, ids[:H - distinct]])[rng.permutation(H)]
+        return h
+
+    try:
+        for call, hist in enumerate([long_hist(), None, long_hist(), "same"]):
+            if hist is None:
+                s.clear_history()
+                hl = [[] for _ in range(B)]
+            elif isinstance(hist, np.ndarray):
+                s.clear_history()
+                s.accept(hist)
+                hl = [list(r) for r in hist]
+            x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
+            u = rng.random(B)
+            ids = s.sample(torch.from_numpy(x).cuda(), torch.from_numpy(u).cuda()).cpu().numpy()
+            torch.cuda.synchronize()
+            say(f"[split_inline_split] call {call}")
+            compare_rows(x, plist, hl, [{}] * B, u, ids, None, f"call {call}")
+    finally:
+        s.close()
+
+
 def test_generate_step_full_sort_rows_split(pkg, torch):
     """nls_generate_step over a batch of full-sort rows only (the rows split
     over slices, sampler.nim:96-121): rows draw from their own RNG streams,
