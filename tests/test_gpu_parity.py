@@ -535,7 +535,7 @@ def _floor_batch(B, V, rng):
 
 
 @pytest.mark.parametrize("B,V", [(8, 1000), (33, 16384), (16, 16385), (40, 50001), (64, 128256),
-                                 (24, 151936), (256, 32000)])
+                                 (24, 151936), (256, 32000), (256, 151936), (16, 200000)])
 def test_full_sort_rows_split_over_slices(pkg, torch, monkeypatch, B, V):
     """A batch of full-sort rows only (sampler.nim:96-121), no more rows than
     CUs: each row split over slices of 16384 values whose workgroups keep the
@@ -543,7 +543,10 @@ def test_full_sort_rows_split_over_slices(pkg, torch, monkeypatch, B, V):
     the tail; rows it cannot finish (flat rows, NaN, a chain past the kept
     values, candidate lists longer than them) go to the whole-row kernel.  Two
     calls on one sampler (with and without candidate lists) against the
-    oracle, then the same batch with the split switched off (NLS_FLOOR=0)."""
+    oracle, then the same batch with the split switched off (NLS_FLOOR=0).
+    (256 x 151936: 2560 slice workgroups, more than the GPU holds at once;
+    16 x 200000: a vocabulary past the grouped path's tables, so the rows
+    handed on take the whole-row sort.)"""
     rng = np.random.default_rng(B * 7 + V)
     x, plist, hists, biases = _floor_batch(B, V, rng)
     params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
