@@ -259,7 +259,8 @@ typedef struct nls_plan {
   int32_t walk_split;      /* 1: the full-sort rows' walks over their groups run in a launch of their own,
                               one wave per row (more full-sort rows than CUs)    */
   int32_t floor_slices;    /* > 0: every row is a full sort, split over this many workgroups that keep the
-                              values near the row maximum; the second kernel takes the rows they leave */
+                              values near the row maximum (rows x slices <= 2 x CUs); the second kernel
+                              takes the rows they leave */
 } nls_plan;
 /* row_streamed: NULL or host [batch], 1 where the streaming kernel runs the row. */
 int nls_get_plan(const nls_sampler* s, nls_plan* out, int32_t* row_streamed);

@@ -615,15 +615,17 @@ int nls_create(const nls_params* per_row, int32_t batch, int64_t vocab, void* st
   // A batch without streaming rows (full sorts only) runs the whole-row
   // kernel alone over a fixed list of every row.
   s->plan.no_stream = !any_fast;
-  // A batch of full sorts only, of no more rows than CUs: each row is split
-  // over slices (floor_kernel), and the whole-row kernel takes the rows that
-  // cannot be finished from the values near their maximum.
+  // A batch of full sorts only whose row slices all fit the GPU at once (two
+  // workgroups per CU): each row is split over slices (floor_kernel), and the
+  // whole-row kernel takes the rows that cannot be finished from the values
+  // near their maximum.  Past one round of slices the grouped path, one row
+  // per CU, is faster (the slices' serial merge latency repeats each round).
   s->plan.floor_slices = 0;
-  if (s->plan.no_stream && B <= ncu && env_int("NLS_FLOOR", 1)) {
+  if (s->plan.no_stream && env_int("NLS_FLOOR", 1)) {
     bool all_full = true;
     for (int b = 0; b < B; ++b) all_full &= s->h_rp[b].mode == kModeFull;
     const int64_t S = (vocab + kFloorSlice - 1) / kFloorSlice;
-    if (all_full && S <= kFloorMaxSlices) s->plan.floor_slices = (int)S;
+    if (all_full && S <= kFloorMaxSlices && (int64_t)B * S <= 2 * (int64_t)ncu) s->plan.floor_slices = (int)S;
   }
   s->plan.gen_blocks = any_full ? std::min(B, 256) : 1;
   s->plan.gen_lds = group_lds_bytes(vocab);

@@ -535,18 +535,20 @@ def _floor_batch(B, V, rng):
 
 
 @pytest.mark.parametrize("B,V", [(8, 1000), (33, 16384), (16, 16385), (40, 50001), (64, 128256),
-                                 (24, 151936), (256, 32000), (256, 151936), (16, 200000)])
+                                 (24, 151936), (256, 32000), (51, 151936), (16, 200000), (96, 128256)])
 def test_full_sort_rows_split_over_slices(pkg, torch, monkeypatch, B, V):
-    """A batch of full-sort rows only (sampler.nim:96-121), no more rows than
-    CUs: each row split over slices of 16384 values whose workgroups keep the
-    values within the floor of their maximum, the last one merging and running
+    """A batch of full-sort rows only (sampler.nim:96-121) whose slices of
+    16384 values fit the GPU at once (two workgroups per CU): each row split
+    over slices whose workgroups keep the values within the floor of their
+    maximum, the last one merging and running
     the tail; rows it cannot finish (flat rows, NaN, a chain past the kept
     values, candidate lists longer than them) go to the whole-row kernel.  Two
     calls on one sampler (with and without candidate lists) against the
     oracle, then the same batch with the split switched off (NLS_FLOOR=0).
-    (256 x 151936: 2560 slice workgroups, more than the GPU holds at once;
+    (51 x 151936: 510 slice workgroups, about all the GPU holds at once;
     16 x 200000: a vocabulary past the grouped path's tables, so the rows
-    handed on take the whole-row sort.)"""
+    handed on take the whole-row sort; 96 x 128256: too many slices for one
+    round, so the grouped path takes the batch.)"""
     rng = np.random.default_rng(B * 7 + V)
     x, plist, hists, biases = _floor_batch(B, V, rng)
     params = [to_pkg_params(pkg, plist[b], biases[b]) for b in range(B)]
@@ -558,7 +560,9 @@ def test_full_sort_rows_split_over_slices(pkg, torch, monkeypatch, B, V):
     s = pkg.BatchSampler(params, V)
     try:
         plan, _ = s.plan()
-        assert plan.floor_slices == (V + 16383) // 16384, plan.floor_slices
+        S = (V + 16383) // 16384
+        ncu = torch.cuda.get_device_properties(0).multi_processor_count
+        assert plan.floor_slices == (S if B * S <= 2 * ncu else 0), (plan.floor_slices, ncu)
         for b in range(B):
             if hists[b]:
                 s.accept(hists[b], row=b)
